@@ -1,0 +1,554 @@
+// Routed SwiGLU expert FFN over packed Q6_K / Q4_K experts.
+//
+// Replaces expert_parallel / grouped_expert_parallel's per-shard body
+// (kaggle/qwen38_tpu/experts.py:61-131, grouped_experts.py:185-292) on one GPU:
+//
+//   moe_route_kernel     route weights per (token, expert) with duplicate ids
+//                        summed in BF16 (experts.py:66-73), active experts in
+//                        ascending id (:74-76), routes grouped by expert with
+//                        tokens ascending, per-token route lists for the combine.
+//   moe_gate_up_kernel   g = RNE(x Wg^T), u = RNE(x Wu^T), a = RNE(RNE(g*sig(g))*u)
+//                        (experts.py:103-107, math.py:10-20) fused in one pass.
+//   moe_down_kernel      y = RNE(a Wd^T) (experts.py:108).
+//   moe_combine_kernel   out[b] = RNE(sum over experts, ascending id, of
+//                        f32(y) * f32(r)) (experts.py:108-110,129-131), plus the
+//                        optional always-on shared expert RNE(routed + shared).
+//
+// No atomics touch floating-point data, so results are bitwise reproducible.
+#include "moe_common.h"
+#include "q6moe_api.h"
+
+namespace q6moe {
+
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteMaxExperts = 256;
+constexpr int kRouteChunk = 512;  // tokens per bitmap pass
+constexpr int kRouteWords = kRouteChunk / 32;
+
+__global__ void __launch_bounds__(kRouteThreads)
+    moe_route_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B, int K,
+                     int E, int mtile, MoeWs ws) {
+  __shared__ int cnt[kRouteMaxExperts];
+  __shared__ int base[kRouteMaxExperts];
+  __shared__ int run[kRouteMaxExperts];
+  __shared__ uint32_t bits[kRouteMaxExperts][kRouteWords];
+  __shared__ int wpre[kRouteMaxExperts][kRouteWords + 1];
+  const int tid = threadIdx.x;
+  const int n = B * K;
+  for (int e = tid; e < E; e += kRouteThreads) {
+    cnt[e] = 0;
+    run[e] = 0;
+  }
+  __syncthreads();
+  // Pass 1: merged route weight of each first occurrence of an id in a token.
+  for (int i = tid; i < n; i += kRouteThreads) {
+    const int b = i / K, kk = i % K;
+    const int id = ids[i];
+    float r = 0.f;
+    bool first = id >= 0 && id < E;
+    for (int k2 = 0; k2 < kk && first; ++k2) first = ids[b * K + k2] != id;
+    if (first) {
+      float s = 0.f;
+      for (int k2 = kk; k2 < K; ++k2)
+        if (ids[b * K + k2] == id) s += bf16_to_float(wts[b * K + k2]);
+      r = bf16_round(s);
+      if (r != 0.f || r != r) atomicAdd(&cnt[id], 1);
+      else r = 0.f;
+    }
+    ws.ent_r[i] = (r != 0.f || r != r) ? r : 0.f;
+    ws.ent_pos[i] = -1;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int s = 0, a = 0, tl = 0;
+    for (int e = 0; e < E; ++e) {
+      base[e] = s;
+      const int c = cnt[e];
+      if (c > 0) {
+        ws.active[a] = e;
+        ws.act_off[a] = s;
+        ws.tile_off[a] = tl;
+        const int nt = (c + mtile - 1) / mtile;
+        for (int j = 0; j < nt; ++j) ws.tile_slot[tl + j] = a;
+        tl += nt;
+        s += c;
+        ++a;
+      }
+    }
+    ws.act_off[a] = s;
+    ws.tile_off[a] = tl;
+    ws.hdr[0] = a;
+    ws.hdr[1] = s;
+    ws.hdr[2] = tl;
+  }
+  __syncthreads();
+  // Pass 2: positions = expert base + rank of the token among that expert's tokens.
+  for (int c0 = 0; c0 < B; c0 += kRouteChunk) {
+    for (int i = tid; i < E * kRouteWords; i += kRouteThreads) bits[i / kRouteWords][i % kRouteWords] = 0u;
+    __syncthreads();
+    const int lo = c0 * K, hi = min(B, c0 + kRouteChunk) * K;
+    for (int i = lo + tid; i < hi; i += kRouteThreads) {
+      const float r = ws.ent_r[i];
+      if (r != 0.f || r != r) {
+        const int rel = i / K - c0;
+        atomicOr(&bits[ids[i]][rel >> 5], 1u << (rel & 31));
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += kRouteThreads) {
+      int acc = 0;
+      for (int w = 0; w < kRouteWords; ++w) {
+        wpre[e][w] = acc;
+        acc += __popc(bits[e][w]);
+      }
+      wpre[e][kRouteWords] = acc;
+    }
+    __syncthreads();
+    for (int i = lo + tid; i < hi; i += kRouteThreads) {
+      const float r = ws.ent_r[i];
+      if (r != 0.f || r != r) {
+        const int e = ids[i];
+        const int rel = i / K - c0;
+        const int w = rel >> 5, bit = rel & 31;
+        const int pos = base[e] + run[e] + wpre[e][w] + __popc(bits[e][w] & ((1u << bit) - 1u));
+        ws.route_tok[pos] = i / K;
+        ws.route_w[pos] = r;
+        ws.ent_pos[i] = pos;
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += kRouteThreads) run[e] += wpre[e][kRouteWords];
+    __syncthreads();
+  }
+  // Per token: its route positions in ascending expert id. Positions are
+  // expert-major, so sorting them ascending sorts by expert (insertion sort).
+  for (int b = tid; b < B; b += kRouteThreads) {
+    int* tp = ws.tok_pos + (int64_t)b * K;
+    int m = 0;
+    for (int kk = 0; kk < K; ++kk) {
+      const int pos = ws.ent_pos[b * K + kk];
+      if (pos < 0) continue;
+      int j = m++;
+      while (j > 0 && tp[j - 1] > pos) {
+        tp[j] = tp[j - 1];
+        --j;
+      }
+      tp[j] = pos;
+    }
+    for (int j = m; j < K; ++j) tp[j] = -1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode-shaped expert GEMMs: each workgroup owns one (expert slot, block of
+// RPW 16-row groups); its KW waves split the K blocks, each wave decoding its
+// units straight into MFMA operands; partial sums meet in LDS in wave order.
+// Tokens of the expert are processed in chunks of 16*NT (one chunk at decode).
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ u32x4 load_row8(const uint16_t* row, int col, int k) {
+  if (col + 8 <= k) return *reinterpret_cast<const u32x4*>(row + col);
+  u32x4 v = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t e = (col + i < k) ? (uint32_t)row[col + i] : 0u;
+    v[i >> 1] |= e << (16 * (i & 1));
+  }
+  return v;
+}
+
+struct SlotInfo {
+  int64_t expert;
+  int t0, cnt;
+};
+
+__device__ __forceinline__ bool slot_info(const TokenSrc& src, int slot, SlotInfo& si) {
+  if (src.dense) {
+    if (slot != 0) return false;
+    si.expert = 0;
+    si.t0 = 0;
+    si.cnt = src.tokens;
+    return true;
+  }
+  if (slot >= src.hdr[0]) return false;
+  si.expert = src.active[slot];
+  si.t0 = src.act_off[slot];
+  si.cnt = src.act_off[slot + 1] - si.t0;
+  return true;
+}
+
+template <int FMT, int NT, int RPW>
+__global__ void __launch_bounds__(512)
+    moe_gate_up_kernel(Proj gate, Proj up, TokenSrc src, const uint16_t* __restrict__ x, int hidden,
+                       uint16_t* __restrict__ act, int inter, int kw) {
+  __shared__ float red[8][2][RPW][NT][256];
+  SlotInfo si;
+  if (!slot_info(src, blockIdx.x, si)) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int jA = lane >> 4, j = lane & 15;
+  const int rg0 = blockIdx.y * RPW;
+  for (int tc = 0; tc < si.cnt; tc += 16 * NT) {
+    f32x4 ag[RPW][NT], au[RPW][NT];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) ag[r][t] = au[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint16_t* xr[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int q = tc + t * 16 + j;
+      const int tok = q < si.cnt ? (src.dense ? q : src.route_tok[si.t0 + q]) : -1;
+      xr[t] = tok >= 0 ? x + (int64_t)tok * hidden : nullptr;
+    }
+    for (int kb = wave; kb < gate.kb; kb += kw) {
+      u32x4 xf[NT][8];
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int f = 0; f < 8; ++f)
+          xf[t][f] = xr[t] ? load_row8(xr[t], kb * kQK + Unit<FMT>::xoff(f, jA), hidden)
+                           : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const int rg = rg0 + r;
+        if (rg * 16 >= inter) break;
+        Unit<FMT> ug, uu;
+        ug.load(gate, si.expert, rg, kb, lane);
+        uu.load(up, si.expert, rg, kb, lane);
+        u32x4 a[8];
+        ug.decode(a, lane);
+#pragma unroll
+        for (int f = 0; f < 8; ++f)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) ag[r][t] = mfma16(a[f], xf[t][f], ag[r][t]);
+        uu.decode(a, lane);
+#pragma unroll
+        for (int f = 0; f < 8; ++f)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) au[r][t] = mfma16(a[f], xf[t][f], au[r][t]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          red[wave][0][r][t][lane * 4 + i] = ag[r][t][i];
+          red[wave][1][r][t][lane * 4 + i] = au[r][t][i];
+        }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < RPW * NT * 256; idx += blockDim.x) {
+      const int r = idx / (NT * 256), t = (idx / 256) % NT, e = idx & 255;
+      float g = 0.f, u = 0.f;
+      for (int w = 0; w < kw; ++w) {
+        g += red[w][0][r][t][e];
+        u += red[w][1][r][t][e];
+      }
+      const int ln = e >> 2;
+      const int row = (rg0 + r) * 16 + 4 * (ln >> 4) + (e & 3);
+      const int q = tc + t * 16 + (ln & 15);
+      if (row < inter && q < si.cnt) {
+        g = bf16_round(g);
+        u = bf16_round(u);
+        const float sg = bf16_round(g * sigmoid_acc(g));
+        act[(int64_t)(si.t0 + q) * inter + row] = bf16_bits(sg * u);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int FMT, int NT, int RPW>
+__global__ void __launch_bounds__(512)
+    moe_down_kernel(Proj down, TokenSrc src, const uint16_t* __restrict__ act, int inter,
+                    uint16_t* __restrict__ y, int hidden, int kw) {
+  __shared__ float red[8][RPW][NT][256];
+  SlotInfo si;
+  if (!slot_info(src, blockIdx.x, si)) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int jA = lane >> 4, j = lane & 15;
+  const int rg0 = blockIdx.y * RPW;
+  for (int tc = 0; tc < si.cnt; tc += 16 * NT) {
+    f32x4 acc[RPW][NT];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint16_t* ar[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int q = tc + t * 16 + j;
+      ar[t] = q < si.cnt ? act + (int64_t)(si.t0 + q) * inter : nullptr;
+    }
+    for (int kb = wave; kb < down.kb; kb += kw) {
+      u32x4 xf[NT][8];
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int f = 0; f < 8; ++f)
+          xf[t][f] = ar[t] ? load_row8(ar[t], kb * kQK + Unit<FMT>::xoff(f, jA), inter)
+                           : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const int rg = rg0 + r;
+        if (rg * 16 >= hidden) break;
+        Unit<FMT> ud;
+        ud.load(down, si.expert, rg, kb, lane);
+        u32x4 a[8];
+        ud.decode(a, lane);
+#pragma unroll
+        for (int f = 0; f < 8; ++f)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[r][t] = mfma16(a[f], xf[t][f], acc[r][t]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave][r][t][lane * 4 + i] = acc[r][t][i];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < RPW * NT * 256; idx += blockDim.x) {
+      const int r = idx / (NT * 256), t = (idx / 256) % NT, e = idx & 255;
+      float s = 0.f;
+      for (int w = 0; w < kw; ++w) s += red[w][r][t][e];
+      const int ln = e >> 2;
+      const int row = (rg0 + r) * 16 + 4 * (ln >> 4) + (e & 3);
+      const int q = tc + t * 16 + (ln & 15);
+      if (row < hidden && q < si.cnt) y[(int64_t)(si.t0 + q) * hidden + row] = bf16_bits(s);
+    }
+    __syncthreads();
+  }
+}
+
+// out[b, h] = RNE(sum_i f32(y[pos_i, h]) * r_i) over the token's routes in
+// ascending expert id; with a shared expert RNE(f32(routed) + f32(shared)).
+__global__ void __launch_bounds__(256)
+    moe_combine_kernel(const int* __restrict__ tok_pos, const float* __restrict__ route_w,
+                       const uint16_t* __restrict__ y, int K, int hidden,
+                       const uint16_t* __restrict__ sh_y, const uint16_t* __restrict__ sh_scale,
+                       uint16_t* __restrict__ out) {
+  const int b = blockIdx.x;
+  const int h = (blockIdx.y * blockDim.x + threadIdx.x) * 8;
+  if (h >= hidden) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < K; ++i) {
+    const int pos = tok_pos[(int64_t)b * K + i];
+    if (pos < 0) break;
+    const float w = route_w[pos];
+    const u32x4 v = *reinterpret_cast<const u32x4*>(y + (int64_t)pos * hidden + h);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] += bf16_to_float((uint16_t)(v[q >> 1] >> (16 * (q & 1)))) * w;
+  }
+  u32x4 o;
+  if (sh_y) {
+    const u32x4 sv = *reinterpret_cast<const u32x4*>(sh_y + (int64_t)b * hidden + h);
+    const float gs = sh_scale ? bf16_to_float(sh_scale[b]) : 1.f;
+    float v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float sy = bf16_to_float((uint16_t)(sv[q >> 1] >> (16 * (q & 1))));
+      if (sh_scale) sy = bf16_round(sy * gs);
+      v[q] = bf16_round(acc[q]) + sy;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(v[2 * q], v[2 * q + 1]);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(acc[2 * q], acc[2 * q + 1]);
+  }
+  *reinterpret_cast<u32x4*>(out + (int64_t)b * hidden + h) = o;
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+struct WsLayout {
+  size_t hdr, active, act_off, tile_off, tile_slot, ent_r, ent_pos, route_tok, route_w, tok_pos, act,
+      y, sh_act, sh_y, total;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I, int64_t Is,
+                          int64_t mtile) {
+  WsLayout L;
+  const int64_t n = B * K;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align256(o + bytes);
+    return at;
+  };
+  L.hdr = take(64);
+  L.active = take(4 * E);
+  L.act_off = take(4 * (E + 1));
+  L.tile_off = take(4 * (E + 1));
+  L.tile_slot = take(4 * (E + n / mtile + 1));
+  L.ent_r = take(4 * n);
+  L.ent_pos = take(4 * n);
+  L.route_tok = take(4 * n);
+  L.route_w = take(4 * n);
+  L.tok_pos = take(4 * n);
+  L.act = take(2 * n * I);
+  L.y = take(2 * n * H);
+  L.sh_act = take(Is > 0 ? 2 * B * Is : 0);
+  L.sh_y = take(Is > 0 ? 2 * B * H : 0);
+  L.total = o;
+  return L;
+}
+
+constexpr int64_t kPrefillTile = 128;
+
+static Proj make_proj(const q6moe_table& t, int rows, int k) {
+  Proj p;
+  p.data = t.data;
+  p.dstride = t.data_stride;
+  p.scales = t.scales;
+  p.sstride = t.scale_stride;
+  p.rows = rows;
+  p.k = k;
+  p.kb = (int)cdiv(k, kQK);
+  return p;
+}
+
+static int validate_table(const q6moe_table& t, const char* name, int64_t rows, int64_t k, int64_t experts) {
+  std::string n(name);
+  if (!t.data) {
+    set_error(n + ": null data");
+    return Q6MOE_ERR_INVALID;
+  }
+  if (t.qtype == Q6MOE_Q6_K) {
+    const int64_t need = cdiv(rows, 64) * cdiv(k, 256) * kTileBytes;
+    const int64_t sneed = cdiv(rows, 64) * cdiv(k, 256) * 128;
+    if (!t.scales || !aligned(t.data, 16) || !aligned(t.scales, 2) || (experts > 1 && t.data_stride % 16) ||
+        (experts > 1 && t.scale_stride % 2) || (experts > 1 && t.data_stride < need) ||
+        (experts > 1 && t.scale_stride < sneed)) {
+      set_error(n + ": Q6_K tables need 16-byte aligned SoA planes with strides covering one expert");
+      return Q6MOE_ERR_INVALID;
+    }
+  } else if (t.qtype == Q6MOE_Q4_K) {
+    const int64_t need = rows * cdiv(k, 256) * 144;
+    if (!aligned(t.data, 16) || (experts > 1 && (t.data_stride % 16 || t.data_stride < need))) {
+      set_error(n + ": Q4_K tables need 16-byte aligned GGUF rows with strides covering one expert");
+      return Q6MOE_ERR_INVALID;
+    }
+  } else {
+    set_error(n + ": qtype must be Q6_K (SoA) or Q4_K");
+    return Q6MOE_ERR_UNSUPPORTED;
+  }
+  return Q6MOE_OK;
+}
+
+template <int FMT>
+static void launch_phases(const Proj& g, const Proj& u, const Proj& d, const TokenSrc& src, int grid_x,
+                          int max_tokens, const uint16_t* x, int H, int I, uint16_t* act, uint16_t* y,
+                          hipStream_t s) {
+  const int kw1 = g.kb < 8 ? g.kb : 8;
+  const int kw2 = d.kb < 8 ? d.kb : 8;
+  const unsigned rb1 = (unsigned)cdiv(I, 16), rb2 = (unsigned)cdiv(H, 16 * 2);
+  if (max_tokens <= 16) {
+    hipLaunchKernelGGL((moe_gate_up_kernel<FMT, 1, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
+                       H, act, I, kw1);
+    hipLaunchKernelGGL((moe_down_kernel<FMT, 1, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
+                       H, kw2);
+  } else {
+    hipLaunchKernelGGL((moe_gate_up_kernel<FMT, 4, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
+                       H, act, I, kw1);
+    hipLaunchKernelGGL((moe_down_kernel<FMT, 4, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
+                       H, kw2);
+  }
+}
+
+}  // namespace q6moe
+
+using namespace q6moe;
+
+extern "C" size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_t experts, int64_t hidden,
+                                           int64_t intermediate, int64_t shared_intermediate) {
+  if (tokens < 1 || top_k < 1 || experts < 1 || hidden < 1 || intermediate < 1 || shared_intermediate < 0)
+    return 0;
+  return ws_layout(tokens, top_k, experts, hidden, intermediate, shared_intermediate, kPrefillTile).total;
+}
+
+extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
+  Q6MOE_REQUIRE(a, "moe_forward: null args");
+  Q6MOE_REQUIRE(a->x && a->ids && a->weights && a->out && a->workspace, "moe_forward: null pointer");
+  const int64_t B = a->tokens, K = a->top_k, E = a->experts, H = a->hidden, I = a->intermediate;
+  Q6MOE_REQUIRE(B >= 1 && K >= 1 && E >= 1 && H >= 1 && I >= 1, "moe_forward: sizes must be positive");
+  Q6MOE_REQUIRE(E <= kRouteMaxExperts, "moe_forward: at most 256 experts per call");
+  Q6MOE_REQUIRE(B * K <= (1 << 28) && H <= (1 << 24) && I <= (1 << 24), "moe_forward: problem too large");
+  Q6MOE_REQUIRE(H % 8 == 0 && I % 8 == 0, "moe_forward: hidden and intermediate must be multiples of 8");
+  Q6MOE_REQUIRE(aligned(a->x, 16) && aligned(a->out, 16) && aligned(a->workspace, 256),
+                "moe_forward: x/out need 16-byte and workspace 256-byte alignment");
+  Q6MOE_REQUIRE(a->gate.qtype == a->up.qtype && a->up.qtype == a->down.qtype,
+                "moe_forward: gate, up and down must share one qtype");
+  Q6MOE_REQUIRE(a->mode >= 0 && a->mode <= 2, "moe_forward: mode must be 0, 1 or 2");
+  int rc;
+  if ((rc = validate_table(a->gate, "gate", I, H, E)) || (rc = validate_table(a->up, "up", I, H, E)) ||
+      (rc = validate_table(a->down, "down", H, I, E)))
+    return rc;
+  const int64_t Is = a->shared_gate.data ? a->shared_intermediate : 0;
+  if (Is) {
+    Q6MOE_REQUIRE(Is >= 1 && Is % 8 == 0 && Is <= (1 << 24), "moe_forward: shared_intermediate");
+    Q6MOE_REQUIRE(a->shared_gate.qtype == a->gate.qtype && a->shared_up.qtype == a->gate.qtype &&
+                      a->shared_down.qtype == a->gate.qtype,
+                  "moe_forward: the shared expert must use the routed experts' qtype");
+    if ((rc = validate_table(a->shared_gate, "shared_gate", Is, H, 1)) ||
+        (rc = validate_table(a->shared_up, "shared_up", Is, H, 1)) ||
+        (rc = validate_table(a->shared_down, "shared_down", H, Is, 1)))
+      return rc;
+  }
+  const WsLayout L = ws_layout(B, K, E, H, I, Is, kPrefillTile);
+  if (a->workspace_bytes < L.total) {
+    set_error("moe_forward: workspace too small (need " + std::to_string(L.total) + " bytes)");
+    return Q6MOE_ERR_INVALID;
+  }
+  uint8_t* w = reinterpret_cast<uint8_t*>(a->workspace);
+  MoeWs ws;
+  ws.hdr = reinterpret_cast<int*>(w + L.hdr);
+  ws.active = reinterpret_cast<int*>(w + L.active);
+  ws.act_off = reinterpret_cast<int*>(w + L.act_off);
+  ws.tile_off = reinterpret_cast<int*>(w + L.tile_off);
+  ws.tile_slot = reinterpret_cast<int*>(w + L.tile_slot);
+  ws.ent_r = reinterpret_cast<float*>(w + L.ent_r);
+  ws.ent_pos = reinterpret_cast<int*>(w + L.ent_pos);
+  ws.route_tok = reinterpret_cast<int*>(w + L.route_tok);
+  ws.route_w = reinterpret_cast<float*>(w + L.route_w);
+  ws.tok_pos = reinterpret_cast<int*>(w + L.tok_pos);
+  ws.act = reinterpret_cast<uint16_t*>(w + L.act);
+  ws.y = reinterpret_cast<uint16_t*>(w + L.y);
+  ws.sh_act = Is ? reinterpret_cast<uint16_t*>(w + L.sh_act) : nullptr;
+  ws.sh_y = Is ? reinterpret_cast<uint16_t*>(w + L.sh_y) : nullptr;
+
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, s, a->ids, a->weights, (int)B, (int)K,
+                     (int)E, (int)kPrefillTile, ws);
+  if ((rc = check_launch("moe_route_kernel"))) return rc;
+
+  TokenSrc routed{0, (int)B, ws.hdr, ws.active, ws.act_off, ws.route_tok};
+  const int slots = (int)(E < B * K ? E : B * K);
+  const Proj g = make_proj(a->gate, (int)I, (int)H), u = make_proj(a->up, (int)I, (int)H),
+             d = make_proj(a->down, (int)H, (int)I);
+  const int max_tokens = (int)B;  // an expert sees each token at most once
+  if (a->gate.qtype == Q6MOE_Q6_K)
+    launch_phases<FMT_Q6>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s);
+  else
+    launch_phases<FMT_Q4K>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s);
+  if ((rc = check_launch("moe expert kernels"))) return rc;
+  if (Is) {
+    TokenSrc dense{1, (int)B, nullptr, nullptr, nullptr, nullptr};
+    const Proj sg = make_proj(a->shared_gate, (int)Is, (int)H), su = make_proj(a->shared_up, (int)Is, (int)H),
+               sd = make_proj(a->shared_down, (int)H, (int)Is);
+    if (a->gate.qtype == Q6MOE_Q6_K)
+      launch_phases<FMT_Q6>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s);
+    else
+      launch_phases<FMT_Q4K>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s);
+    if ((rc = check_launch("moe shared expert kernels"))) return rc;
+  }
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)B, (unsigned)cdiv(H, 256 * 8)), dim3(256), 0, s,
+                     ws.tok_pos, ws.route_w, ws.y, (int)K, (int)H, ws.sh_y, a->shared_scale, a->out);
+  return check_launch("moe_combine_kernel");
+}

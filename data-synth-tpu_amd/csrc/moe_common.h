@@ -1,0 +1,126 @@
+// Shared definitions of the routed-expert kernels (decode and grouped GEMM).
+#pragma once
+#include "q6moe_device.h"
+
+namespace q6moe {
+
+enum { FMT_Q6 = 0, FMT_Q4K = 1 };
+
+// One projection's expert table: [rows x k] per expert.
+struct Proj {
+  const uint8_t* data;
+  int64_t dstride;
+  const uint8_t* scales;
+  int64_t sstride;
+  int rows, k, kb;
+};
+
+// Workspace views written by the routing kernel and read by the GEMM kernels.
+struct MoeWs {
+  int* hdr;          // [0] active experts, [1] routes, [2] prefill tiles
+  int* active;       // [E] expert id per slot (ascending)
+  int* act_off;      // [E+1] first route position of each slot
+  int* tile_off;     // [E+1] first prefill tile of each slot
+  int* tile_slot;    // [max tiles] slot of each prefill tile
+  float* ent_r;      // [B*k] merged BF16 route weight of an entry (0: no route)
+  int* ent_pos;      // [B*k] route position of an entry (-1: none)
+  int* route_tok;    // [routes] token of each route, grouped by expert, tokens ascending
+  float* route_w;    // [routes] its BF16 weight as FP32
+  int* tok_pos;      // [B*k] per token: route positions in ascending expert id, -1 padded
+  uint16_t* act;     // [B*k, I] BF16 SwiGLU activations
+  uint16_t* y;       // [B*k, H] BF16 expert outputs
+  uint16_t* sh_act;  // [B, Is]
+  uint16_t* sh_y;    // [B, H]
+};
+
+// Where a workgroup's tokens come from: routed slots or the dense shared expert.
+struct TokenSrc {
+  int dense;            // 1: one slot, expert 0, tokens 0..B-1
+  int tokens;           // B
+  const int* hdr;
+  const int* active;
+  const int* act_off;
+  const int* route_tok; // token of route position (phase 1 input rows)
+};
+
+// ---------------------------------------------------------------------------
+// Unit decoders: 16 output rows x one 256-wide K block -> 8 MFMA A operands.
+// ---------------------------------------------------------------------------
+template <int FMT>
+struct Unit;
+
+template <>
+struct Unit<FMT_Q6> {
+  Q6Raw r;
+  __device__ __forceinline__ void load(const Proj& p, int64_t e, int rgroup, int kb, int lane) {
+    const int tile = rgroup >> 2;
+    const int row = (rgroup & 3) * 16 + (lane & 15);
+    const int64_t t = (int64_t)tile * p.kb + kb;
+    q6_load(r, p.data + e * p.dstride + t * kTileBytes, p.scales + e * p.sstride + t * 128, row,
+            lane >> 4);
+  }
+  __device__ __forceinline__ void decode(u32x4 a[8], int lane) const {
+    q6_decode_unit(r, lane >> 4, a);
+  }
+  static __device__ __forceinline__ int xoff(int f, int jA) { return q6_xfrag_offset(f, jA); }
+};
+
+// GGUF Q4_K rows [rows, KB, 144] (16-byte aligned blocks). Lane (row l%16,
+// chunk jA = l/16) decodes qs bytes [32jA, 32jA+32): low nibbles are sub-block
+// 2jA (positions 64jA + l), high nibbles sub-block 2jA+1 (64jA + 32 + l)
+// (kaggle/glm53_offload/gguf_quant.py:115-157). w = fma(q, d*sc, -dmin*m),
+// one rounding of the exact value, then RNE to BF16.
+template <>
+struct Unit<FMT_Q4K> {
+  u32x4 hdr, qa, qb;
+  __device__ __forceinline__ void load(const Proj& p, int64_t e, int rgroup, int kb, int lane) {
+    int row = rgroup * 16 + (lane & 15);
+    row = row < p.rows ? row : p.rows - 1;  // stay in bounds; result row discarded
+    const uint8_t* blk = p.data + e * p.dstride + ((int64_t)row * p.kb + kb) * 144;
+    hdr = ld16_stream(blk);
+    qa = ld16_stream(blk + 16 + 32 * (lane >> 4));
+    qb = ld16_stream(blk + 32 + 32 * (lane >> 4));
+  }
+  __device__ __forceinline__ void decode(u32x4 a[8], int lane) const {
+    const int jA = lane >> 4;
+    const float d = half_bits_to_float(hdr[0] & 0xffff);
+    const float dmin = half_bits_to_float(hdr[0] >> 16);
+    // scale bytes: s = bytes 4..7 (hdr[1]), m = 8..11 (hdr[2]), x = 12..15 (hdr[3])
+    float ds[2], dm[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = 2 * jA + h;
+      int sc, mn;
+      if (j < 4) {
+        sc = (hdr[1] >> (8 * j)) & 63;
+        mn = (hdr[2] >> (8 * j)) & 63;
+      } else {
+        const int jj = j - 4;
+        const uint32_t xb = (hdr[3] >> (8 * jj)) & 0xff;
+        sc = (int)((xb & 15) | (((hdr[1] >> (8 * jj)) >> 2) & 48));
+        mn = (int)((xb >> 4) | (((hdr[2] >> (8 * jj)) >> 2) & 48));
+      }
+      ds[h] = d * (float)sc;
+      dm[h] = -(dmin * (float)mn);
+    }
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      const int hn = f >> 2, bg = f & 3;
+      const u32x4& src = bg < 2 ? qa : qb;
+      uint32_t c0 = src[2 * (bg & 1)], c1 = src[2 * (bg & 1) + 1];
+      if (hn) {
+        c0 = (c0 >> 4) & 0x0f0f0f0fu;
+        c1 = (c1 >> 4) & 0x0f0f0f0fu;
+      } else {
+        c0 &= 0x0f0f0f0fu;
+        c1 &= 0x0f0f0f0fu;
+      }
+      a[f] = q6_frag(c0, c1, ds[hn], dm[hn]);
+    }
+  }
+  static __device__ __forceinline__ int xoff(int f, int jA) {
+    return 64 * jA + 32 * (f >> 2) + 8 * (f & 3);
+  }
+};
+
+}  // namespace q6moe

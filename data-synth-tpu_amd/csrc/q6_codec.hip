@@ -1,0 +1,194 @@
+// Q6_K / Q4_K / Q8_0 decode kernels and the on-device GGUF -> SoA repack.
+//
+//  * q6_soa_decode_kernel  -- whole-matrix decode of the packed SoA planes to
+//    BF16, through the SAME unit decoder the matmul kernels use, so the
+//    bit-exact decode test also pins the operands the MFMA path consumes
+//    (kaggle/packed_q6/kernel.py:44-62).
+//  * gguf_decode_kernel    -- dequantize_rows for raw GGUF rows
+//    (kaggle/glm53_offload/gguf_quant.py:111-173).
+//  * q6_pack_kernel        -- pack_q6's byte permutation
+//    (kaggle/packed_q6/layout.py:71-89).
+#include "q6moe_api.h"
+#include "q6moe_device.h"
+
+namespace q6moe {
+
+// grid (tiles, KB), block 256 = 4 waves = the 4 row groups of a 64-row tile.
+__global__ void __launch_bounds__(256) q6_soa_decode_kernel(const uint8_t* __restrict__ data,
+                                                            const uint8_t* __restrict__ scales,
+                                                            int n, int k, int kb_count,
+                                                            uint16_t* __restrict__ out, int64_t ldo,
+                                                            int vec_ok) {
+  const int tile = blockIdx.x, kb = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)tile * kb_count + kb;
+  const int row = wave * 16 + (lane & 15);
+  const int jA = lane >> 4;
+  Q6Raw raw;
+  q6_load(raw, data + t * kTileBytes, scales + t * 128, row, jA);
+  u32x4 a[8];
+  q6_decode_unit(raw, jA, a);
+  const int gn = tile * kTileRows + row;
+  if (gn >= n) return;
+  uint16_t* orow = out + (int64_t)gn * ldo;
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    const int col = kb * kQK + q6_xfrag_offset(f, jA);
+    if (vec_ok && col + 8 <= k) {
+      *reinterpret_cast<u32x4*>(orow + col) = a[f];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (col + i < k) orow[col + i] = (uint16_t)(a[f][i >> 1] >> (16 * (i & 1)));
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ void store_val(void* out, int64_t idx, float v, int bf16) {
+  if (bf16)
+    reinterpret_cast<uint16_t*>(out)[idx] = bf16_bits(v);
+  else
+    reinterpret_cast<float*>(out)[idx] = v;
+}
+
+__device__ __forceinline__ float rd_half(const uint8_t* p) {
+  return half_bits_to_float((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+}
+
+// One thread per 16 values of a Q6_K/Q4_K block (16 threads per block) or per
+// 32-value Q8_0 block.
+__global__ void gguf_decode_kernel(const uint8_t* __restrict__ raw, int qtype, int64_t rows,
+                                   int width, int blocks, int block_bytes, void* __restrict__ out,
+                                   int bf16) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (qtype == Q6MOE_Q8_0) {
+    if (gid >= rows * blocks) return;
+    const int64_t row = gid / blocks;
+    const int b = (int)(gid % blocks);
+    const uint8_t* blk = raw + gid * block_bytes;
+    const float d = rd_half(blk);
+    for (int i = 0; i < 32; ++i) {
+      const int col = b * 32 + i;
+      if (col < width) store_val(out, row * width + col, d * (float)(int8_t)blk[2 + i], bf16);
+    }
+    return;
+  }
+  if (gid >= rows * blocks * 16) return;
+  const int sub = (int)(gid & 15);
+  const int64_t rb = gid >> 4;
+  const int64_t row = rb / blocks;
+  const int b = (int)(rb % blocks);
+  const uint8_t* blk = raw + rb * block_bytes;
+  if (qtype == Q6MOE_Q6_K) {
+    const float d = rd_half(blk + 208);
+    const float ds = d * (float)(int8_t)blk[192 + sub];
+    for (int i = 0; i < 16; ++i) {
+      const int p = sub * 16 + i;
+      const int h = p >> 7, q = (p & 127) >> 5, l = p & 31;
+      const int lo = (blk[h * 64 + (q & 1) * 32 + l] >> (4 * (q >> 1))) & 15;
+      const int hi = (blk[128 + h * 32 + l] >> (2 * q)) & 3;
+      const int code = (lo | (hi << 4)) - 32;
+      const int col = b * kQK + p;
+      if (col < width) store_val(out, row * width + col, ds * (float)code, bf16);
+    }
+  } else {  // Q4_K: 8 sub-blocks of 32; thread handles half of one
+    const float d = rd_half(blk), dmin = rd_half(blk + 2);
+    const int j = sub >> 1;  // sub-block 0..7
+    int sc, mn;
+    if (j < 4) {
+      sc = blk[4 + j] & 63;
+      mn = blk[8 + j] & 63;
+    } else {
+      sc = (blk[12 + j - 4] & 15) | ((blk[4 + j - 4] >> 2) & 48);
+      mn = (blk[12 + j - 4] >> 4) | ((blk[8 + j - 4] >> 2) & 48);
+    }
+    const float a = d * (float)sc, m = dmin * (float)mn;
+    const uint8_t* qs = blk + 16 + (j >> 1) * 32;
+    for (int i = 0; i < 16; ++i) {
+      const int l = (sub & 1) * 16 + i;
+      const int q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 15);
+      const int col = b * kQK + j * 32 + l;
+      if (col < width) store_val(out, row * width + col, __builtin_fmaf(a, (float)q, -m), bf16);
+    }
+  }
+}
+
+// One thread per (padded row, K block): moves the 208 code/sub-scale bytes into
+// the three regions of its tile and the FP16 d into the scale plane.
+__global__ void q6_pack_kernel(const uint8_t* __restrict__ raw, int n, int kb_count, int tiles,
+                               uint8_t* __restrict__ data, uint8_t* __restrict__ scales,
+                               int64_t scale_bytes) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)tiles * kTileRows * kb_count;
+  if (gid < total) {
+    const int64_t rowg = gid / kb_count;
+    const int kb = (int)(gid % kb_count);
+    const int tile = (int)(rowg / kTileRows), r = (int)(rowg % kTileRows);
+    const int64_t t = (int64_t)tile * kb_count + kb;
+    uint8_t* tb = data + t * kTileBytes;
+    const bool live = rowg < n;
+    const uint8_t* src = raw + (rowg * kb_count + kb) * 210;
+    for (int b = 0; b < 128; ++b) tb[kQlOff + r * 128 + b] = live ? src[b] : 0;
+    for (int b = 0; b < 64; ++b) tb[kQhOff + r * 64 + b] = live ? src[128 + b] : 0;
+    for (int b = 0; b < 16; ++b) tb[kScOff + r * 16 + b] = live ? src[192 + b] : 0;
+    scales[(t * kTileRows + r) * 2] = live ? src[208] : 0;
+    scales[(t * kTileRows + r) * 2 + 1] = live ? src[209] : 0;
+  }
+  // zero the 512-byte padding of the scale plane
+  const int64_t used = total * 2;
+  const int64_t pad = scale_bytes - used;
+  if (gid < pad) scales[used + gid] = 0;
+}
+
+}  // namespace q6moe
+
+using namespace q6moe;
+
+extern "C" int q6moe_q6_decode(const uint8_t* data, const uint8_t* scales, int64_t n, int64_t k,
+                               uint16_t* out, int64_t ldo, void* stream) {
+  Q6MOE_REQUIRE(data && scales && out, "q6_decode: null pointer");
+  Q6MOE_REQUIRE(n >= 1 && k >= 1 && ldo >= k, "q6_decode: need n >= 1, k >= 1, ldo >= k");
+  Q6MOE_REQUIRE(n <= (1 << 30) && k <= (1 << 30), "q6_decode: dimension too large");
+  Q6MOE_REQUIRE(aligned(data, 16) && aligned(scales, 2), "q6_decode: data must be 16-byte aligned");
+  const int kb = (int)cdiv(k, kQK), tiles = (int)cdiv(n, kTileRows);
+  const int vec_ok = (ldo % 8 == 0) && aligned(out, 16);
+  hipLaunchKernelGGL(q6_soa_decode_kernel, dim3(tiles, kb), dim3(256), 0, (hipStream_t)stream, data,
+                     scales, (int)n, (int)k, kb, out, ldo, vec_ok);
+  return check_launch("q6_soa_decode_kernel");
+}
+
+extern "C" int q6moe_q6_pack(const uint8_t* raw, int64_t n, int64_t k, uint8_t* data,
+                             uint8_t* scales, void* stream) {
+  Q6MOE_REQUIRE(raw && data && scales, "q6_pack: null pointer");
+  Q6MOE_REQUIRE(n >= 1 && k >= 1 && n <= (1 << 30) && k <= (1 << 30), "q6_pack: bad shape");
+  const int kb = (int)cdiv(k, kQK), tiles = (int)cdiv(n, kTileRows);
+  const int64_t total = (int64_t)tiles * kTileRows * kb;
+  const int64_t scale_bytes = cdiv(total * 2, 512) * 512;
+  const int64_t threads = total > scale_bytes - total * 2 ? total : scale_bytes - total * 2;
+  hipLaunchKernelGGL(q6_pack_kernel, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0,
+                     (hipStream_t)stream, raw, (int)n, kb, tiles, data, scales, scale_bytes);
+  return check_launch("q6_pack_kernel");
+}
+
+extern "C" int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, int64_t width,
+                                 void* out, int out_dtype, void* stream) {
+  Q6MOE_REQUIRE(raw && out, "gguf_decode: null pointer");
+  Q6MOE_REQUIRE(rows >= 1 && width >= 1 && width <= (1 << 30), "gguf_decode: bad shape");
+  Q6MOE_REQUIRE(out_dtype == Q6MOE_F32 || out_dtype == Q6MOE_BF16, "gguf_decode: out dtype");
+  int vals, bytes;
+  switch (qtype) {
+    case Q6MOE_Q6_K: vals = 256; bytes = 210; break;
+    case Q6MOE_Q4_K: vals = 256; bytes = 144; break;
+    case Q6MOE_Q8_0: vals = 32; bytes = 34; break;
+    default:
+      set_error("gguf_decode: unsupported GGUF quantization type (Q6_K, Q4_K, Q8_0 only)");
+      return Q6MOE_ERR_UNSUPPORTED;
+  }
+  const int blocks = (int)cdiv(width, vals);
+  const int64_t threads = qtype == Q6MOE_Q8_0 ? rows * blocks : rows * blocks * 16;
+  hipLaunchKernelGGL(gguf_decode_kernel, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0,
+                     (hipStream_t)stream, raw, qtype, rows, (int)width, blocks, bytes, out,
+                     out_dtype == Q6MOE_BF16);
+  return check_launch("gguf_decode_kernel");
+}

@@ -1,0 +1,167 @@
+// Device-side helpers shared by the q6moe kernels (gfx950 / CDNA4 only).
+//
+// Number formats follow the reference exactly:
+//  * FP16 block scales widen to FP32 exactly (kaggle/packed_q6/kernel.py:27-41).
+//  * Q6_K values (d * sc) * code are exact in FP32; Q4_K values round once at
+//    the final subtraction (kaggle/glm53_offload/gguf_quant.py:115-173).
+//  * BF16 conversion is round-to-nearest-even (kaggle/qwen38_tpu/precision.py:7-17);
+//    v_cvt_pk_bf16_f32 implements it in one instruction for two values.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q6moe {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kQK = 256;              // values per Q6_K / Q4_K block
+constexpr int kTileRows = 64;         // SoA output tile (layout.py:15)
+constexpr int kTileBytes = 64 * 208;  // 13312 (layout.py:16)
+constexpr int kQlOff = 0;             // 64 rows x 128 B
+constexpr int kQhOff = 8192;          // 64 rows x 64 B
+constexpr int kScOff = 12288;         // 64 rows x 16 B
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits) {
+  // v_cvt_f32_f16 widens every finite FP16 pattern (subnormals, signed zero) exactly.
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 v;
+  v[0] = (__bf16)lo;  // v_cvt_pk_bf16_f32: RNE
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint16_t bf16_bits(float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+
+__device__ __forceinline__ float bf16_round(float x) {
+  return (float)(__bf16)x;
+}
+
+__device__ __forceinline__ float bf16_to_float(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+__device__ __forceinline__ float ubyte_f(uint32_t w, int b) {
+  return (float)((w >> (8 * b)) & 0xffu);  // v_cvt_f32_ubyteN
+}
+
+// Four 6-bit Q6_K codes (as unsigned bytes 0..63, value = byte - 32) from one
+// ql dword and the matching qh dword. ``hs`` is qh already shifted right by
+// 2*q0 so that bits 0-1 of each byte hold the quarter-q0 high bits and bits
+// 4-5 the quarter-(q0+2) high bits (gguf_quant.py:159-167).
+__device__ __forceinline__ uint32_t q6_codes_lo(uint32_t ql, uint32_t hs) {
+  return (ql & 0x0f0f0f0fu) | ((hs << 4) & 0x30303030u);
+}
+__device__ __forceinline__ uint32_t q6_codes_hi(uint32_t ql, uint32_t hs) {
+  return ((ql >> 4) & 0x0f0f0f0fu) | (hs & 0x30303030u);
+}
+
+// Eight weights (two code dwords) -> one MFMA bf16x8 operand (4 dwords),
+// w = RNE_bf16(ds * (c - 32)) computed as fma(c, ds, -32*ds), which is exact
+// because both ds*c and ds*32 are exact in FP32 (F7 of the numerics contract).
+__device__ __forceinline__ u32x4 q6_frag(uint32_t c0, uint32_t c1, float ds, float nds) {
+  u32x4 r;
+  r[0] = pack_bf16x2(__builtin_fmaf(ubyte_f(c0, 0), ds, nds), __builtin_fmaf(ubyte_f(c0, 1), ds, nds));
+  r[1] = pack_bf16x2(__builtin_fmaf(ubyte_f(c0, 2), ds, nds), __builtin_fmaf(ubyte_f(c0, 3), ds, nds));
+  r[2] = pack_bf16x2(__builtin_fmaf(ubyte_f(c1, 0), ds, nds), __builtin_fmaf(ubyte_f(c1, 1), ds, nds));
+  r[3] = pack_bf16x2(__builtin_fmaf(ubyte_f(c1, 2), ds, nds), __builtin_fmaf(ubyte_f(c1, 3), ds, nds));
+  return r;
+}
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Non-temporal 16-byte load for streamed weight bytes that are read once.
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// Accurate FP32 sigmoid: where(x >= 0, 1, e) / (1 + e), e = exp(-|x|)
+// (kaggle/qwen38_tpu/numerics.py:42-45), IEEE division.
+__device__ __forceinline__ float sigmoid_acc(float x) {
+  float e = expf(-fabsf(x));
+  float num = x >= 0.f ? 1.f : e;
+  return num / (1.f + e);
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K SoA "unit": 16 output rows x one 256-wide K block, decoded by one wave
+// straight into eight MFMA A operands.
+//
+// Lane l handles row (l % 16) of the 16-row group and ql chunks jA = l / 16 and
+// jA + 4 (16 bytes each). With q0 = jA >> 1 and e = fragment half, fragment f =
+// 2g + e covers block positions
+//     p = 128*(g >> 1) + 32*(q0 + 2*(g & 1)) + 16*(jA & 1) + 8*e + [0..7]
+// and sub-block jA + 4g. The matching x operand for token j is the 8
+// consecutive BF16 values at that position (see q6_xfrag_offset).
+// ---------------------------------------------------------------------------
+struct Q6Raw {
+  u32x4 qlA, qlB;  // ql chunks jA, jA+4 of the row
+  u32x4 qhA, qhB;  // qh bytes for h = 0, 1 (same l range)
+  u32x4 sc;        // the row's 16 signed sub-scales
+  uint32_t d;      // FP16 bits of the block scale
+};
+
+__device__ __forceinline__ void q6_load(Q6Raw& r, const uint8_t* tile, const uint8_t* dplane,
+                                        int row, int jA) {
+  const uint8_t* ql = tile + kQlOff + row * 128 + 16 * jA;
+  const uint8_t* qh = tile + kQhOff + row * 64 + 16 * (jA & 1);
+  r.qlA = ld16_stream(ql);
+  r.qlB = ld16_stream(ql + 64);
+  r.qhA = ld16_stream(qh);
+  r.qhB = ld16_stream(qh + 32);
+  r.sc = ld16_stream(tile + kScOff + row * 16);
+  r.d = *reinterpret_cast<const uint16_t*>(dplane + row * 2);
+}
+
+// Decode a loaded unit into 8 A fragments.
+__device__ __forceinline__ void q6_decode_unit(const Q6Raw& r, int jA, u32x4 a[8]) {
+  const float d = half_bits_to_float(r.d);
+  const int q0 = jA >> 1;
+  const int sh = 8 * jA;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int scv = (int)(int8_t)((r.sc[g] >> sh) & 0xff);
+    const float ds = d * (float)scv;
+    const float nds = -32.f * ds;
+    const u32x4& ql = (g >> 1) ? r.qlB : r.qlA;
+    const u32x4& qh = (g >> 1) ? r.qhB : r.qhA;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      uint32_t c0, c1;
+      const uint32_t h0 = qh[2 * e] >> (2 * q0), h1 = qh[2 * e + 1] >> (2 * q0);
+      if (g & 1) {
+        c0 = q6_codes_hi(ql[2 * e], h0);
+        c1 = q6_codes_hi(ql[2 * e + 1], h1);
+      } else {
+        c0 = q6_codes_lo(ql[2 * e], h0);
+        c1 = q6_codes_lo(ql[2 * e + 1], h1);
+      }
+      a[2 * g + e] = q6_frag(c0, c1, ds, nds);
+    }
+  }
+}
+
+// Element offset, inside one 256-wide K block, of the 8 x values that pair
+// with fragment f of a lane in k-group jA.
+__device__ __forceinline__ int q6_xfrag_offset(int f, int jA) {
+  const int g = f >> 1, e = f & 1;
+  return 128 * (g >> 1) + 32 * ((jA >> 1) + 2 * (g & 1)) + 16 * (jA & 1) + 8 * e;
+}
+
+}  // namespace q6moe

@@ -1,0 +1,126 @@
+"""INT8 KV cache reads on the GPU: ``read_quantized`` and the paged variant.
+
+Mirrors kaggle/qwen38_tpu/attention_cache.py:46-81:
+
+* dense reference cache: ``cache[name]`` int8 [B, T, KVH*D], ``cache[name +
+  "_scale"]`` BF16 [B*G, T] with G = KVH*D/cache_group; ``indices`` [B, S]
+  follow JAX gather rules (negative adds T, then clamp);
+* result ``compute_cast(f32(code) * f32(scale), dtype)``, i.e. RNE to BF16.
+
+``read_paged`` is the paged generalisation (page tables per sequence, FP32
+per-token-per-head scales). Both run the HIP kernel ``q6moe_kv_read``.
+``quantize`` / ``gather_scale_plane`` keep the reference contract and error
+messages.
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+def _dtype_code(dtype):
+    if dtype == torch.bfloat16:
+        return _lib.BF16
+    if dtype == torch.float32:
+        return _lib.F32
+    raise ValueError("dtype must be torch.bfloat16 or torch.float32")
+
+
+def _run(args, device):
+    lib = _lib.load()
+    with torch.cuda.device(device):
+        rc = lib.q6moe_kv_read(ctypes.byref(args), _lib.stream_handle(device))
+    _lib.check(rc, "kv_read")
+
+
+def read_quantized(cache, name, indices, c, dtype=torch.bfloat16, *, scale_gather=None):
+    """Gather + dequantize cached tokens -> dtype [B, S, kv_heads, head_dim].
+
+    ``c`` needs ``kv_heads``, ``head_dim`` and ``cache_group`` (or ``group``).
+    ``scale_gather`` ("indexed" / "rowwise") is validated; both reference
+    methods give identical values, and the HIP kernel implements that value.
+    """
+    if scale_gather not in (None, "indexed", "rowwise"):
+        raise ValueError("Scale gather method must be indexed or rowwise")
+    codes = cache[name]
+    plane = cache[name + "_scale"]
+    heads, dim = c.kv_heads, c.head_dim
+    group = getattr(c, "cache_group", None) or getattr(c, "group")
+    if codes.dtype != torch.int8 or codes.ndim != 3 or codes.shape[2] != heads * dim:
+        raise ValueError("cache codes must be int8 [batch, time, kv_heads * head_dim]")
+    batch, time, chans = codes.shape
+    groups = chans // group
+    if indices.ndim != 2 or plane.ndim != 2 or plane.shape[0] != indices.shape[0] * groups:
+        raise ValueError("Scale plane must be [batch * groups, time] for [batch, selected] indices")
+    if indices.shape[0] != batch or plane.shape[1] != time:
+        raise ValueError("indices and the scale plane must match the cache's batch and time")
+    if plane.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("scale plane must be BF16 or FP32")
+    idx = indices.to(device=codes.device, dtype=torch.int32).contiguous()
+    out = torch.empty((batch, idx.shape[1], heads, dim), dtype=dtype, device=codes.device)
+    codes, plane = codes.contiguous(), plane.contiguous()
+    a = _lib.KvArgs()
+    a.codes, a.scales = codes.data_ptr(), plane.data_ptr()
+    a.scale_dtype = _dtype_code(plane.dtype)
+    a.scale_layout = 0
+    a.indices = idx.data_ptr()
+    a.batch, a.selected, a.capacity = batch, idx.shape[1], time
+    a.kv_heads, a.head_dim, a.group = heads, dim, group
+    a.out, a.out_dtype = out.data_ptr(), _dtype_code(dtype)
+    _run(a, codes.device)
+    return out
+
+
+def read_paged(pool, scales, page_table, *, page_size, kv_heads, head_dim, group=None, indices=None,
+               dtype=torch.bfloat16, out=None):
+    """Paged cache -> dtype [B, S, kv_heads, head_dim].
+
+    pool int8 [pages, page_size, kv_heads*head_dim]; scales [pages, page_size,
+    kv_heads*head_dim/group] (FP32 or BF16); page_table int32 [B, pages_per_seq];
+    indices int32 [B, S] or None for every token of every page.
+    """
+    group = head_dim if group is None else group
+    if pool.dtype != torch.int8 or pool.ndim < 3 or pool.shape[1] != page_size:
+        raise ValueError("pool must be int8 [pages, page_size, ...]")
+    chans = kv_heads * head_dim
+    if pool[0, 0].numel() != chans:
+        raise ValueError("pool rows must hold kv_heads * head_dim codes")
+    if scales[0, 0].numel() != chans // group:
+        raise ValueError("scales must hold kv_heads * head_dim / group values per token")
+    table = page_table.to(device=pool.device, dtype=torch.int32).contiguous()
+    batch, pps = table.shape
+    cap = pps * page_size
+    idx = None if indices is None else indices.to(device=pool.device, dtype=torch.int32).contiguous()
+    sel = cap if idx is None else idx.shape[1]
+    if out is None:
+        out = torch.empty((batch, sel, kv_heads, head_dim), dtype=dtype, device=pool.device)
+    pool, scales = pool.contiguous(), scales.contiguous()
+    a = _lib.KvArgs()
+    a.codes, a.scales = pool.data_ptr(), scales.data_ptr()
+    a.scale_dtype = _dtype_code(scales.dtype)
+    a.scale_layout = 1
+    a.page_table = table.data_ptr()
+    a.pool_pages, a.pages_per_seq, a.page_size = pool.shape[0], pps, page_size
+    a.indices = None if idx is None else idx.data_ptr()
+    a.batch, a.selected, a.capacity = batch, sel, cap
+    a.kv_heads, a.head_dim, a.group = kv_heads, head_dim, group
+    a.out, a.out_dtype = out.data_ptr(), _dtype_code(out.dtype)
+    _run(a, pool.device)
+    return out
+
+
+def gather_scale_plane(plane, indices, groups, *, method="indexed"):
+    """[B*G, T] scale plane, [B, S] indices -> [B, S, G] (attention_cache.py:46-68)."""
+    if indices.ndim != 2 or plane.ndim != 2 or plane.shape[0] != indices.shape[0] * groups:
+        raise ValueError("Scale plane must be [batch * groups, time] for [batch, selected] indices")
+    if method not in ("indexed", "rowwise"):
+        raise ValueError("Scale gather method must be indexed or rowwise")
+    time = plane.shape[1]
+    t = indices.to(torch.int64)
+    t = torch.where(t < 0, t + time, t).clamp(0, time - 1)
+    batch = indices.shape[0]
+    rows = (torch.arange(batch, device=plane.device)[:, None] * groups
+            + torch.arange(groups, device=plane.device)[None, :])
+    return plane[rows[:, None, :], t[:, :, None].to(plane.device)]

@@ -1,0 +1,160 @@
+/*
+ * q6moe -- C ABI of the MI355X (gfx950) packed-weight expert matmul and the
+ * Q8 KV-cache gather. Plain pointers and sizes only; every device pointer is
+ * HIP device memory and ``stream`` is a hipStream_t (NULL = default stream).
+ *
+ * Conventions
+ *  - Every entry point returns 0 on success or a negative Q6MOE_ERR_* code;
+ *    q6moe_last_error() then holds a message (thread-local).
+ *  - Launches are stream-ordered and asynchronous; nothing synchronises.
+ *  - No entry point allocates device memory: scratch space is the caller's
+ *    ``workspace`` (size from the matching *_workspace_size query).
+ *  - Results are deterministic: no floating-point atomics anywhere.
+ *  - BF16 values are passed as uint16 bit patterns.
+ *
+ * Reference interfaces replaced (paths relative to the reference tree of
+ * AhmadSaeedZaidi/data-synth-tpu):
+ *  - q6moe_q6_matmul      kaggle/packed_q6/kernel.py:98-148  (q6_matmul)
+ *  - q6moe_q6_decode      kaggle/packed_q6/kernel.py:44-62   (decode_tile, whole matrix)
+ *  - q6moe_q6_pack        kaggle/packed_q6/layout.py:49-90   (pack_q6, on device)
+ *  - q6moe_gguf_decode    kaggle/glm53_offload/gguf_quant.py:180-216 (dequantize_rows)
+ *  - q6moe_moe_forward    kaggle/qwen38_tpu/experts.py:17-140 (expert_parallel's fn)
+ *                         kaggle/qwen38_tpu/grouped_experts.py:21-163
+ *  - q6moe_kv_read        kaggle/qwen38_tpu/attention_cache.py:71-81 (read_quantized)
+ *                         kaggle/qwen38_tpu/attention_cache.py:46-68 (gather_scale_plane)
+ */
+#ifndef Q6MOE_H
+#define Q6MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q6MOE_OK 0
+#define Q6MOE_ERR_INVALID (-1)     /* bad argument: shapes, sizes, alignment, dtype */
+#define Q6MOE_ERR_HIP (-2)         /* a HIP runtime call or launch failed */
+#define Q6MOE_ERR_UNSUPPORTED (-3) /* valid request this build does not implement */
+
+/* dtype codes */
+#define Q6MOE_F32 0
+#define Q6MOE_BF16 1
+
+/* GGUF block types (values of GGMLQuantizationType) */
+#define Q6MOE_Q8_0 8
+#define Q6MOE_Q4_K 12
+#define Q6MOE_Q6_K 14
+
+/* Library version (major*10000 + minor*100 + patch). */
+int q6moe_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* q6moe_last_error(void);
+
+/*
+ * y[M, N] = x[M, K] @ decode(W)^T, BF16 operands, FP32 accumulation.
+ * Replaces q6_matmul (kaggle/packed_q6/kernel.py:98-148).
+ *   x       BF16 [M, ldx], row-major, K <= ldx
+ *   data    SoA plane, ceil(N/64)*ceil(K/256)*13312 bytes (layout q6_k_soa_n64_k256_v1)
+ *   scales  FP16 scale plane of the same layout (>= ceil(N/64)*ceil(K/256)*128 bytes)
+ *   y       [M, ldy] of y_dtype (Q6MOE_F32 as the reference returns, or Q6MOE_BF16 = RNE)
+ * Columns of x beyond K are treated as zero (the reference zero-pads x).
+ */
+int q6moe_q6_matmul(const uint16_t* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* data,
+                    const uint8_t* scales, int64_t n, void* y, int y_dtype, int64_t ldy,
+                    void* stream);
+
+/*
+ * Whole-matrix decode of a packed projection to BF16 [N, ldo] (first K columns).
+ * Bit-exact RNE_bf16((d*sc)*code) (kaggle/packed_q6/kernel.py:44-62).
+ */
+int q6moe_q6_decode(const uint8_t* data, const uint8_t* scales, int64_t n, int64_t k,
+                    uint16_t* out, int64_t ldo, void* stream);
+
+/*
+ * GGUF Q6_K rows [N, ceil(K/256), 210] -> SoA planes (kaggle/packed_q6/layout.py:49-90).
+ * data: ceil(N/64)*KB*13312 bytes; scales: the 512-byte-padded plane, fully written
+ * (padding and rows >= N are zero). Does not validate d (the host packer does).
+ */
+int q6moe_q6_pack(const uint8_t* raw, int64_t n, int64_t k, uint8_t* data, uint8_t* scales,
+                  void* stream);
+
+/*
+ * dequantize_rows(raw, qtype, width) for Q6_K, Q4_K and Q8_0 on device
+ * (kaggle/glm53_offload/gguf_quant.py:180-216): raw [rows, ceil(width/vals), bytes]
+ * -> out [rows, width] as FP32 or BF16 (RNE of the FP32 value).
+ */
+int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, int64_t width, void* out,
+                      int out_dtype, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Routed SwiGLU expert FFN (expert_parallel / grouped_expert_parallel).     */
+/* ------------------------------------------------------------------------ */
+
+/* Weight tables of one projection for all experts. */
+typedef struct q6moe_table {
+  int qtype;                /* Q6MOE_Q6_K (SoA planes) or Q6MOE_Q4_K (raw GGUF rows) */
+  const uint8_t* data;      /* expert e starts at data + e * data_stride */
+  int64_t data_stride;      /* bytes between experts */
+  const uint8_t* scales;    /* Q6_K: FP16 scale plane of expert e at scales + e * scale_stride */
+  int64_t scale_stride;     /* Q4_K: unused (NULL / 0) */
+} q6moe_table;
+
+typedef struct q6moe_moe_args {
+  q6moe_table gate, up, down;  /* gate/up: [I rows, H], down: [H rows, I] per expert */
+  int64_t experts;             /* E */
+  int64_t hidden;              /* H */
+  int64_t intermediate;        /* I */
+  const uint16_t* x;           /* BF16 [B, H] */
+  const int32_t* ids;          /* [B, top_k]; ids outside [0, E) are ignored */
+  const uint16_t* weights;     /* BF16 [B, top_k]; zero means no route */
+  int64_t tokens;              /* B */
+  int64_t top_k;               /* k */
+  /* optional always-on shared expert (gate/up [Is, H], down [H, Is]); data == NULL: none */
+  q6moe_table shared_gate, shared_up, shared_down;
+  int64_t shared_intermediate; /* Is */
+  const uint16_t* shared_scale;/* optional BF16 [B] per-token gate of the shared output; NULL = 1 */
+  uint16_t* out;               /* BF16 [B, H] */
+  void* workspace;             /* >= q6moe_moe_workspace_size(...) bytes, 256-byte aligned */
+  size_t workspace_bytes;
+  int mode;                    /* 0 auto, 1 decode kernels, 2 grouped-GEMM (prefill) kernels */
+} q6moe_moe_args;
+
+size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_t experts, int64_t hidden,
+                                int64_t intermediate, int64_t shared_intermediate);
+
+int q6moe_moe_forward(const q6moe_moe_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* INT8 KV cache gather + dequant (read_quantized).                         */
+/* ------------------------------------------------------------------------ */
+
+typedef struct q6moe_kv_args {
+  const int8_t* codes;      /* dense: [B, T, KVH*D]; paged: [pages, page_size, KVH*D] */
+  const void* scales;       /* see scale_layout */
+  int scale_dtype;          /* Q6MOE_BF16 (reference) or Q6MOE_F32 */
+  int scale_layout;         /* 0: plane [B*G, T] (reference); 1: token-major [rows, G] */
+  const int32_t* page_table;/* NULL: dense cache; else [B, pages_per_seq] */
+  int64_t pool_pages;       /* pages in the pool; table entries outside [0, pool_pages) read as 0 */
+  int64_t pages_per_seq;
+  int64_t page_size;
+  const int32_t* indices;   /* NULL: tokens 0..S-1; else [B, S] (negative adds T, then clamp) */
+  int64_t batch;            /* B */
+  int64_t selected;         /* S */
+  int64_t capacity;         /* T (dense) -- paged: pages_per_seq * page_size */
+  int64_t kv_heads;
+  int64_t head_dim;
+  int64_t group;            /* channels per scale; divides KVH*D */
+  void* out;                /* [B, S, KVH*D] */
+  int out_dtype;            /* Q6MOE_BF16 or Q6MOE_F32 (compute_cast target) */
+} q6moe_kv_args;
+
+int q6moe_kv_read(const q6moe_kv_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* Q6MOE_H */

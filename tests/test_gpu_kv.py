@@ -1,0 +1,96 @@
+"""GPU parity of the INT8 KV gather + dequant (bit-exact against the oracle)."""
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv as oracle_kv
+from oracle.packed_q6 import bf16_bits, bf16_round
+from q6moe.attention_cache import gather_scale_plane, read_paged, read_quantized
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def test_dense_reference_cache_read_bit_exact(device):
+    rng = np.random.default_rng(413)
+    B, T, H, D, group = 3, 64, 2, 256, 32
+    G = H * D // group
+    codes = rng.integers(-127, 128, (B, T, H * D), dtype=np.int8)
+    plane = bf16_round(rng.uniform(0, 0.03, (B * G, T)).astype(np.float32))
+    plane[:, 0] = 0
+    idx = np.tile(np.array([0, 0, 1, T // 8, T - 1, -1, -T - 2, T + 3, 17]), (B, 1)).astype(np.int32)
+    c = SimpleNamespace(kv_heads=H, head_dim=D, cache_group=group)
+    cache = {"k": torch.from_numpy(codes).to(device),
+             "k_scale": torch.from_numpy(plane).to(device).to(torch.bfloat16)}
+    got = read_quantized(cache, "k", torch.from_numpy(idx).to(device), c)
+    want = oracle_kv.read_dense(codes, plane, idx, H, D, group)
+    np.testing.assert_array_equal(_bits(got), bf16_bits(want))
+    got32 = read_quantized(cache, "k", torch.from_numpy(idx).to(device), c, torch.float32).cpu().numpy()
+    t = oracle_kv.normalize_index(idx, T)
+    sc = oracle_kv.gather_scale_plane(plane, idx, G)
+    for b in range(B):
+        want32 = codes[b, t[b]].astype(np.float32).reshape(len(idx[b]), G, group) * sc[b][..., None]
+        np.testing.assert_array_equal(got32[b].reshape(len(idx[b]), -1), want32.reshape(len(idx[b]), -1))
+
+
+@pytest.mark.parametrize("method", ["indexed", "rowwise"])
+def test_scale_plane_gather_matches_oracle(device, method):
+    rng = np.random.default_rng(629)
+    plane = bf16_round(rng.normal(size=(2 * 16, 32)).astype(np.float32))
+    idx = np.tile(np.array([0, 0, 1, 4, 31, -1, -34, 35]), (2, 1))
+    got = gather_scale_plane(torch.from_numpy(plane).to(device), torch.from_numpy(idx).to(device), 16,
+                             method=method).cpu().numpy()
+    np.testing.assert_array_equal(got, oracle_kv.gather_scale_plane(plane, idx, 16))
+
+
+def test_paged_read_bit_exact_and_unmapped_pages_read_zero(device):
+    rng = np.random.default_rng(4)
+    B, P, pps, H, D = 2, 16, 5, 4, 128
+    pages = B * pps + 1
+    pool = rng.integers(-127, 128, (pages, P, H, D), dtype=np.int8)
+    scales = rng.uniform(0, 0.05, (pages, P, H)).astype(np.float32)
+    table = rng.permutation(pages)[: B * pps].astype(np.int32).reshape(B, pps)
+    got = read_paged(torch.from_numpy(pool).to(device), torch.from_numpy(scales).to(device),
+                     torch.from_numpy(table).to(device), page_size=P, kv_heads=H, head_dim=D)
+    want = oracle_kv.read_paged(pool, scales, table, P, H, D, D)
+    np.testing.assert_array_equal(_bits(got), bf16_bits(want))
+    idx = rng.integers(-pps * P - 3, pps * P + 3, (B, 37)).astype(np.int32)
+    got = read_paged(torch.from_numpy(pool).to(device), torch.from_numpy(scales).to(device),
+                     torch.from_numpy(table).to(device), page_size=P, kv_heads=H, head_dim=D,
+                     indices=torch.from_numpy(idx).to(device))
+    np.testing.assert_array_equal(_bits(got), bf16_bits(oracle_kv.read_paged(pool, scales, table, P, H, D, D, idx)))
+    bad = table.copy()
+    bad[1, 2] = pages + 7
+    got = read_paged(torch.from_numpy(pool).to(device), torch.from_numpy(scales).to(device),
+                     torch.from_numpy(bad).to(device), page_size=P, kv_heads=H, head_dim=D).float().cpu().numpy()
+    assert np.all(got[1, 2 * P : 3 * P] == 0)
+
+
+def test_odd_shapes_take_the_scalar_path(device):
+    rng = np.random.default_rng(7)
+    B, P, pps, H, D, group = 2, 3, 2, 3, 10, 5
+    pool = rng.integers(-127, 128, (B * pps, P, H, D), dtype=np.int8)
+    scales = rng.uniform(0, 0.05, (B * pps, P, H * D // group)).astype(np.float32)
+    table = np.arange(B * pps, dtype=np.int32).reshape(B, pps)
+    got = read_paged(torch.from_numpy(pool).to(device), torch.from_numpy(scales).to(device),
+                     torch.from_numpy(table).to(device), page_size=P, kv_heads=H, head_dim=D, group=group)
+    np.testing.assert_array_equal(_bits(got), bf16_bits(oracle_kv.read_paged(pool, scales, table, P, H, D, group)))
+
+
+def test_kv_pages_workload_reduced_shape(device):
+    # Same generator as the bench workload (paged int8 K/V, FP32 per-token-per-head
+    # scales, random page permutation), at 2 sequences x 4096 tokens.
+    from q6moe.synth import kv_pages
+
+    W = kv_pages(seed=4, batch=2, context=4096)
+    for name in ("k", "v"):
+        got = read_paged(torch.from_numpy(W[name]).to(device), torch.from_numpy(W[name + "_scale"]).to(device),
+                         torch.from_numpy(W["page_table"]).to(device), page_size=256, kv_heads=4, head_dim=128)
+        want = oracle_kv.read_paged(W[name], W[name + "_scale"], W["page_table"], 256, 4, 128, 128)
+        np.testing.assert_array_equal(_bits(got), bf16_bits(want))

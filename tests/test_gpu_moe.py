@@ -1,0 +1,157 @@
+"""GPU parity of the routed SwiGLU expert FFN against the NumPy oracle.
+
+Tolerance (BF16 output, FP32 accumulation vs. the oracle's FP64 sums):
+  * max relative error max|got - want| / max|want| <= 1e-2;
+  * elementwise |got - want| <= 1e-2 * |want| + 1e-2 * max|want|;
+  * at least 90 % of outputs bit-identical to the oracle (a differing FP32
+    summation order only flips an intermediate BF16 rounding now and then,
+    moving a few outputs by one BF16 ulp; a wrong index or term would not).
+Structural invariants are exact: zero routes give exact zeros, poisoned
+unrouted experts never leak, repeat runs are bitwise identical."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as oracle_moe
+from oracle import routing as oracle_routing
+from q6moe.experts import expert_parallel, pack_experts
+from q6moe.synth import moe_layer
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-2
+
+
+def _max_rel(got, want):
+    return float(np.max(np.abs(got - want)) / max(np.abs(want).max(), 1e-30))
+
+
+def assert_moe_close(got, want, exact_frac=0.9):
+    assert np.isfinite(got).all()
+    assert _max_rel(got, want) <= REL
+    np.testing.assert_allclose(got, want, rtol=REL, atol=REL * np.abs(want).max())
+    assert np.mean(got == want) >= exact_frac
+
+
+def _run(L, device, mode=0, shared=None, weights=None, ids=None):
+    q, H, I = L["qtype"], L["hidden"], L["intermediate"]
+    fn = expert_parallel(None, gate_type=q, up_type=q, down_type=q, hidden=H, intermediate=I)
+    tabs = [pack_experts(L[n], q, I if n != "down" else H, H if n != "down" else I, device)
+            for n in ("gate", "up", "down")]
+    x = torch.from_numpy(L["x"]).to(device).to(torch.bfloat16)
+    ids = torch.from_numpy(L["ids"] if ids is None else ids).to(device)
+    w = torch.from_numpy(L["weights"] if weights is None else weights).to(device).to(torch.bfloat16)
+    sh = None
+    if shared is not None:
+        Is = shared["intermediate"]
+        sh = dict(gate=pack_experts(shared["gate"][None], q, Is, H, device),
+                  up=pack_experts(shared["up"][None], q, Is, H, device),
+                  down=pack_experts(shared["down"][None], q, H, Is, device))
+    fn.mode = mode
+    try:
+        out = fn(*tabs, x, ids, w, shared=sh)
+    finally:
+        fn.mode = 0
+    return out.float().cpu().numpy(), (fn, tabs, x, ids, w, sh)
+
+
+def _oracle(L, shared=None, weights=None, ids=None):
+    q = L["qtype"]
+    sh = None
+    if shared is not None:
+        from oracle.gguf import dequantize_rows
+        from oracle.packed_q6 import bf16_round
+
+        H, Is = L["hidden"], shared["intermediate"]
+        sh = dict(gate=bf16_round(dequantize_rows(shared["gate"], q, H)),
+                  up=bf16_round(dequantize_rows(shared["up"], q, H)),
+                  down=bf16_round(dequantize_rows(shared["down"], q, Is)))
+    return oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"],
+                                 L["ids"] if ids is None else ids,
+                                 L["weights"] if weights is None else weights,
+                                 types=(q, q, q), hidden=L["hidden"], intermediate=L["intermediate"],
+                                 shared=sh)
+
+
+@pytest.mark.parametrize("qtype", ["Q6_K", "Q4_K"])
+@pytest.mark.parametrize("tokens,experts,top_k", [(1, 8, 2), (8, 16, 4), (20, 12, 3), (70, 6, 2)])
+def test_small_layers_match_oracle(device, qtype, tokens, experts, top_k):
+    L = moe_layer(seed=tokens + experts, experts=experts, top_k=top_k, hidden=512, intermediate=256,
+                  tokens=tokens, qtype=qtype, pack=False)
+    got, _ = _run(L, device)
+    assert_moe_close(got, _oracle(L))
+
+
+def test_decode_workload_full_size(device):
+    # 128 experts, top-8, hidden 2048, intermediate 768, Q6_K, 8 tokens, seed 1.
+    L = moe_layer(seed=1, pack=False)
+    got, ctx = _run(L, device)
+    want = _oracle(L)
+    assert_moe_close(got, want)
+    # repeat run is bitwise identical (no atomics on values)
+    fn, tabs, x, ids, w, _ = ctx
+    again = fn(*tabs, x, ids, w).float().cpu().numpy()
+    np.testing.assert_array_equal(got, again)
+
+
+def test_duplicate_routes_sum_and_zero_rows_are_exact_zero(device):
+    L = moe_layer(seed=9, experts=6, top_k=3, hidden=256, intermediate=256, tokens=9, pack=False)
+    ids = L["ids"].copy()
+    w = L["weights"].copy()
+    ids[:3, 1] = ids[:3, 0]  # duplicate expert in one token: weights add
+    w[4] = 0  # finished request
+    got, _ = _run(L, device, ids=ids, weights=w)
+    want = _oracle(L, ids=ids, weights=w)
+    assert np.all(got[4] == 0)
+    assert_moe_close(got, want)
+    zero, _ = _run(L, device, ids=ids, weights=np.zeros_like(w))
+    assert np.all(zero == 0)
+
+
+def test_poisoned_unrouted_experts_do_not_leak(device):
+    L = moe_layer(seed=10, experts=8, top_k=2, hidden=256, intermediate=256, tokens=4, pack=False)
+    used = set(L["ids"].ravel().tolist())
+    for e in set(range(8)) - used:
+        for n in ("gate", "up", "down"):
+            L[n][e, ..., 208:210] = np.array([np.nan], "<f2").view(np.uint8)
+    got, _ = _run(L, device)
+    assert_moe_close(got, _oracle(L))
+
+
+def test_out_of_range_ids_are_ignored(device):
+    L = moe_layer(seed=12, experts=6, top_k=2, hidden=256, intermediate=256, tokens=3, pack=False)
+    ids = L["ids"].copy()
+    ids[0, 1] = 99
+    ids[1, 0] = -1
+    got, _ = _run(L, device, ids=ids)
+    assert_moe_close(got, _oracle(L, ids=ids))
+
+
+@pytest.mark.parametrize("tokens", [1, 8])
+def test_q4_with_shared_expert(device, tokens):
+    L = moe_layer(seed=3, experts=8, top_k=3, hidden=512, intermediate=256, tokens=tokens, qtype="Q4_K",
+                  sigma=0.015, shared_intermediate=512, pack=False)
+    got, _ = _run(L, device, shared=L["shared"])
+    assert_moe_close(got, _oracle(L, shared=L["shared"]))
+
+
+def test_raw_gguf_tables_match_packed_tables(device):
+    L = moe_layer(seed=13, experts=4, top_k=2, hidden=512, intermediate=256, tokens=5, pack=False)
+    got, ctx = _run(L, device)
+    fn, tabs, x, ids, w, _ = ctx
+    raw = [torch.from_numpy(L[n].reshape(4, -1)).to(device) for n in ("gate", "up", "down")]
+    out = fn(*raw, x, ids, w).float().cpu().numpy()
+    np.testing.assert_array_equal(got, out)
+
+
+def test_route_weights_match_oracle_merging(device):
+    # The combine uses the oracle's merged BF16 route weights; check them
+    # indirectly through a single-expert layer where out = RNE(y * r).
+    L = moe_layer(seed=14, experts=2, top_k=2, hidden=256, intermediate=256, tokens=2, pack=False)
+    ids = np.array([[1, 1], [0, 0]], np.int32)
+    w = np.array([[0.375, 0.25], [0.5, 0.5]], np.float32)
+    got, _ = _run(L, device, ids=ids, weights=w)
+    r = oracle_routing.route_weights(ids, w, 2)
+    assert r[0, 1] == 0.625 and r[1, 0] == 1.0
+    assert_moe_close(got, _oracle(L, ids=ids, weights=w))

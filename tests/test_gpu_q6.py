@@ -1,0 +1,158 @@
+"""GPU parity for the Q6_K decode and the decode-fused projection (q6_matmul).
+
+Decode must be bit-exact against the oracle; the projection must meet the
+reference's own tolerance against its FP64 oracle (rtol 2e-5, atol 2e-4,
+kaggle/tests/test_packed_q6.py:51-81) and, with BF16 output, a max relative
+error of 1e-2."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gguf, packed_q6
+from q6moe import pack_q6
+from q6moe.kernel import q6_decode, q6_matmul, q6_pack
+from q6moe.quant import dequantize_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def _to_dev(packed, device):
+    return (torch.from_numpy(packed.data).to(device), torch.from_numpy(packed.scales).to(device))
+
+
+def _bf16_bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def test_decode_bit_exact_all_codes_subscales_and_fp16_extremes(device):
+    raw = packed_q6.fixture(64, 256)
+    d = np.array([0, -0.0, 65504, -65504, 2**-24, -(2**-24), 2**-14, 1], dtype="<f2")
+    raw[:8, 0, 208:] = d.view(np.uint8).reshape(8, 2)
+    raw[..., 192:208] = np.arange(1024, dtype=np.uint16).astype(np.uint8).reshape(64, 1, 16)
+    data, scales = _to_dev(pack_q6(raw, 256), device)
+    got = _bf16_bits(q6_decode(data, scales, output_features=64, input_features=256))
+    want = packed_q6.bf16_bits(packed_q6.decode_reference(raw, 256))
+    np.testing.assert_array_equal(got, want)
+
+
+def test_decode_every_finite_fp16_block_scale(device):
+    bits = np.arange(65536, dtype=np.uint32)
+    bits = bits[(bits & 0x7C00) != 0x7C00].astype(np.uint16)
+    n = bits.size  # 63488 rows, one block each
+    raw = packed_q6.fixture(n, 256, seed=17)
+    raw[:, 0, 192:208] = 1  # sub-scale 1: value = d * code
+    raw[:, 0, 208:210] = bits.view(np.uint8).reshape(n, 2)
+    data, scales = _to_dev(pack_q6(raw, 256), device)
+    got = _bf16_bits(q6_decode(data, scales, output_features=n, input_features=256))
+    want = packed_q6.bf16_bits(packed_q6.decode_reference(raw, 256))
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("outputs,inputs", [(1, 1), (65, 263), (320, 2560), (768, 2048)])
+def test_decode_ragged_shapes_bit_exact(device, outputs, inputs):
+    raw = packed_q6.fixture(outputs, inputs, seed=outputs + inputs)
+    data, scales = _to_dev(pack_q6(raw, inputs), device)
+    got = _bf16_bits(q6_decode(data, scales, output_features=outputs, input_features=inputs))
+    np.testing.assert_array_equal(got, packed_q6.bf16_bits(packed_q6.decode_reference(raw, inputs)))
+
+
+@pytest.mark.parametrize(
+    "batch,outputs,inputs",
+    [(1, 1, 1), (2, 67, 255), (4, 128, 257), (8, 64, 512), (9, 65, 263), (1, 320, 2560),
+     (8, 640, 2560), (8, 768, 2048), (16, 64, 256), (17, 130, 600), (70, 96, 512)],
+)
+def test_projection_matches_fp64_oracle(device, batch, outputs, inputs):
+    raw = packed_q6.fixture(outputs, inputs)
+    x = np.random.default_rng(721).normal(size=(batch, inputs)).astype(np.float32)
+    if batch > 1:
+        x[0] = 0
+    data, scales = _to_dev(pack_q6(raw, inputs), device)
+    xt = torch.from_numpy(x).to(device).to(torch.bfloat16)
+    got = q6_matmul(xt, data, scales, output_features=outputs).cpu().numpy()
+    want = packed_q6.projection_reference(x, raw)
+    assert got.dtype == np.float32 and got.shape == (batch, outputs)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-4)
+    if batch > 1:
+        assert np.all(got[0] == 0)
+
+
+def test_projection_unaligned_x_view(device):
+    raw = packed_q6.fixture(64, 300)
+    x = np.random.default_rng(5).normal(size=(3, 301)).astype(np.float32)
+    data, scales = _to_dev(pack_q6(raw, 300), device)
+    xt = torch.from_numpy(x).to(device).to(torch.bfloat16)[:, 1:]  # ldx 301, offset 1 element
+    got = q6_matmul(xt, data, scales, output_features=64).cpu().numpy()
+    np.testing.assert_allclose(got, packed_q6.projection_reference(x[:, 1:], raw), rtol=2e-5, atol=2e-4)
+
+
+def test_accumulator_reset_between_row_and_token_tiles(device):
+    raw = packed_q6.fixture(128, 512)
+    raw[64:] = raw[:64]
+    data, scales = _to_dev(pack_q6(raw, 512), device)
+    x = np.ones((40, 512), np.float32)
+    x[20:] = -1
+    got = q6_matmul(torch.from_numpy(x).to(device).to(torch.bfloat16), data, scales,
+                    output_features=128).cpu().numpy()
+    np.testing.assert_array_equal(got[:, :64], got[:, 64:])
+    np.testing.assert_array_equal(got[:20], -got[20:])
+    np.testing.assert_array_equal(got[:20], np.broadcast_to(got[0], (20, 128)))
+
+
+def test_single_projection_workload_bf16_output(device):
+    # x bf16 [8, 2048] ~ N(0,1), W [2048 -> 768] ~ N(0, 0.02) quantized to Q6_K, seed 0.
+    from q6moe.synth import projection
+
+    w = projection(seed=0)
+    data, scales = _to_dev(pack_q6(w["raw"], 2048), device)
+    xt = torch.from_numpy(w["x"]).to(device).to(torch.bfloat16)
+    got = q6_matmul(xt, data, scales, output_features=768, out_dtype=torch.bfloat16).float().cpu().numpy()
+    want32 = packed_q6.projection_reference(w["x"], w["raw"])
+    want = packed_q6.bf16_round(want32)
+    rel = np.abs(got - want) / np.maximum(np.abs(want), 1e-3 * np.abs(want).max())
+    assert rel.max() <= 1e-2
+    # bit agreement with RNE of the FP32 result of the same kernel
+    f32 = q6_matmul(xt, data, scales, output_features=768)
+    np.testing.assert_array_equal(_bf16_bits(f32.to(torch.bfloat16)),
+                                  _bf16_bits(torch.from_numpy(got).to(torch.bfloat16)))
+
+
+def test_repeat_runs_are_bitwise_identical(device):
+    raw = packed_q6.fixture(256, 1024)
+    data, scales = _to_dev(pack_q6(raw, 1024), device)
+    x = torch.randn(8, 1024, generator=torch.Generator().manual_seed(1)).to(device).to(torch.bfloat16)
+    a = q6_matmul(x, data, scales, output_features=256)
+    b = q6_matmul(x, data, scales, output_features=256)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("outputs,inputs", [(1, 1), (65, 263), (768, 2048)])
+def test_device_pack_matches_host_pack(device, outputs, inputs):
+    raw = packed_q6.fixture(outputs, inputs, seed=3)
+    host = pack_q6(raw, inputs)
+    data, scales = q6_pack(torch.from_numpy(raw).to(device), inputs)
+    np.testing.assert_array_equal(data.cpu().numpy(), host.data)
+    np.testing.assert_array_equal(scales.cpu().numpy(), host.scales)
+
+
+@pytest.mark.parametrize("qtype", ["Q6_K", "Q4_K", "Q8_0"])
+def test_dequantize_rows_hip_matches_oracle_and_frozen_vectors(device, qtype):
+    from .conftest import GOLDEN
+
+    ref = np.load(GOLDEN / "gguf_py_decoder_reference.npz")
+    raw = ref[f"{qtype}_raw"]
+    values, _ = gguf.block_layout(qtype)
+    width = raw.shape[-2] * values
+    got = dequantize_rows(torch.from_numpy(raw).to(device), qtype, width).cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), ref[f"{qtype}_expected"].view(np.uint32))
+    rng = np.random.default_rng(8)
+    raw = rng.integers(0, 256, (37, 3, raw.shape[-1]), dtype=np.uint8)
+    for off in {"Q6_K": (208,), "Q4_K": (0, 2), "Q8_0": (0,)}[qtype]:
+        raw[..., off : off + 2] = rng.uniform(-0.3, 0.3, (37, 3)).astype("<f2").view(np.uint8).reshape(37, 3, 2)
+    width = 3 * values - 5
+    want = gguf.dequantize_rows(raw, qtype, width)
+    got = dequantize_rows(torch.from_numpy(raw).to(device), qtype, width).cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    gotb = dequantize_rows(torch.from_numpy(raw).to(device), qtype, width, dtype=torch.bfloat16)
+    np.testing.assert_array_equal(_bf16_bits(gotb), packed_q6.bf16_bits(want))
