@@ -1,0 +1,201 @@
+#!/usr/bin/env python3
+"""Benchmark of the packed-Q6 routed-expert decode step on one MI355X.
+
+Workload (default): one MoE expert-FFN decode step with Q6_K experts --
+128 experts, top-8 routing, hidden 2048, expert intermediate 768, SwiGLU,
+8 tokens, weights N(0, 0.02) quantized to Q6_K, x N(0, 1) BF16, router
+logits N(0, 1) -> softmax -> top-8 -> renormalised BF16 weights, seed 1.
+
+A step is one call of the routed FFN (route sort, fused gate/up + SwiGLU,
+down projection, combine). Steps rotate over ``--layers`` copies of the
+layer's expert tables at distinct HBM addresses (default 4: about 0.8 GB of
+active expert bytes per rotation, over 3x the 256 MB Infinity Cache), so the
+weights stream from HBM. The metric is algorithmic bytes per step (active
+experts' packed weights + activations + routing inputs + output) / time.
+
+Output: one JSON line (rank 0) with the ``roofline`` of the dominant kernel
+(moe_gate_up_kernel, timed with HIP events on its own stream) and the
+``cpu_baseline`` (the NumPy oracle on this host, one step, one thread).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "data-synth-tpu_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "Q6 expert-GEMM HBM GB/s (decode) + TFLOP/s (prefill), % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0
+EXPERTS, TOP_K, HIDDEN, INTER, TOKENS, SEED = 128, 8, 2048, 768, 8, 1
+Q6_PROJ_BYTES = 1_277_952 + 12_288  # one 768x2048 (or 2048x768) Q6_K projection, SoA planes
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def step_bytes(active, routes):
+    """Algorithmic HBM bytes of one decode step (each needed byte once)."""
+    weights = active * 3 * Q6_PROJ_BYTES
+    x = TOKENS * HIDDEN * 2
+    out = TOKENS * HIDDEN * 2
+    routing = TOKENS * TOP_K * (4 + 2)
+    return weights + x + out + routing
+
+
+def gate_up_bytes(active, routes):
+    """Algorithmic bytes of one moe_gate_up_kernel launch: gate+up of the active
+    experts, the token activations it reads and the SwiGLU rows it writes."""
+    return active * 2 * Q6_PROJ_BYTES + TOKENS * HIDDEN * 2 + routes * INTER * 2
+
+
+def cpu_baseline(L):
+    """The NumPy oracle (one thread) on one full decode step of the same workload."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import moe as oracle_moe
+
+    with threadpool_limits(1):
+        t0 = time.perf_counter()
+        oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"], L["ids"], L["weights"],
+                              types=("Q6_K",) * 3, hidden=HIDDEN, intermediate=INTER)
+        return time.perf_counter() - t0
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        log("bench.py measures one GPU: the packed-expert path runs on a single MI355X here "
+            "(sharding is by expert, see the design notes); run with --gpus 1")
+        return 2
+    if not (1 <= args.steps <= 100000 and 0 <= args.warmup <= 10000 and 1 <= args.layers <= 16):
+        log("steps must be 1..100000, warmup 0..10000, layers 1..16")
+        return 2
+
+    import numpy as np
+    import torch
+
+    from q6moe.experts import expert_parallel, pack_experts
+    from q6moe.synth import moe_layer
+
+    dev = torch.device("cuda", 0)
+    log("generating the decode workload (seed 1) ...")
+    t0 = time.perf_counter()
+    L = moe_layer(seed=SEED, experts=EXPERTS, top_k=TOP_K, hidden=HIDDEN, intermediate=INTER,
+                  tokens=TOKENS, pack=False)
+    log(f"  quantized {EXPERTS} experts in {time.perf_counter() - t0:.1f}s")
+    base = [pack_experts(L[n], "Q6_K", INTER if n != "down" else HIDDEN, HIDDEN if n != "down" else INTER, dev)
+            for n in ("gate", "up", "down")]
+    layers = [base]
+    for _ in range(args.layers - 1):
+        layers.append([type(t)(t.qtype, t.data.clone(), t.scales.clone(), t.rows, t.width) for t in base])
+    x = torch.from_numpy(L["x"]).to(dev).to(torch.bfloat16)
+    ids = torch.from_numpy(L["ids"]).to(dev)
+    w = torch.from_numpy(L["weights"]).to(dev).to(torch.bfloat16)
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q6_K", hidden=HIDDEN,
+                         intermediate=INTER)
+    ws = torch.empty(fn.workspace_bytes(TOKENS, TOP_K, EXPERTS), dtype=torch.uint8, device=dev)
+    out = torch.empty((TOKENS, HIDDEN), dtype=torch.bfloat16, device=dev)
+    active = len(np.unique(L["ids"]))
+    routes = int(np.count_nonzero(L["weights"]))
+
+    def step(i, events=None):
+        g, u, d = layers[i % len(layers)]
+        fn(g, u, d, x, ids, w, workspace=ws, out=out, events=events)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # Whole-step throughput: K back-to-back steps between two synchronisations.
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    start.record()
+    for i in range(args.steps):
+        step(i)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    gpu_ms = start.elapsed_time(end)
+    ms_per_step = max(wall * 1e3, gpu_ms) / args.steps
+    nbytes = step_bytes(active, routes)
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+
+    # Per-kernel durations with HIP events recorded between the launches.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    for row in evs:
+        for ev in row:
+            ev.record()
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        step(i, events=evs[i])
+    torch.cuda.synchronize()
+    phase = np.array([[row[j].elapsed_time(row[j + 1]) for j in range(4)] for row in evs]) * 1e3  # us
+    ph = phase.mean(0)
+    gu_bytes = gate_up_bytes(active, routes)
+    achieved = gu_bytes / (ph[1] * 1e-6) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations/logits, N(0,0.02) weights quantized to Q6_K)",
+        "config": {
+            "workload": "moe_decode_q6k_e128_top8_h2048_i768_b8",
+            "experts": EXPERTS, "top_k": TOP_K, "hidden": HIDDEN, "intermediate": INTER,
+            "tokens": TOKENS, "seed": SEED, "active_experts": active, "layer_copies": args.layers,
+            "bytes_per_step": nbytes,
+        },
+        "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
+        "phases_us": {k: round(float(v), 2) for k, v in zip(("route", "gate_up", "down", "combine"), ph)},
+        "roofline": {
+            "kernel": "moe_gate_up_kernel",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": gu_bytes,
+            "avg_launch_us": round(float(ph[1]), 3),
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle on one step (one thread) ...")
+        secs = cpu_baseline(L)
+        result["cpu_baseline"] = {
+            "value": round(nbytes / secs / 1e9, 4),
+            "unit": "GB/s",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"one full decode step of the same workload ({active} active experts decoded, "
+                      f"SwiGLU FFN, combine) by the NumPy oracle: {secs:.2f} s",
+        }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -442,21 +442,23 @@ static int validate_table(const q6moe_table& t, const char* name, int64_t rows, 
   return Q6MOE_OK;
 }
 
-template <int FMT>
+template <int FMT, typename Mark>
 static void launch_phases(const Proj& g, const Proj& u, const Proj& d, const TokenSrc& src, int grid_x,
                           int max_tokens, const uint16_t* x, int H, int I, uint16_t* act, uint16_t* y,
-                          hipStream_t s) {
+                          hipStream_t s, Mark mark) {
   const int kw1 = g.kb < 8 ? g.kb : 8;
   const int kw2 = d.kb < 8 ? d.kb : 8;
   const unsigned rb1 = (unsigned)cdiv(I, 16), rb2 = (unsigned)cdiv(H, 16 * 2);
   if (max_tokens <= 16) {
     hipLaunchKernelGGL((moe_gate_up_kernel<FMT, 1, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
                        H, act, I, kw1);
+    mark(2);
     hipLaunchKernelGGL((moe_down_kernel<FMT, 1, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
                        H, kw2);
   } else {
     hipLaunchKernelGGL((moe_gate_up_kernel<FMT, 4, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
                        H, act, I, kw1);
+    mark(2);
     hipLaunchKernelGGL((moe_down_kernel<FMT, 4, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
                        H, kw2);
   }
@@ -524,9 +526,14 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   ws.sh_y = Is ? reinterpret_cast<uint16_t*>(w + L.sh_y) : nullptr;
 
   hipStream_t s = (hipStream_t)stream;
+  auto mark = [&](int i) {
+    if (a->events && a->events[i]) hipEventRecord((hipEvent_t)a->events[i], s);
+  };
+  mark(0);
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, s, a->ids, a->weights, (int)B, (int)K,
                      (int)E, (int)kPrefillTile, ws);
   if ((rc = check_launch("moe_route_kernel"))) return rc;
+  mark(1);
 
   TokenSrc routed{0, (int)B, ws.hdr, ws.active, ws.act_off, ws.route_tok};
   const int slots = (int)(E < B * K ? E : B * K);
@@ -534,21 +541,25 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
              d = make_proj(a->down, (int)H, (int)I);
   const int max_tokens = (int)B;  // an expert sees each token at most once
   if (a->gate.qtype == Q6MOE_Q6_K)
-    launch_phases<FMT_Q6>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s);
+    launch_phases<FMT_Q6>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s, mark);
   else
-    launch_phases<FMT_Q4K>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s);
+    launch_phases<FMT_Q4K>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s, mark);
   if ((rc = check_launch("moe expert kernels"))) return rc;
   if (Is) {
     TokenSrc dense{1, (int)B, nullptr, nullptr, nullptr, nullptr};
     const Proj sg = make_proj(a->shared_gate, (int)Is, (int)H), su = make_proj(a->shared_up, (int)Is, (int)H),
                sd = make_proj(a->shared_down, (int)H, (int)Is);
+    auto none = [](int) {};
     if (a->gate.qtype == Q6MOE_Q6_K)
-      launch_phases<FMT_Q6>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s);
+      launch_phases<FMT_Q6>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s, none);
     else
-      launch_phases<FMT_Q4K>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s);
+      launch_phases<FMT_Q4K>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s, none);
     if ((rc = check_launch("moe shared expert kernels"))) return rc;
   }
+  mark(3);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)B, (unsigned)cdiv(H, 256 * 8)), dim3(256), 0, s,
                      ws.tok_pos, ws.route_w, ws.y, (int)K, (int)H, ws.sh_y, a->shared_scale, a->out);
-  return check_launch("moe_combine_kernel");
+  rc = check_launch("moe_combine_kernel");
+  mark(4);
+  return rc;
 }

@@ -1,9 +1,9 @@
 // Q6_K / Q4_K / Q8_0 decode kernels and the on-device GGUF -> SoA repack.
 //
 //  * q6_soa_decode_kernel  -- whole-matrix decode of the packed SoA planes to
-//    BF16, through the SAME unit decoder the matmul kernels use, so the
-//    bit-exact decode test also pins the operands the MFMA path consumes
-//    (kaggle/packed_q6/kernel.py:44-62).
+//    BF16 through the unit decoder the matmul kernels use, in its exact-sign
+//    form ds * (c - 32) (kaggle/packed_q6/kernel.py:44-62); the matmul form
+//    differs only in the sign of exact zeros.
 //  * gguf_decode_kernel    -- dequantize_rows for raw GGUF rows
 //    (kaggle/glm53_offload/gguf_quant.py:111-173).
 //  * q6_pack_kernel        -- pack_q6's byte permutation
@@ -27,7 +27,7 @@ __global__ void __launch_bounds__(256) q6_soa_decode_kernel(const uint8_t* __res
   Q6Raw raw;
   q6_load(raw, data + t * kTileBytes, scales + t * 128, row, jA);
   u32x4 a[8];
-  q6_decode_unit(raw, jA, a);
+  q6_decode_unit<true>(raw, jA, a);
   const int gn = tile * kTileRows + row;
   if (gn >= n) return;
   uint16_t* orow = out + (int64_t)gn * ldo;

@@ -66,14 +66,25 @@ __device__ __forceinline__ uint32_t q6_codes_hi(uint32_t ql, uint32_t hs) {
 }
 
 // Eight weights (two code dwords) -> one MFMA bf16x8 operand (4 dwords),
-// w = RNE_bf16(ds * (c - 32)) computed as fma(c, ds, -32*ds), which is exact
-// because both ds*c and ds*32 are exact in FP32 (F7 of the numerics contract).
+// w = RNE_bf16(ds * (c - 32)) computed as fma(c, ds, -32*ds). Both ds*c and
+// ds*32 are exact in FP32, so the value is exact; only the sign of an exact
+// zero can differ from ds * (c - 32) (+0 instead of -0), which no sum of
+// products can observe. q6_frag_exact keeps the reference's signed zeros.
 __device__ __forceinline__ u32x4 q6_frag(uint32_t c0, uint32_t c1, float ds, float nds) {
   u32x4 r;
   r[0] = pack_bf16x2(__builtin_fmaf(ubyte_f(c0, 0), ds, nds), __builtin_fmaf(ubyte_f(c0, 1), ds, nds));
   r[1] = pack_bf16x2(__builtin_fmaf(ubyte_f(c0, 2), ds, nds), __builtin_fmaf(ubyte_f(c0, 3), ds, nds));
   r[2] = pack_bf16x2(__builtin_fmaf(ubyte_f(c1, 0), ds, nds), __builtin_fmaf(ubyte_f(c1, 1), ds, nds));
   r[3] = pack_bf16x2(__builtin_fmaf(ubyte_f(c1, 2), ds, nds), __builtin_fmaf(ubyte_f(c1, 3), ds, nds));
+  return r;
+}
+
+__device__ __forceinline__ u32x4 q6_frag_exact(uint32_t c0, uint32_t c1, float ds) {
+  u32x4 r;
+  r[0] = pack_bf16x2(ds * (ubyte_f(c0, 0) - 32.f), ds * (ubyte_f(c0, 1) - 32.f));
+  r[1] = pack_bf16x2(ds * (ubyte_f(c0, 2) - 32.f), ds * (ubyte_f(c0, 3) - 32.f));
+  r[2] = pack_bf16x2(ds * (ubyte_f(c1, 0) - 32.f), ds * (ubyte_f(c1, 1) - 32.f));
+  r[3] = pack_bf16x2(ds * (ubyte_f(c1, 2) - 32.f), ds * (ubyte_f(c1, 3) - 32.f));
   return r;
 }
 
@@ -129,7 +140,8 @@ __device__ __forceinline__ void q6_load(Q6Raw& r, const uint8_t* tile, const uin
   r.d = *reinterpret_cast<const uint16_t*>(dplane + row * 2);
 }
 
-// Decode a loaded unit into 8 A fragments.
+// Decode a loaded unit into 8 A fragments (kExact: reference signed zeros).
+template <bool kExact = false>
 __device__ __forceinline__ void q6_decode_unit(const Q6Raw& r, int jA, u32x4 a[8]) {
   const float d = half_bits_to_float(r.d);
   const int q0 = jA >> 1;
@@ -152,7 +164,7 @@ __device__ __forceinline__ void q6_decode_unit(const Q6Raw& r, int jA, u32x4 a[8
         c0 = q6_codes_lo(ql[2 * e], h0);
         c1 = q6_codes_lo(ql[2 * e + 1], h1);
       }
-      a[2 * g + e] = q6_frag(c0, c1, ds, nds);
+      a[2 * g + e] = kExact ? q6_frag_exact(c0, c1, ds) : q6_frag(c0, c1, ds, nds);
     }
   }
 }

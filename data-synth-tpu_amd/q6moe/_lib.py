@@ -57,6 +57,7 @@ class MoeArgs(ctypes.Structure):
         ("workspace", _vp),
         ("workspace_bytes", _size),
         ("mode", _int),
+        ("events", ctypes.POINTER(_vp)),
     ]
 
 

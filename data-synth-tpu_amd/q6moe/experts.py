@@ -159,7 +159,11 @@ class ExpertFFN:
         return int(_lib.load().q6moe_moe_workspace_size(
             tokens, top_k, experts, self.hidden, self.intermediate, shared_intermediate))
 
-    def __call__(self, gate, up, down, x, ids, weights, *, shared=None, workspace=None, out=None):
+    def __call__(self, gate, up, down, x, ids, weights, *, shared=None, workspace=None, out=None,
+                 events=None):
+        """``events``: optional 5 timing events (torch.cuda.Event, already
+        recorded once so they exist) stamped before routing, after routing,
+        after gate/up, after down and after the combine."""
         H, I, q = self.hidden, self.intermediate, self.qtype
         gate = _as_table(gate, q, I, H, "gate")
         up = _as_table(up, q, I, H, "up")
@@ -209,6 +213,12 @@ class ExpertFFN:
         args.workspace = workspace.data_ptr()
         args.workspace_bytes = workspace.numel()
         args.mode = self.mode
+        if events is not None:
+            if len(events) != 5:
+                raise ValueError("events must hold 5 timing events")
+            handles = (ctypes.c_void_p * 5)(*[ctypes.c_void_p(ev.cuda_event) for ev in events])
+            keep.append(handles)
+            args.events = ctypes.cast(handles, ctypes.POINTER(ctypes.c_void_p))
         lib = _lib.load()
         with torch.cuda.device(x.device):
             rc = lib.q6moe_moe_forward(ctypes.byref(args), _lib.stream_handle(x.device))

@@ -120,7 +120,12 @@ typedef struct q6moe_moe_args {
   void* workspace;             /* >= q6moe_moe_workspace_size(...) bytes, 256-byte aligned */
   size_t workspace_bytes;
   int mode;                    /* 0 auto, 1 decode kernels, 2 grouped-GEMM (prefill) kernels */
+  /* optional profiling: NULL, or Q6MOE_MOE_EVENTS hipEvent_t handles recorded on ``stream``
+     before routing, after routing, after gate/up, after down, after the combine */
+  void* const* events;
 } q6moe_moe_args;
+
+#define Q6MOE_MOE_EVENTS 5
 
 size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_t experts, int64_t hidden,
                                 int64_t intermediate, int64_t shared_intermediate);

@@ -49,6 +49,22 @@ def test_decode_every_finite_fp16_block_scale(device):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("outputs,inputs", [(64, 256), (65, 600)])
+def test_matmul_operands_equal_decoded_weights(device, outputs, inputs):
+    # x = identity rows: y[i, n] = W[n, i] exactly (one nonzero product per
+    # sum), so the MFMA operands are pinned value-for-value (+0 == -0).
+    raw = packed_q6.fixture(outputs, inputs, seed=21)
+    data, scales = _to_dev(pack_q6(raw, inputs), device)
+    w = packed_q6.bf16_round(packed_q6.decode_reference(raw, inputs))
+    for start in range(0, inputs, 128):
+        rows = np.arange(start, min(inputs, start + 128))
+        x = np.zeros((rows.size, inputs), np.float32)
+        x[np.arange(rows.size), rows] = 1
+        y = q6_matmul(torch.from_numpy(x).to(device).to(torch.bfloat16), data, scales,
+                      output_features=outputs).cpu().numpy()
+        np.testing.assert_array_equal(y, w[:, rows].T)
+
+
 @pytest.mark.parametrize("outputs,inputs", [(1, 1), (65, 263), (320, 2560), (768, 2048)])
 def test_decode_ragged_shapes_bit_exact(device, outputs, inputs):
     raw = packed_q6.fixture(outputs, inputs, seed=outputs + inputs)
