@@ -169,7 +169,7 @@ def main():
             "bytes_per_step": nbytes,
         },
         "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
-        "phases_us": {k: round(float(v), 2) for k, v in zip(("route", "gate_up", "down", "combine"), ph)},
+        "phases_us": {k: round(float(v), 2) for k, v in zip(("pre", "gate_up", "down", "combine"), ph)},
         "roofline": {
             "kernel": "moe_gate_up_kernel",
             "bound": "hbm",

@@ -367,7 +367,7 @@ __global__ void __launch_bounds__(256)
 // ---------------------------------------------------------------------------
 struct WsLayout {
   size_t hdr, active, act_off, tile_off, tile_slot, ent_r, ent_pos, route_tok, route_w, tok_pos, act,
-      y, sh_act, sh_y, total;
+      y, sh_act, sh_y, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -396,6 +396,12 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
   L.y = take(2 * n * H);
   L.sh_act = take(Is > 0 ? 2 * B * Is : 0);
   L.sh_y = take(Is > 0 ? 2 * B * H : 0);
+  L.slot_e = take(4 * E);
+  L.slot_t0 = take(4 * E);
+  L.slot_cnt = take(4 * E);
+  L.tok_n = take(4 * B);
+  L.route_dst = take(4 * n);
+  L.contrib = take(4 * n * H);
   L.total = o;
   return L;
 }
@@ -529,6 +535,54 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   auto mark = [&](int i) {
     if (a->events && a->events[i]) hipEventRecord((hipEvent_t)a->events[i], s);
   };
+  const bool decode = dec_supported(B, K, E) && (a->mode == 1 || (a->mode == 0 && B <= 64));
+  if (a->mode == 1 && !dec_supported(B, K, E)) {
+    set_error("moe_forward: decode mode needs tokens*top_k <= 1024, top_k <= 32, experts <= 256");
+    return Q6MOE_ERR_INVALID;
+  }
+  const int fmt = a->gate.qtype == Q6MOE_Q6_K ? FMT_Q6 : FMT_Q4K;
+  if (decode) {
+    mark(0);
+    if (Is) {
+      TokenSrc dense{1, (int)B, nullptr, nullptr, nullptr, nullptr};
+      const Proj sg = make_proj(a->shared_gate, (int)Is, (int)H), su = make_proj(a->shared_up, (int)Is, (int)H),
+                 sd = make_proj(a->shared_down, (int)H, (int)Is);
+      auto none = [](int) {};
+      if (fmt == FMT_Q6)
+        launch_phases<FMT_Q6>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s, none);
+      else
+        launch_phases<FMT_Q4K>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s, none);
+      if ((rc = check_launch("moe shared expert kernels"))) return rc;
+    }
+    mark(1);
+    DecArgs D;
+    D.gate = make_proj(a->gate, (int)I, (int)H);
+    D.up = make_proj(a->up, (int)I, (int)H);
+    D.down = make_proj(a->down, (int)H, (int)I);
+    D.R = DecRoute{a->ids, a->weights, (int)B, (int)K, (int)E};
+    D.T.hdr = ws.hdr;
+    D.T.slot_e = reinterpret_cast<int*>(w + L.slot_e);
+    D.T.slot_t0 = reinterpret_cast<int*>(w + L.slot_t0);
+    D.T.slot_cnt = reinterpret_cast<int*>(w + L.slot_cnt);
+    D.T.tok_n = reinterpret_cast<int*>(w + L.tok_n);
+    D.T.route_w = ws.route_w;
+    D.T.route_dst = reinterpret_cast<int*>(w + L.route_dst);
+    D.x = a->x;
+    D.H = (int)H;
+    D.I = (int)I;
+    D.max_slots = (int)(E < B * K ? E : B * K);
+    D.act = ws.act;
+    D.contrib = reinterpret_cast<float*>(w + L.contrib);
+    D.sh_y = ws.sh_y;
+    D.sh_scale = a->shared_scale;
+    D.out = a->out;
+    D.after_gate_up = a->events ? a->events[2] : nullptr;
+    D.after_down = a->events ? a->events[3] : nullptr;
+    if ((rc = launch_moe_decode(fmt, D, s))) return rc;
+    rc = check_launch("moe decode kernels");
+    mark(4);
+    return rc;
+  }
   mark(0);
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, s, a->ids, a->weights, (int)B, (int)K,
                      (int)E, (int)kPrefillTile, ws);

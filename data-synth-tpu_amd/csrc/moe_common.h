@@ -1,5 +1,6 @@
 // Shared definitions of the routed-expert kernels (decode and grouped GEMM).
 #pragma once
+#include "q6moe_api.h"
 #include "q6moe_device.h"
 
 namespace q6moe {
@@ -42,6 +43,41 @@ struct TokenSrc {
   const int* act_off;
   const int* route_tok; // token of route position (phase 1 input rows)
 };
+
+// Decode path (small token counts): routing inputs and published tables.
+struct DecRoute {
+  const int32_t* ids;
+  const uint16_t* wts;
+  int B, K, E;
+};
+
+struct DecTables {
+  int* hdr;          // [0] active experts
+  int* slot_e;       // [E] expert of slot
+  int* slot_t0;      // [E] first route position
+  int* slot_cnt;     // [E] routes
+  int* tok_n;        // [B] routes of each token
+  float* route_w;    // [routes] BF16 route weight as FP32
+  int* route_dst;    // [routes] token-major slot b*K + rank (rank = ascending expert id)
+};
+
+struct DecArgs {
+  Proj gate, up, down;
+  DecRoute R;
+  DecTables T;
+  const uint16_t* x;
+  int H, I, max_slots;
+  uint16_t* act;
+  float* contrib;  // [B*K, H] FP32 f32(y) * f32(r), token-major
+  const uint16_t* sh_y;
+  const uint16_t* sh_scale;
+  uint16_t* out;
+  void* after_gate_up;  // optional hipEvent_t
+  void* after_down;     // optional hipEvent_t
+};
+
+bool dec_supported(int64_t B, int64_t K, int64_t E);
+int launch_moe_decode(int fmt, const DecArgs& A, hipStream_t s);
 
 // ---------------------------------------------------------------------------
 // Unit decoders: 16 output rows x one 256-wide K block -> 8 MFMA A operands.
