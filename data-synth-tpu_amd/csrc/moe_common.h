@@ -52,7 +52,7 @@ struct DecRoute {
 };
 
 struct DecTables {
-  int* hdr;          // [0] active experts
+  int* hdr;          // [0] active experts, [1] routes
   int* slot_e;       // [E] expert of slot
   int* slot_t0;      // [E] first route position
   int* slot_cnt;     // [E] routes

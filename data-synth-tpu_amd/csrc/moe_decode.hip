@@ -1,87 +1,143 @@
-// Decode-shaped routed experts: three launches per step.
+// Decode-shaped routed experts: three launches per step, one wave per workgroup.
 //
-//   moe_dec_gate_up_kernel  every workgroup derives the (small) routing itself
-//        -- merged BF16 route weights (kaggle/qwen38_tpu/experts.py:66-73),
-//        active experts in ascending id (:74-76), the expert's tokens in
-//        ascending order -- then each wave streams one 16-row group of gate
-//        and up over the full K for that expert and applies SwiGLU in
+//   moe_dec_gate_up_kernel  grid (16-row group, expert slot). The wave derives
+//        the (small) routing itself -- merged BF16 route weight per (token,
+//        expert) (kaggle/qwen38_tpu/experts.py:66-73), active experts in
+//        ascending id (:74-76), the slot's tokens ascending -- then streams its
+//        16 rows of gate and up over the full K and applies SwiGLU in
 //        registers: a = RNE(RNE(g * sigmoid(g)) * u) (experts.py:103-107).
-//        Workgroups of row block 0 publish the routing tables.
-//   moe_dec_down_kernel     each wave streams one 16-row group of down,
-//        y = RNE(a Wd^T) (experts.py:108), and stores the exact FP32 product
-//        f32(y) * f32(r) token-major at the route's rank among its token's
-//        experts (ascending expert id).
+//        Row group 0 of every slot publishes that slot's routing tables.
+//   moe_dec_down_kernel     grid (block of kDownRows row groups, expert slot).
+//        The wave streams its rows of down, y = RNE(a Wd^T) (experts.py:108),
+//        and stores the exact FP32 product f32(y) * f32(r) token-major at the
+//        route's rank among its token's experts (ascending expert id).
 //   moe_dec_combine_kernel  out = RNE(sum over ranks of the contributions),
 //        i.e. the FP32 sum over experts in ascending id (experts.py:129-131),
 //        plus RNE(routed + shared) with a shared expert (engine.py:199-203).
 //
 // Memory pipeline: each wave owns a ring of kStages weight units (16 rows x
 // one 256-wide K block) in LDS, filled by direct global->LDS DMA
-// (global_load_lds) kStages-1 units ahead of the unit being decoded, so the
-// bytes in flight do not cost registers. The token activations a workgroup
-// multiplies are staged in LDS once, so inside the main loop the only vector
-// memory traffic is the ring DMA and every wait count is a compile-time
-// constant. Weights are read exactly once per step.
+// (global_load_lds) kStages-1 units ahead of the unit being decoded, so bytes
+// in flight cost no registers. The token operands of a K block (at most 16
+// tokens: one per MFMA column) are loaded into one of two register sets
+// together with the first unit of the previous K block. Every wait count is a
+// compile-time constant of the unit's position in its K block. One-wave
+// workgroups spread the waves evenly over the SIMDs. Weights are read once
+// per 16 routes of an expert.
+#include <type_traits>
+
 #include "moe_common.h"
 #include "q6moe_api.h"
 
-#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(p))
+// LDS address of a generic pointer into shared memory (its low 32 bits).
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(uint32_t)(uintptr_t)(p))
 
 namespace q6moe {
 
 constexpr int kDecMaxEntries = 1024;  // tokens * top_k handled by the decode path
 constexpr int kDecMaxTokens = 256;    // tokens handled by the decode path
 constexpr int kDecMaxExperts = 256;
-constexpr int kDecWaves = 4;
-constexpr int kStages = 2;
-constexpr int kLdsBudget = 40 * 1024;  // per workgroup: four workgroups per CU
+constexpr int kStages = 3;
+constexpr int kDownRows = 3;  // 16-row groups of down per wave
+constexpr int kPassTokens = 16;  // routes per weight pass (MFMA columns)
 
 // One unit in LDS. Q6_K: ql 2048 B and qh 1024 B chunk-major (slot = chunk*16 +
 // row), sub-scales 256 B and FP16 d 32 B (+ padding) row-major. Q4_K: 16 rows x
 // 9 chunks of 16 B, chunk-major in three 1 KB groups.
-constexpr int kStageBytes = 3584;
+constexpr int kUnitBytes = 3584;
 constexpr int kUnitDma = 5;  // DMA instructions per unit (both formats)
+constexpr int kXLoads = 8;   // token-operand loads per K block (one per MFMA)
 
-__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, LDS_PTR(lds_base), 16, 0, 0);
+static_assert(kStages * kUnitBytes >= 8 * kDecMaxEntries + 4 * kDecMaxExperts,
+              "routing scratch overlays the ring");
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
-__device__ __forceinline__ void dma4(const void* src, void* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, LDS_PTR(lds_base), 4, 0, 0);
+
+// Stream addresses are a wave-uniform base (SGPRs) plus a 32-bit per-lane
+// offset that stays in one VGPR for the whole stream.
+// (readfirstlane pins the base to SGPRs so the load uses the SGPR-base form.)
+__device__ __forceinline__ const uint8_t* sgpr_ptr(const uint8_t* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t*)(((uint64_t)hi << 32) | lo);
+}
+// Hides how a per-lane offset was formed, so that no constant part of it is
+// re-associated into a 64-bit per-lane address.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t voff, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(sgpr_ptr(base) + voff, LDS_PTR(lds_base), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t voff, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(sgpr_ptr(base) + voff, LDS_PTR(lds_base), 4, 0, 0);
+}
+
+// Token operands are read through a buffer resource (base in SGPRs).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
 // s_waitcnt vmcnt(n) with lgkmcnt/expcnt left alone (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Wait until at most ``ahead`` units issued after the current one are pending.
-__device__ __forceinline__ void wait_units(int ahead) {
-  if (kStages > 2 && ahead >= 2)
-    wait_vm<2 * kUnitDma>();
-  else if (ahead >= 1)
-    wait_vm<kUnitDma>();
-  else
-    wait_vm<0>();
+// Vector-memory instructions issued for unit p of P per K block: the unit's
+// DMA, plus the next K block's token operands with unit 0.
+template <int P>
+constexpr int unit_ops(int p) {
+  return kUnitDma + (p % P == 0 ? kXLoads : 0);
+}
+template <int P>
+constexpr int younger_ops(int p, int ahead) {
+  int s = 0;
+  for (int i = 1; i <= ahead; ++i) s += unit_ops<P>(p + i);
+  return s;
 }
 
+// One expert's projection streamed as units of 16 rows x one K block into a
+// ring stage; decode() turns a stage into the 8 MFMA A operands of the lane.
 template <int FMT>
-struct LdsUnit;
+struct WStream;
 
 template <>
-struct LdsUnit<FMT_Q6> {
-  // Issue the DMA of rows 16*(rg%4).. of tile (rg/4), K block kb into ``st``.
-  static __device__ __forceinline__ void issue(const Proj& p, int64_t e, int rg, int kb, int lane,
-                                               uint8_t* st) {
-    const int64_t t = (int64_t)(rg >> 2) * p.kb + kb;
-    const uint8_t* tile = p.data + e * p.dstride + t * kTileBytes;
-    const int r0 = (rg & 3) * 16, j = lane & 15, c = lane >> 4;
-    const uint8_t* ql = tile + kQlOff + (r0 + j) * 128 + 16 * c;
-    dma16(ql, st);
-    dma16(ql + 64, st + 1024);
-    dma16(tile + kQhOff + (r0 + j) * 64 + 16 * c, st + 2048);
-    dma4(tile + kScOff + r0 * 16 + 4 * lane, st + 3072);
-    dma4(p.scales + e * p.sstride + t * 128 + r0 * 2 + 4 * (lane & 7), st + 3328);
+struct WStream<FMT_Q6> {
+  const uint8_t* data;
+  const uint8_t* scales;
+  int kbs;
+  uint32_t v_ql, v_qh, v_sc, v_d;  // per-lane byte offsets
+  __device__ __forceinline__ WStream(const Proj& p, int64_t e, int lane) {
+    data = p.data + e * p.dstride;
+    scales = p.scales + e * p.sstride;
+    kbs = p.kb;
+    const int j = lane & 15, c = lane >> 4;
+    v_ql = opaque(kQlOff + j * 128 + 16 * c);
+    v_qh = opaque(kQhOff + j * 64 + 16 * c);
+    v_sc = opaque(kScOff + 4 * lane);
+    v_d = opaque(4 * (lane & 7));
+  }
+  // rows 16*(rg%4).. of tile row rg/4, K block kb
+  __device__ __forceinline__ void issue(int rg, int kb, uint8_t* st) const {
+    const int64_t t = (int64_t)(rg >> 2) * kbs + kb;
+    const int r0 = (rg & 3) * 16;
+    const uint8_t* tile = data + t * kTileBytes;
+    dma16(tile + r0 * 128, v_ql, st);
+    dma16(tile + r0 * 128 + 64, v_ql, st + 1024);
+    dma16(tile + r0 * 64, v_qh, st + 2048);
+    dma4(tile + r0 * 16, v_sc, st + 3072);
+    dma4(scales + t * 128 + r0 * 2, v_d, st + 3328);
   }
   static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {
     const int j = lane & 15, jA = lane >> 4;
@@ -97,25 +153,34 @@ struct LdsUnit<FMT_Q6> {
 };
 
 template <>
-struct LdsUnit<FMT_Q4K> {
+struct WStream<FMT_Q4K> {
   // 16 GGUF rows (144 B each) of K block kb: chunk c (16 B) of row j goes to
   // group c/4, slot (c%4)*16 + j. Chunk 0 is the header, chunks 1-8 the codes.
-  static __device__ __forceinline__ void issue(const Proj& p, int64_t e, int rg, int kb, int lane,
-                                               uint8_t* st) {
-    const int j = lane & 15, c = lane >> 4;
+  const uint8_t* data;
+  int rows, row_bytes, j;
+  uint32_t v_c;
+  __device__ __forceinline__ WStream(const Proj& p, int64_t e, int lane) {
+    data = p.data + e * p.dstride;
+    rows = p.rows;
+    row_bytes = p.kb * 144;
+    j = lane & 15;
+    v_c = 16 * (lane >> 4);
+  }
+  __device__ __forceinline__ void issue(int rg, int kb, uint8_t* st) const {
     int row = rg * 16 + j;
-    row = row < p.rows ? row : p.rows - 1;  // stay in bounds; result row discarded
-    const uint8_t* blk = p.data + e * p.dstride + ((int64_t)row * p.kb + kb) * 144;
-    dma16(blk + 16 * c, st);
-    dma16(blk + 64 + 16 * c, st + 1024);
-    dma16(blk + 128, st + 2048);  // chunk 8 (each lane group repeats it)
-    dma4(blk, st + 3072);         // keeps kUnitDma uniform; not read
-    dma4(blk, st + 3328);
+    row = row < rows ? row : rows - 1;  // stay in bounds; result row discarded
+    const uint32_t vo = opaque((uint32_t)(row * row_bytes)), voc = opaque(vo + v_c);
+    const uint8_t* blk = data + kb * 144;
+    dma16(blk, voc, st);
+    dma16(blk + 64, voc, st + 1024);
+    dma16(blk + 128, vo, st + 2048);  // chunk 8 (each lane group repeats it)
+    dma4(blk, vo, st + 3072);         // keeps kUnitDma uniform; not read
+    dma4(blk, vo, st + 3328);
   }
   static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {
-    const int j = lane & 15, jA = lane >> 4;
+    const int jj = lane & 15, jA = lane >> 4;
     auto chunk = [&](int c) -> u32x4 {
-      return *reinterpret_cast<const u32x4*>(st + 1024 * (c >> 2) + 16 * ((c & 3) * 16 + j));
+      return *reinterpret_cast<const u32x4*>(st + 1024 * (c >> 2) + 16 * ((c & 3) * 16 + jj));
     };
     Unit<FMT_Q4K> u;
     u.hdr = chunk(0);
@@ -125,103 +190,217 @@ struct LdsUnit<FMT_Q4K> {
   }
 };
 
-// Per-workgroup routing. On return (uniform across the block): slot's expert,
-// first position and count, the active-expert count, and the slot's token list
-// in LDS. Returns false for an inactive slot.
-__device__ bool dec_route(const DecRoute& R, int slot, int publish, const DecTables& T, int* s_ids,
-                          float* s_r, int* s_cnt, int* s_tok, int* s_info) {
-  const int tid = threadIdx.x, nthr = blockDim.x;
+// Token operands: lane (token column j, K group jA) reads row ``row`` of the
+// BF16 matrix [rows, k] at columns kb*256 + xoff(f, jA); xoff splits into a
+// lane part xoff(0, jA) and a fragment part xoff(f, 0) in both formats.
+template <int FMT, bool kFullK>
+struct XStream {
+  rsrc_t r;
+  int v_row, k, lane_col;
+  __device__ __forceinline__ XStream(const uint16_t* x, int nrows, int k_, int row, int lane) {
+    k = k_;
+    r = make_rsrc(x, (uint32_t)nrows * (uint32_t)k * 2u);
+    lane_col = Unit<FMT>::xoff(0, lane >> 4);
+    v_row = (int)opaque(2 * (row * k + lane_col));
+  }
+  __device__ __forceinline__ void load(u32x4 (&xb)[8], int kb) const {
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      const int fo = Unit<FMT>::xoff(f, 0);
+      if (kFullK) {
+        xb[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, v_row, kb * 2 * kQK + 2 * fo, 0));
+      } else {
+        int vo = v_row + 2 * fo;
+        if (kb * kQK + lane_col + fo + 8 > k) vo = v_row - 2 * lane_col;  // in bounds; zeroed at use
+        xb[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, kb * 2 * kQK, 0));
+      }
+    }
+  }
+  __device__ __forceinline__ void mask(u32x4 (&xb)[8], int kb) const {
+    if (!kFullK) {
+#pragma unroll
+      for (int f = 0; f < 8; ++f)
+        if (kb * kQK + lane_col + Unit<FMT>::xoff(f, 0) + 8 > k) xb[f] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+};
+
+// Streams P units per K block over kbs K blocks through the wave's ring:
+// unit (kb, p) is DMA'd by issue_w(p, kb, stage) and multiplied into acc[p].
+// The token operands of K block kb are loaded with unit (kb, 0), one K block
+// ahead of their use, into the register set of kb's parity. The steady-state
+// loop issues unconditionally so that the compiler's own wait counts for the
+// token operands stay exact across the back edge.
+template <int FMT, bool kFullK, int P, typename IssueW>
+__device__ __forceinline__ void stream_units(uint8_t* ring, int kbs, const XStream<FMT, kFullK>& xs,
+                                             IssueW&& issue_w, f32x4 (&acc)[P]) {
+  static_assert(kStages == 3 && P >= kStages - 1, "one K block of token operands in flight");
+  const int lane = threadIdx.x;
+  u32x4 xA[8], xB[8];
+  auto stage = [&](int u) { return ring + (u % kStages) * kUnitBytes; };
+  auto compute = [&](auto pc, int u, u32x4(&xc)[8]) {
+    constexpr int p = decltype(pc)::value;
+    if constexpr (p == 0) xs.mask(xc, u / P);
+    u32x4 a[8];
+    WStream<FMT>::decode(stage(u), lane, a);
+#pragma unroll
+    for (int f = 0; f < 8; ++f) acc[p] = mfma16(a[f], xc[f], acc[p]);
+  };
+  // K block kb when K block kb+1 exists: every unit issues the one 2 ahead.
+  auto steady = [&](int kb, u32x4(&xc)[8], u32x4(&xo)[8]) {
+    static_for<0, P>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      constexpr int pv = (p + 2) % P, dkb = (p + 2) / P;
+      const int u = kb * P + p;
+      issue_w(pv, kb + dkb, stage(u + 2));
+      if constexpr (pv == 0) xs.load(xo, kb + 1);
+      wait_vm<younger_ops<P>(p, 2)>();
+      compute(pc, u, xc);
+    });
+  };
+  // The last K block: only units inside it remain to be issued.
+  auto last = [&](int kb, u32x4(&xc)[8]) {
+    static_for<0, P>([&](auto pc) {
+      constexpr int p = decltype(pc)::value;
+      constexpr int ahead = P - 1 - p < 2 ? P - 1 - p : 2;
+      const int u = kb * P + p;
+      if constexpr (p + 2 < P) issue_w(p + 2, kb, stage(u + 2));
+      wait_vm<younger_ops<P>(p, ahead)>();
+      compute(pc, u, xc);
+    });
+  };
+  issue_w(0, 0, stage(0));
+  xs.load(xA, 0);
+  issue_w(1, 0, stage(1));  // P >= 2: unit (0, 1)
+  int kb = 0;
+  for (; kb + 2 < kbs; kb += 2) {
+    steady(kb, xA, xB);
+    steady(kb + 1, xB, xA);
+  }
+  if (kb + 1 < kbs) {
+    steady(kb, xA, xB);
+    last(kb + 1, xB);
+  } else {
+    last(kb, xA);
+  }
+}
+
+// Wave-level routing. Fills ``tok`` with the slot's tokens (ascending) and
+// returns the slot's expert, first route position and route count; returns
+// false for an inactive slot. ``publish`` also writes the slot's route tables,
+// and slot 0 the per-slot and per-token tables.
+struct SlotRoute {
+  int expert, t0, cnt;
+};
+
+__device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTables& T, uint8_t* scratch,
+                          int* tok, SlotRoute& out) {
+  const int lane = threadIdx.x;
   const int n = R.B * R.K;
-  for (int e = tid; e < R.E; e += nthr) s_cnt[e] = 0;
-  for (int i = tid; i < n; i += nthr) s_ids[i] = R.ids[i];
+  int* s_ids = reinterpret_cast<int*>(scratch);
+  float* s_r = reinterpret_cast<float*>(scratch + 4 * kDecMaxEntries);
+  int* s_cnt = reinterpret_cast<int*>(scratch + 8 * kDecMaxEntries);
+#pragma unroll
+  for (int q = 0; q < kDecMaxExperts / 64; ++q) s_cnt[q * 64 + lane] = 0;
+  for (int i = lane; i < n; i += 64) {
+    s_ids[i] = R.ids[i];
+    s_r[i] = bf16_to_float(R.wts[i]);
+  }
   __syncthreads();
-  for (int i = tid; i < n; i += nthr) {
-    const int b = i / R.K, kk = i - b * R.K;
-    const int id = s_ids[i];
-    bool first = id >= 0 && id < R.E;
-    for (int k2 = 0; k2 < kk && first; ++k2) first = s_ids[b * R.K + k2] != id;
+  // merged weight at the first occurrence of each id in a token; 0 elsewhere.
+  // A chunk's sums read entries at or after their own position only, which
+  // still hold raw weights when the chunk's results are written.
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const int i = i0 + lane;
     float r = 0.f;
-    if (first) {
-      float s = 0.f;
-      for (int k2 = kk; k2 < R.K; ++k2)
-        if (s_ids[b * R.K + k2] == id) s += bf16_to_float(R.wts[b * R.K + k2]);
-      r = bf16_round(s);
+    int id = -1;
+    if (i < n) {
+      const int b = i / R.K, kk = i - b * R.K;
+      id = s_ids[i];
+      bool first = id >= 0 && id < R.E;
+      for (int k2 = 0; k2 < kk && first; ++k2) first = s_ids[b * R.K + k2] != id;
+      if (first) {
+        float s = 0.f;
+        for (int k2 = kk; k2 < R.K; ++k2)
+          if (s_ids[b * R.K + k2] == id) s += s_r[b * R.K + k2];
+        r = bf16_round(s);
+        r = r != 0.f ? r : 0.f;
+      }
+    }
+    __syncthreads();
+    if (i < n) {
+      s_r[i] = r;
       if (r != 0.f) atomicAdd(&s_cnt[id], 1);
-      else r = 0.f;
     }
-    s_r[i] = r;
+    __syncthreads();
   }
-  __syncthreads();
-  if (tid < 64) {
-    // wave 0: exclusive scans over experts (4 per lane) of active flags and counts
-    const int lane = tid;
-    int act[4], cnt[4];
-    int la = 0, lc = 0;
+  // exclusive scans over experts (4 per lane) of active flags and counts
+  int act[4], cnt[4], la = 0, lc = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = lane * 4 + q;
-      cnt[q] = e < R.E ? s_cnt[e] : 0;
-      act[q] = cnt[q] > 0;
-      la += act[q];
-      lc += cnt[q];
+  for (int q = 0; q < 4; ++q) {
+    cnt[q] = s_cnt[lane * 4 + q];
+    act[q] = cnt[q] > 0;
+    la += act[q];
+    lc += cnt[q];
+  }
+  int ia = la, ic = lc;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int ta = __shfl_up(ia, off), tc = __shfl_up(ic, off);
+    if (lane >= off) {
+      ia += ta;
+      ic += tc;
     }
-    int ia = la, ic = lc;  // inclusive scans across lanes
+  }
+  const int total = __builtin_amdgcn_readfirstlane(__shfl(ia, 63));
+  const int routes = __builtin_amdgcn_readfirstlane(__shfl(ic, 63));
+  const bool tables = publish && slot == 0;
+  int ea = ia - la, ec = ic - lc;
+  int my_e = -1, my_t0 = 0, my_c = 0;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int ta = __shfl_up(ia, off), tc = __shfl_up(ic, off);
-      if (lane >= off) {
-        ia += ta;
-        ic += tc;
+  for (int q = 0; q < 4; ++q) {
+    if (act[q]) {
+      if (ea == slot) {
+        my_e = lane * 4 + q;
+        my_t0 = ec;
+        my_c = cnt[q];
+      }
+      if (tables) {
+        T.slot_e[ea] = lane * 4 + q;
+        T.slot_t0[ea] = ec;
+        T.slot_cnt[ea] = cnt[q];
       }
     }
-    int ea = ia - la, ec = ic - lc;
-    const int total_active = __shfl(ia, 63);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (act[q]) {
-        if (ea == slot) {
-          s_info[0] = lane * 4 + q;
-          s_info[1] = ec;
-          s_info[2] = cnt[q];
-        }
-        if (publish) {
-          T.slot_e[ea] = lane * 4 + q;
-          T.slot_t0[ea] = ec;
-          T.slot_cnt[ea] = cnt[q];
-        }
-      }
-      ea += act[q];
-      ec += cnt[q];
-    }
-    if (lane == 0) s_info[3] = total_active;
-    if (publish && lane == 0) T.hdr[0] = total_active;
+    ea += act[q];
+    ec += cnt[q];
   }
-  if (publish && slot == 0) {
-    // one workgroup publishes each token's route count
-    for (int b = tid; b < R.B; b += nthr) {
+  if (tables) {
+    if (lane == 0) {
+      T.hdr[0] = total;
+      T.hdr[1] = routes;
+    }
+    for (int b = lane; b < R.B; b += 64) {
       int m = 0;
       for (int kk = 0; kk < R.K; ++kk) m += s_r[b * R.K + kk] != 0.f;
       T.tok_n[b] = m;
     }
   }
-  __syncthreads();
-  const int total_active = s_info[3];
-  if (slot >= total_active) return false;
-  const int e = s_info[0], t0 = s_info[1];
-  if (tid < 64) {
-    // wave 0: this expert's routes in ascending entry (= token) order
+  bool live = slot < total;
+  if (live) {
+    const unsigned long long own = __ballot(my_e >= 0);
+    const int src = __ffsll((long long)own) - 1;
+    const int e = __shfl(my_e, src), t0 = __shfl(my_t0, src), c = __shfl(my_c, src);
     int run = 0;
     for (int c0 = 0; c0 < n; c0 += 64) {
-      const int i = c0 + tid;
+      const int i = c0 + lane;
       const bool hit = i < n && s_ids[i] == e && s_r[i] != 0.f;
       const unsigned long long m = __ballot(hit);
       if (hit) {
-        const int rank = run + __popcll(m & ((1ull << tid) - 1ull));
+        const int rank = run + __popcll(m & ((1ull << lane) - 1ull));
         const int b = i / R.K;
-        s_tok[rank] = b;
+        tok[rank] = b;
         if (publish) {
-          // rank of this route among its token's routes = routed experts with a smaller id
-          int er = 0;
+          int er = 0;  // routed experts of this token with a smaller id
           for (int kk = 0; kk < R.K; ++kk) {
             const int o = b * R.K + kk;
             er += (s_r[o] != 0.f) && s_ids[o] < e;
@@ -232,133 +411,44 @@ __device__ bool dec_route(const DecRoute& R, int slot, int publish, const DecTab
       }
       run += __popcll(m);
     }
+    out = SlotRoute{__builtin_amdgcn_readfirstlane(e), __builtin_amdgcn_readfirstlane(t0),
+                    __builtin_amdgcn_readfirstlane(c)};
   }
+  // Stores must not count against the ring's wait counts; the ring overlays
+  // this scratch, so its reads finish first as well.
+  wait_vm<0>();
   __syncthreads();
-  return true;
-}
-
-// Copy ``rows`` activation rows (row r -> src_row(r)) of width k into LDS.
-template <typename RowFn>
-__device__ __forceinline__ void stage_rows(uint16_t* xs, int rows, int k, RowFn src_row) {
-  const int per_row = k / 8;
-  for (int i = threadIdx.x; i < rows * per_row; i += blockDim.x) {
-    const int r = i / per_row, c = (i - r * per_row) * 8;
-    *reinterpret_cast<u32x4*>(xs + r * k + c) = *reinterpret_cast<const u32x4*>(src_row(r) + c);
-  }
-}
-
-// 8 x operands of K block kb for token row ``xr`` (LDS), zero past k.
-template <int FMT, bool kFullK>
-__device__ __forceinline__ void lds_x(u32x4 xf[8], const uint16_t* xr, int kb, int jA, int k) {
-#pragma unroll
-  for (int f = 0; f < 8; ++f) {
-    const int col = kb * kQK + Unit<FMT>::xoff(f, jA);
-    xf[f] = (kFullK || col + 8 <= k) ? *reinterpret_cast<const u32x4*>(xr + col) : u32x4{0u, 0u, 0u, 0u};
-  }
-}
-
-// The shared memory of one decode workgroup: [token list | x stage | rings].
-// The routing scratch overlays the rings (it is dead before the first DMA).
-struct DecLds {
-  int* tok;
-  uint16_t* xs;
-  uint8_t* ring;
-  int* s_ids;
-  float* s_r;
-  int* s_cnt;
-  int* info;
-};
-
-__device__ __forceinline__ DecLds carve(uint8_t* base, int xt, int k) {
-  DecLds L;
-  L.info = reinterpret_cast<int*>(base);
-  L.tok = reinterpret_cast<int*>(base + 64);
-  L.xs = reinterpret_cast<uint16_t*>(base + 64 + 4 * kDecMaxTokens);
-  L.ring = base + 64 + 4 * kDecMaxTokens + 2 * xt * k;
-  L.s_ids = reinterpret_cast<int*>(L.ring);
-  L.s_r = reinterpret_cast<float*>(L.ring + 4 * kDecMaxEntries);
-  L.s_cnt = reinterpret_cast<int*>(L.ring + 8 * kDecMaxEntries);
-  return L;
-}
-
-size_t dec_lds_bytes(int xt, int k) {
-  return 64 + 4 * kDecMaxTokens + 2 * (size_t)xt * k + (size_t)kDecWaves * kStages * kStageBytes;
-}
-
-// Token rows staged per pass so that one workgroup stays within both the
-// budget (four workgroups per CU) and the device's per-workgroup LDS limit.
-int dec_x_tokens(int k, int max_lds) {
-  const int64_t fixed = 64 + 4 * kDecMaxTokens + (int64_t)kDecWaves * kStages * kStageBytes;
-  const int64_t budget = max_lds < kLdsBudget ? max_lds : kLdsBudget;
-  int64_t xt = (budget - fixed) / (2 * (int64_t)k);
-  return (int)(xt > 16 ? 16 : xt);
-}
-
-static int device_max_lds() {
-  int dev = 0, v = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 65536;
-  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) return 65536;
-  return v;
+  return live;
 }
 
 template <int FMT, bool kFullK>
-__global__ void __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
     moe_dec_gate_up_kernel(Proj gate, Proj up, DecRoute R, DecTables T, const uint16_t* __restrict__ x,
-                           int hidden, uint16_t* __restrict__ act, int inter, int xt) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const DecLds L = carve(smem, xt, hidden);
-  const int slot = blockIdx.x;
-  const int publish = blockIdx.y == 0;
-  if (!dec_route(R, slot, publish, T, L.s_ids, L.s_r, L.s_cnt, L.tok, L.info)) return;
-  const int64_t e = L.info[0];
-  const int t0 = L.info[1], cnt = L.info[2];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int jA = lane >> 4, j = lane & 15;
-  const int rg = blockIdx.y * kDecWaves + wave;
-  const bool live = rg * 16 < inter;
-  uint8_t* ring = L.ring + wave * kStages * kStageBytes;
-  const int kbs = gate.kb;
-  const int nu = 2 * kbs;  // units: gate kb, up kb, gate kb+1, ...
-  for (int tc = 0; tc < cnt; tc += xt) {
-    const int nt = cnt - tc < xt ? cnt - tc : xt;
-    __syncthreads();  // previous chunk's readers are done with the x stage
-    stage_rows(L.xs, nt, hidden, [&](int r) { return x + (int64_t)L.tok[tc + r] * hidden; });
-    __syncthreads();
-    if (live) {
-      const uint16_t* xr = L.xs + (j < nt ? j : 0) * hidden;
-      f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-      auto issue = [&](int u) {
-        LdsUnit<FMT>::issue((u & 1) ? up : gate, e, rg, u >> 1, lane, ring + (u % kStages) * kStageBytes);
-      };
-      for (int u = 0; u < kStages - 1 && u < nu; ++u) issue(u);
-      u32x4 xf[8];
-      for (int u = 0; u < nu; ++u) {
-        if (u + kStages - 1 < nu) issue(u + kStages - 1);
-        const int ahead = nu - 1 - u;
-        wait_units(ahead < kStages - 1 ? ahead : kStages - 1);
-        if (!(u & 1)) lds_x<FMT, kFullK>(xf, xr, u >> 1, jA, hidden);
-        u32x4 a[8];
-        LdsUnit<FMT>::decode(ring + (u % kStages) * kStageBytes, lane, a);
-        if (u & 1) {
+                           int hidden, uint16_t* __restrict__ act, int inter) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kUnitBytes];
+  __shared__ int tok[kDecMaxTokens];
+  const int rg = blockIdx.x, slot = blockIdx.y;
+  const int lane = threadIdx.x, jA = lane >> 4, j = lane & 15;
+  SlotRoute sr;
+  if (!dec_route(R, slot, rg == 0, T, ring, tok, sr)) return;
+  const WStream<FMT> wg(gate, sr.expert, lane), wu(up, sr.expert, lane);
+  for (int tc = 0; tc < sr.cnt; tc += kPassTokens) {
+    const int nt = sr.cnt - tc < kPassTokens ? sr.cnt - tc : kPassTokens;
+    if (tc) wait_vm<0>();  // the previous pass's stores
+    const XStream<FMT, kFullK> xs(x, R.B, hidden, tok[tc + (j < nt ? j : nt - 1)], lane);
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    stream_units<FMT, kFullK, 2>(
+        ring, gate.kb, xs, [&](int p, int kb, uint8_t* st) { (p ? wu : wg).issue(rg, kb, st); }, acc);
+    // lane holds rows 4*(lane/16)+q, token column lane%16 of both accumulators
+    if (j < nt) {
 #pragma unroll
-          for (int f = 0; f < 8; ++f) au = mfma16(a[f], xf[f], au);
-        } else {
-#pragma unroll
-          for (int f = 0; f < 8; ++f) ag = mfma16(a[f], xf[f], ag);
-        }
-      }
-      // lane holds rows 4*(lane/16)+i, token column lane%16 of both accumulators
-      if (j < nt) {
-        const int q = tc + j;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = rg * 16 + 4 * jA + i;
-          if (row < inter) {
-            const float g = bf16_round(ag[i]);
-            const float uu = bf16_round(au[i]);
-            const float sg = bf16_round(g * sigmoid_acc(g));
-            act[(int64_t)(t0 + q) * inter + row] = bf16_bits(sg * uu);
-          }
+      for (int q = 0; q < 4; ++q) {
+        const int row = rg * 16 + 4 * jA + q;
+        if (row < inter) {
+          const float g = bf16_round(acc[0][q]);
+          const float uu = bf16_round(acc[1][q]);
+          const float sg = bf16_round(g * sigmoid_acc(g));
+          act[(int64_t)(sr.t0 + tc + j) * inter + row] = bf16_bits(sg * uu);
         }
       }
     }
@@ -366,58 +456,46 @@ __global__ void __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_pe
 }
 
 template <int FMT, bool kFullK>
-__global__ void __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
     moe_dec_down_kernel(Proj down, DecTables T, const uint16_t* __restrict__ act, int inter,
-                        float* __restrict__ contrib, int hidden, int xt) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const DecLds L = carve(smem, xt, inter);
-  const int slot = blockIdx.x;
-  const int n_active = T.hdr[0];
-  if (slot >= n_active) return;
-  const int64_t e = T.slot_e[slot];
+                        float* __restrict__ contrib, int hidden) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kUnitBytes];
+  const int slot = blockIdx.y;
+  if (slot >= T.hdr[0]) return;
   const int t0 = T.slot_t0[slot], cnt = T.slot_cnt[slot];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int jA = lane >> 4, j = lane & 15;
-  const int rg = blockIdx.y * kDecWaves + wave;
-  const bool live = rg * 16 < hidden;
-  uint8_t* ring = L.ring + wave * kStages * kStageBytes;
-  const int kbs = down.kb;
-  for (int tc = 0; tc < cnt; tc += xt) {
-    const int nt = cnt - tc < xt ? cnt - tc : xt;
-    __syncthreads();
-    stage_rows(L.xs, nt, inter, [&](int r) { return act + (int64_t)(t0 + tc + r) * inter; });
-    __syncthreads();
-    if (live) {
-      const uint16_t* xr = L.xs + (j < nt ? j : 0) * inter;
-      const int pos = t0 + tc + (j < nt ? j : 0);
-      const int dst = T.route_dst[pos];
-      const float w = T.route_w[pos];
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      auto issue = [&](int u) {
-        LdsUnit<FMT>::issue(down, e, rg, u, lane, ring + (u % kStages) * kStageBytes);
-      };
-      for (int u = 0; u < kStages - 1 && u < kbs; ++u) issue(u);
-      for (int u = 0; u < kbs; ++u) {
-        if (u + kStages - 1 < kbs) issue(u + kStages - 1);
-        const int ahead = kbs - 1 - u;
-        wait_units(ahead < kStages - 1 ? ahead : kStages - 1);
-        u32x4 xf[8];
-        lds_x<FMT, kFullK>(xf, xr, u, jA, inter);
-        u32x4 a[8];
-        LdsUnit<FMT>::decode(ring + (u % kStages) * kStageBytes, lane, a);
+  const int lane = threadIdx.x, jA = lane >> 4, j = lane & 15;
+  const WStream<FMT> wd(down, T.slot_e[slot], lane);
+  const int groups = (hidden + 15) / 16;
+  const int rg0 = blockIdx.x * kDownRows;
+  for (int tc = 0; tc < cnt; tc += kPassTokens) {
+    const int nt = cnt - tc < kPassTokens ? cnt - tc : kPassTokens;
+    if (tc) wait_vm<0>();
+    const int pos = t0 + tc + (j < nt ? j : nt - 1);
+    const int dst = T.route_dst[pos];
+    const float w = T.route_w[pos];
+    f32x4 acc[kDownRows];
 #pragma unroll
-        for (int f = 0; f < 8; ++f) acc = mfma16(a[f], xf[f], acc);
-      }
-      if (j < nt) {
+    for (int r = 0; r < kDownRows; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const XStream<FMT, kFullK> xs(act, T.hdr[1], inter, pos, lane);
+    stream_units<FMT, kFullK, kDownRows>(
+        ring, down.kb, xs,
+        [&](int p, int kb, uint8_t* st) {
+          const int rg = rg0 + p < groups ? rg0 + p : groups - 1;  // clamped rows are discarded
+          wd.issue(rg, kb, st);
+        },
+        acc);
+    if (j < nt) {
+#pragma unroll
+      for (int r = 0; r < kDownRows; ++r) {
+        const int row = (rg0 + r) * 16 + 4 * jA;
         f32x4 c;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) c[i] = bf16_round(acc[i]) * w;  // exact product
-        const int row = rg * 16 + 4 * jA;
+        for (int q = 0; q < 4; ++q) c[q] = bf16_round(acc[r][q]) * w;  // exact product
         if (row + 4 <= hidden) {
           *reinterpret_cast<f32x4*>(contrib + (int64_t)dst * hidden + row) = c;
         } else {
-          for (int i = 0; i < 4; ++i)
-            if (row + i < hidden) contrib[(int64_t)dst * hidden + row + i] = c[i];
+          for (int q = 0; q < 4; ++q)
+            if (row + q < hidden) contrib[(int64_t)dst * hidden + row + q] = c[q];
         }
       }
     }
@@ -426,65 +504,57 @@ __global__ void __launch_bounds__(64 * kDecWaves) __attribute__((amdgpu_waves_pe
 
 // out[b, h] = RNE(sum_r contrib[b, r, h]) over the token's routes in rank
 // (= ascending expert id) order; with a shared expert RNE(f32(routed) + shared).
-__global__ void __launch_bounds__(256)
+// One lane per 4 hidden columns; the rank rows are loaded 8 at a time before
+// they are summed in order.
+__global__ void __launch_bounds__(64)
     moe_dec_combine_kernel(DecTables T, const float* __restrict__ contrib, int hidden, int K,
                            const uint16_t* __restrict__ sh_y, const uint16_t* __restrict__ sh_scale,
                            uint16_t* __restrict__ out) {
   const int b = blockIdx.x;
-  const int h = (blockIdx.y * blockDim.x + threadIdx.x) * 8;
+  const int h = (blockIdx.y * 64 + threadIdx.x) * 4;
   if (h >= hidden) return;
   const int m = T.tok_n[b];
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const float* base = contrib + (int64_t)b * K * hidden + h;
-  for (int r = 0; r < m; ++r) {
-    const f32x4 v0 = *reinterpret_cast<const f32x4*>(base + (int64_t)r * hidden);
-    const f32x4 v1 = *reinterpret_cast<const f32x4*>(base + (int64_t)r * hidden + 4);
+  for (int r0 = 0; r0 < m; r0 += 8) {
+    f32x4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (r0 + i < m) v[i] = *reinterpret_cast<const f32x4*>(base + (int64_t)(r0 + i) * hidden);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (r0 + i < m) acc += v[i];
+  }
+  u32x2 o;
+  if (sh_y) {
+    const u32x2 sv = *reinterpret_cast<const u32x2*>(sh_y + (int64_t)b * hidden + h);
+    const float gs = sh_scale ? bf16_to_float(sh_scale[b]) : 1.f;
+    float v[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      acc[c] += v0[c];
-      acc[4 + c] += v1[c];
-    }
-  }
-  u32x4 o;
-  if (sh_y) {
-    const u32x4 sv = *reinterpret_cast<const u32x4*>(sh_y + (int64_t)b * hidden + h);
-    const float gs = sh_scale ? bf16_to_float(sh_scale[b]) : 1.f;
-    float v[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
       float sy = bf16_to_float((uint16_t)(sv[c >> 1] >> (16 * (c & 1))));
       if (sh_scale) sy = bf16_round(sy * gs);
       v[c] = bf16_round(acc[c]) + sy;
     }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) o[c] = pack_bf16x2(v[2 * c], v[2 * c + 1]);
+    o[0] = pack_bf16x2(v[0], v[1]);
+    o[1] = pack_bf16x2(v[2], v[3]);
   } else {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) o[c] = pack_bf16x2(acc[2 * c], acc[2 * c + 1]);
+    o[0] = pack_bf16x2(acc[0], acc[1]);
+    o[1] = pack_bf16x2(acc[2], acc[3]);
   }
-  *reinterpret_cast<u32x4*>(out + (int64_t)b * hidden + h) = o;
+  *reinterpret_cast<u32x2*>(out + (int64_t)b * hidden + h) = o;
 }
 
 template <int FMT, bool kFullK>
 static int launch(const DecArgs& A, hipStream_t s) {
-  const int max_lds = device_max_lds();
-  const int xt1 = dec_x_tokens(A.H, max_lds), xt2 = dec_x_tokens(A.I, max_lds);
-  if (xt1 < 1 || xt2 < 1) {
-    set_error("moe_forward: hidden/intermediate too wide for the decode kernels' LDS stage");
-    return Q6MOE_ERR_UNSUPPORTED;
-  }
-  const size_t lds1 = dec_lds_bytes(xt1, A.H), lds2 = dec_lds_bytes(xt2, A.I);
-  hipFuncSetAttribute((const void*)moe_dec_gate_up_kernel<FMT, kFullK>,
-                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds1);
-  hipFuncSetAttribute((const void*)moe_dec_down_kernel<FMT, kFullK>,
-                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
-  hipLaunchKernelGGL((moe_dec_gate_up_kernel<FMT, kFullK>),
-                     dim3(A.max_slots, (unsigned)cdiv(A.I, 16 * kDecWaves)), dim3(64 * kDecWaves), lds1, s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I, xt1);
+  const int groups_i = (int)cdiv(A.I, 16), groups_h = (int)cdiv(A.H, 16);
+  hipLaunchKernelGGL((moe_dec_gate_up_kernel<FMT, kFullK>), dim3((unsigned)groups_i, A.max_slots), dim3(64), 0,
+                     s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I);
   if (A.after_gate_up) hipEventRecord((hipEvent_t)A.after_gate_up, s);
-  hipLaunchKernelGGL((moe_dec_down_kernel<FMT, kFullK>),
-                     dim3(A.max_slots, (unsigned)cdiv(A.H, 16 * kDecWaves)), dim3(64 * kDecWaves), lds2, s, A.down, A.T, A.act, A.I, A.contrib, A.H, xt2);
+  hipLaunchKernelGGL((moe_dec_down_kernel<FMT, kFullK>), dim3((unsigned)cdiv(groups_h, kDownRows), A.max_slots),
+                     dim3(64), 0, s, A.down, A.T, A.act, A.I, A.contrib, A.H);
   if (A.after_down) hipEventRecord((hipEvent_t)A.after_down, s);
-  hipLaunchKernelGGL(moe_dec_combine_kernel, dim3(A.R.B, (unsigned)cdiv(A.H, 256 * 8)), dim3(256), 0, s, A.T,
+  hipLaunchKernelGGL(moe_dec_combine_kernel, dim3(A.R.B, (unsigned)cdiv(A.H, 256)), dim3(64), 0, s, A.T,
                      A.contrib, A.H, A.R.K, A.sh_y, A.sh_scale, A.out);
   return Q6MOE_OK;
 }
