@@ -20,122 +20,148 @@
 
 namespace q6moe {
 
-constexpr int kRouteThreads = 1024;
 constexpr int kRouteMaxExperts = 256;
-constexpr int kRouteChunk = 512;  // tokens per bitmap pass
-constexpr int kRouteWords = kRouteChunk / 32;
+constexpr int kChunk = 256;  // tokens per routing workgroup
+constexpr int kChunkWords = kChunk / 32;
 
-__global__ void __launch_bounds__(kRouteThreads)
-    moe_route_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B, int K,
-                     int E, int mtile, MoeWs ws) {
+__device__ __forceinline__ bool is_route(float r) { return r != 0.f || r != r; }
+
+// Routing, pass 1 (one workgroup per chunk of kChunk tokens, one lane per
+// token): merged BF16 weight of each first occurrence of an id in a token
+// (experts.py:66-73; 0 for repeats and out-of-range ids) and the chunk's
+// route count per expert.
+__global__ void __launch_bounds__(kChunk)
+    moe_route_count_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B, int K,
+                           int E, MoeWs ws, int* __restrict__ chunk_cnt) {
+  extern __shared__ int sm[];
+  int* s_ids = sm;                                  // [kChunk * K]
+  float* s_w = reinterpret_cast<float*>(sm + kChunk * K);
   __shared__ int cnt[kRouteMaxExperts];
-  __shared__ int base[kRouteMaxExperts];
-  __shared__ int run[kRouteMaxExperts];
-  __shared__ uint32_t bits[kRouteMaxExperts][kRouteWords];
-  __shared__ int wpre[kRouteMaxExperts][kRouteWords + 1];
-  const int tid = threadIdx.x;
-  const int n = B * K;
-  for (int e = tid; e < E; e += kRouteThreads) {
-    cnt[e] = 0;
-    run[e] = 0;
+  const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
+  const int nb = B - b0 < kChunk ? B - b0 : kChunk;
+  for (int e = tid; e < E; e += kChunk) cnt[e] = 0;
+  for (int i = tid; i < nb * K; i += kChunk) {
+    s_ids[i] = ids[(int64_t)b0 * K + i];
+    s_w[i] = bf16_to_float(wts[(int64_t)b0 * K + i]);
   }
   __syncthreads();
-  // Pass 1: merged route weight of each first occurrence of an id in a token.
-  for (int i = tid; i < n; i += kRouteThreads) {
-    const int b = i / K, kk = i % K;
-    const int id = ids[i];
-    float r = 0.f;
-    bool first = id >= 0 && id < E;
-    for (int k2 = 0; k2 < kk && first; ++k2) first = ids[b * K + k2] != id;
-    if (first) {
-      float s = 0.f;
-      for (int k2 = kk; k2 < K; ++k2)
-        if (ids[b * K + k2] == id) s += bf16_to_float(wts[b * K + k2]);
-      r = bf16_round(s);
-      if (r != 0.f || r != r) atomicAdd(&cnt[id], 1);
-      else r = 0.f;
+  if (tid < nb) {
+    const int* id = s_ids + tid * K;
+    const float* w = s_w + tid * K;
+    for (int kk = 0; kk < K; ++kk) {
+      const int e = id[kk];
+      bool first = e >= 0 && e < E;
+      for (int k2 = 0; k2 < kk && first; ++k2) first = id[k2] != e;
+      float r = 0.f;
+      if (first) {
+        float sum = 0.f;
+        for (int k2 = kk; k2 < K; ++k2)
+          if (id[k2] == e) sum += w[k2];
+        r = bf16_round(sum);
+        if (is_route(r)) atomicAdd(&cnt[e], 1);
+      }
+      ws.ent_r[(int64_t)(b0 + tid) * K + kk] = is_route(r) ? r : 0.f;
     }
-    ws.ent_r[i] = (r != 0.f || r != r) ? r : 0.f;
-    ws.ent_pos[i] = -1;
   }
   __syncthreads();
-  if (tid == 0) {
-    int s = 0, a = 0, tl = 0;
-    for (int e = 0; e < E; ++e) {
-      base[e] = s;
-      const int c = cnt[e];
-      if (c > 0) {
-        ws.active[a] = e;
-        ws.act_off[a] = s;
-        ws.tile_off[a] = tl;
-        const int nt = (c + mtile - 1) / mtile;
-        for (int j = 0; j < nt; ++j) ws.tile_slot[tl + j] = a;
-        tl += nt;
-        s += c;
-        ++a;
-      }
+  for (int e = tid; e < E; e += kChunk) chunk_cnt[(int64_t)blockIdx.x * E + e] = cnt[e];
+}
+
+// Routing, pass 2 (one workgroup, one lane per expert): active experts in
+// ascending id (experts.py:74-76), each expert's first route position, the
+// 128-route prefill tiles, and each chunk's first position per expert
+// (chunk_cnt is rewritten in place as absolute positions).
+__global__ void __launch_bounds__(kRouteMaxExperts)
+    moe_route_scan_kernel(int E, int nchunks, int mtile, MoeWs ws, int* __restrict__ chunk_cnt) {
+  __shared__ int s_a[kRouteMaxExperts], s_c[kRouteMaxExperts], s_t[kRouteMaxExperts];
+  const int e = threadIdx.x;
+  int total = 0;
+  if (e < E) {
+    for (int c = 0; c < nchunks; ++c) {
+      const int v = chunk_cnt[(int64_t)c * E + e];
+      chunk_cnt[(int64_t)c * E + e] = total;
+      total += v;
     }
-    ws.act_off[a] = s;
-    ws.tile_off[a] = tl;
-    ws.hdr[0] = a;
-    ws.hdr[1] = s;
-    ws.hdr[2] = tl;
   }
+  const int act = total > 0, nt = (total + mtile - 1) / mtile;
+  s_a[e] = act;
+  s_c[e] = total;
+  s_t[e] = nt;
   __syncthreads();
-  // Pass 2: positions = expert base + rank of the token among that expert's tokens.
-  for (int c0 = 0; c0 < B; c0 += kRouteChunk) {
-    for (int i = tid; i < E * kRouteWords; i += kRouteThreads) bits[i / kRouteWords][i % kRouteWords] = 0u;
+  // inclusive Hillis-Steele scans over the 256 lanes
+  for (int off = 1; off < kRouteMaxExperts; off <<= 1) {
+    const int va = e >= off ? s_a[e - off] : 0, vc = e >= off ? s_c[e - off] : 0, vt = e >= off ? s_t[e - off] : 0;
     __syncthreads();
-    const int lo = c0 * K, hi = min(B, c0 + kRouteChunk) * K;
-    for (int i = lo + tid; i < hi; i += kRouteThreads) {
-      const float r = ws.ent_r[i];
-      if (r != 0.f || r != r) {
-        const int rel = i / K - c0;
-        atomicOr(&bits[ids[i]][rel >> 5], 1u << (rel & 31));
-      }
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += kRouteThreads) {
-      int acc = 0;
-      for (int w = 0; w < kRouteWords; ++w) {
-        wpre[e][w] = acc;
-        acc += __popc(bits[e][w]);
-      }
-      wpre[e][kRouteWords] = acc;
-    }
-    __syncthreads();
-    for (int i = lo + tid; i < hi; i += kRouteThreads) {
-      const float r = ws.ent_r[i];
-      if (r != 0.f || r != r) {
-        const int e = ids[i];
-        const int rel = i / K - c0;
-        const int w = rel >> 5, bit = rel & 31;
-        const int pos = base[e] + run[e] + wpre[e][w] + __popc(bits[e][w] & ((1u << bit) - 1u));
-        ws.route_tok[pos] = i / K;
-        ws.route_w[pos] = r;
-        ws.ent_pos[i] = pos;
-      }
-    }
-    __syncthreads();
-    for (int e = tid; e < E; e += kRouteThreads) run[e] += wpre[e][kRouteWords];
+    s_a[e] += va;
+    s_c[e] += vc;
+    s_t[e] += vt;
     __syncthreads();
   }
-  // Per token: its route positions in ascending expert id. Positions are
-  // expert-major, so sorting them ascending sorts by expert (insertion sort).
-  for (int b = tid; b < B; b += kRouteThreads) {
+  const int slot = s_a[e] - act, base = s_c[e] - total, t0 = s_t[e] - nt;
+  if (e < E) {
+    for (int c = 0; c < nchunks; ++c) chunk_cnt[(int64_t)c * E + e] += base;
+    if (act) {
+      ws.active[slot] = e;
+      ws.act_off[slot] = base;
+      ws.tile_off[slot] = t0;
+      for (int j = 0; j < nt; ++j) ws.tile_slot[t0 + j] = slot;
+    }
+  }
+  if (e == kRouteMaxExperts - 1) {
+    const int na = s_a[e];
+    ws.act_off[na] = s_c[e];
+    ws.tile_off[na] = s_t[e];
+    ws.hdr[0] = na;
+    ws.hdr[1] = s_c[e];
+    ws.hdr[2] = s_t[e];
+  }
+}
+
+// Routing, pass 3 (one workgroup per chunk): a route's position is its
+// chunk's first position for the expert plus the number of earlier tokens of
+// the chunk routed to that expert (per-expert token bitmaps), so routes are
+// grouped by expert with tokens ascending. Per token, its positions in
+// ascending expert id feed the combine.
+__global__ void __launch_bounds__(kChunk)
+    moe_route_scatter_kernel(const int32_t* __restrict__ ids, int B, int K, int E, MoeWs ws,
+                             const int* __restrict__ chunk_pos) {
+  __shared__ uint32_t bits[kRouteMaxExperts][kChunkWords];
+  const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
+  const int nb = B - b0 < kChunk ? B - b0 : kChunk;
+  for (int i = tid; i < E * kChunkWords; i += kChunk) bits[i / kChunkWords][i % kChunkWords] = 0u;
+  __syncthreads();
+  const int b = b0 + tid;
+  if (tid < nb)
+    for (int kk = 0; kk < K; ++kk) {
+      const int64_t i = (int64_t)b * K + kk;
+      if (is_route(ws.ent_r[i])) atomicOr(&bits[ids[i]][tid >> 5], 1u << (tid & 31));
+    }
+  __syncthreads();
+  if (tid < nb) {
     int* tp = ws.tok_pos + (int64_t)b * K;
     int m = 0;
     for (int kk = 0; kk < K; ++kk) {
-      const int pos = ws.ent_pos[b * K + kk];
-      if (pos < 0) continue;
-      int j = m++;
-      while (j > 0 && tp[j - 1] > pos) {
-        tp[j] = tp[j - 1];
-        --j;
+      const int64_t i = (int64_t)b * K + kk;
+      const float r = ws.ent_r[i];
+      int pos = -1;
+      if (is_route(r)) {
+        const int e = ids[i];
+        int rank = __popc(bits[e][tid >> 5] & ((1u << (tid & 31)) - 1u));
+        for (int w = 0; w < (tid >> 5); ++w) rank += __popc(bits[e][w]);
+        pos = chunk_pos[(int64_t)blockIdx.x * E + e] + rank;
+        ws.route_tok[pos] = b;
+        ws.route_w[pos] = r;
+        // positions are expert-major: keep the token's list sorted (insertion)
+        int q = m++;
+        while (q > 0 && tp[q - 1] > pos) {
+          tp[q] = tp[q - 1];
+          --q;
+        }
+        tp[q] = pos;
       }
-      tp[j] = pos;
+      ws.ent_pos[i] = pos;
     }
-    for (int j = m; j < K; ++j) tp[j] = -1;
+    for (int q = m; q < K; ++q) tp[q] = -1;
   }
 }
 
@@ -367,7 +393,7 @@ __global__ void __launch_bounds__(256)
 // ---------------------------------------------------------------------------
 struct WsLayout {
   size_t hdr, active, act_off, tile_off, tile_slot, ent_r, ent_pos, route_tok, route_w, tok_pos, act,
-      y, sh_act, sh_y, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, total;
+      y, sh_act, sh_y, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, chunk_cnt, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -402,6 +428,7 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
   L.tok_n = take(4 * B);
   L.route_dst = take(4 * n);
   L.contrib = take(4 * n * H);
+  L.chunk_cnt = take(4 * cdiv(B, kChunk) * E);
   L.total = o;
   return L;
 }
@@ -487,6 +514,7 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   const int64_t B = a->tokens, K = a->top_k, E = a->experts, H = a->hidden, I = a->intermediate;
   Q6MOE_REQUIRE(B >= 1 && K >= 1 && E >= 1 && H >= 1 && I >= 1, "moe_forward: sizes must be positive");
   Q6MOE_REQUIRE(E <= kRouteMaxExperts, "moe_forward: at most 256 experts per call");
+  Q6MOE_REQUIRE(K <= 32, "moe_forward: top_k must be at most 32");
   Q6MOE_REQUIRE(B * K <= (1 << 28) && H <= (1 << 24) && I <= (1 << 24), "moe_forward: problem too large");
   Q6MOE_REQUIRE(H % 8 == 0 && I % 8 == 0, "moe_forward: hidden and intermediate must be multiples of 8");
   Q6MOE_REQUIRE(aligned(a->x, 16) && aligned(a->out, 16) && aligned(a->workspace, 256),
@@ -584,9 +612,17 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
     return rc;
   }
   mark(0);
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(kRouteThreads), 0, s, a->ids, a->weights, (int)B, (int)K,
-                     (int)E, (int)kPrefillTile, ws);
-  if ((rc = check_launch("moe_route_kernel"))) return rc;
+  {
+    const int nchunks = (int)cdiv(B, kChunk);
+    int* chunk_cnt = reinterpret_cast<int*>(w + L.chunk_cnt);
+    hipLaunchKernelGGL(moe_route_count_kernel, dim3(nchunks), dim3(kChunk), (size_t)kChunk * K * 8, s, a->ids,
+                       a->weights, (int)B, (int)K, (int)E, ws, chunk_cnt);
+    hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3(kRouteMaxExperts), 0, s, (int)E, nchunks,
+                       (int)kPrefillTile, ws, chunk_cnt);
+    hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nchunks), dim3(kChunk), 0, s, a->ids, (int)B, (int)K,
+                       (int)E, ws, chunk_cnt);
+    if ((rc = check_launch("moe routing kernels"))) return rc;
+  }
   mark(1);
 
   TokenSrc routed{0, (int)B, ws.hdr, ws.active, ws.act_off, ws.route_tok};
@@ -594,10 +630,16 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   const Proj g = make_proj(a->gate, (int)I, (int)H), u = make_proj(a->up, (int)I, (int)H),
              d = make_proj(a->down, (int)H, (int)I);
   const int max_tokens = (int)B;  // an expert sees each token at most once
-  if (a->gate.qtype == Q6MOE_Q6_K)
+  // The tiled MFMA path addresses token rows with 32-bit byte offsets.
+  const bool tiled = pf_supported(fmt, H, I) && B * H * 2 < (1ll << 31) && B * K * I * 2 < (1ll << 31);
+  if (tiled) {
+    const int max_tiles = (int)(E + B * K / kPrefillTile + 1);
+    launch_moe_prefill(g, u, d, ws, max_tiles, a->x, (int)H, (int)I, s, a->events ? a->events[2] : nullptr);
+  } else if (a->gate.qtype == Q6MOE_Q6_K) {
     launch_phases<FMT_Q6>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s, mark);
-  else
+  } else {
     launch_phases<FMT_Q4K>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s, mark);
+  }
   if ((rc = check_launch("moe expert kernels"))) return rc;
   if (Is) {
     TokenSrc dense{1, (int)B, nullptr, nullptr, nullptr, nullptr};

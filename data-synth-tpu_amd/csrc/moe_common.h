@@ -79,6 +79,11 @@ struct DecArgs {
 bool dec_supported(int64_t B, int64_t K, int64_t E);
 int launch_moe_decode(int fmt, const DecArgs& A, hipStream_t s);
 
+// Prefill grouped GEMM (Q6_K, hidden and intermediate multiples of 256).
+bool pf_supported(int fmt, int64_t H, int64_t I);
+int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
+                       const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up);
+
 // ---------------------------------------------------------------------------
 // Unit decoders: 16 output rows x one 256-wide K block -> 8 MFMA A operands.
 // ---------------------------------------------------------------------------

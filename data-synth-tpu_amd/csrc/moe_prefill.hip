@@ -1,0 +1,325 @@
+// Prefill-shaped routed experts on Q6_K tables: tiled grouped GEMM on BF16 MFMA.
+//
+// The routing kernel (moe.hip) groups the routes by expert (ascending id,
+// tokens ascending) and splits each expert's routes into tiles of 128. One
+// workgroup computes a 128-route tile against a block of output rows:
+//
+//   moe_pf_gate_up_kernel  128 intermediate rows (gate and up) per workgroup;
+//        g = RNE(x Wg^T), u = RNE(x Wu^T), a = RNE(RNE(g*sigmoid(g))*u)
+//        (kaggle/qwen38_tpu/experts.py:103-107, grouped_experts.py:96-101).
+//   moe_pf_down_kernel     256 hidden rows per workgroup; y = RNE(a Wd^T)
+//        (experts.py:108). The combine kernel in moe.hip sums f32(y)*f32(r).
+//
+// Each of the 4 waves owns 4 units (16 weight rows x one 256-wide K block)
+// per K block and decodes them straight into MFMA A operands; decoded
+// weights never leave registers. The 128 token rows of the current K half
+// sit in LDS (double-buffered, XOR-swizzled so the 16 token columns of an
+// MFMA read hit distinct banks) and every wave multiplies them against its
+// own rows. Both the token half-tiles and the packed weight half-units come
+// in by direct global->LDS DMA, two K halves ahead of their use.
+#include <type_traits>
+
+#include "moe_common.h"
+#include "q6moe_api.h"
+
+#define LDS_PTR(p) ((__attribute__((address_space(3))) void*)(uint32_t)(uintptr_t)(p))
+
+namespace q6moe {
+
+namespace pf {
+
+constexpr int kWaves = 4;
+constexpr int kM = 128;            // routes per tile (MFMA column groups of 16)
+constexpr int kTG = kM / 16;       // token groups
+constexpr int kUnits = 4;          // units per wave per K block
+constexpr int kHalfBytes = kM * 128 * 2;  // one K half of the token tile (32 KB)
+constexpr int kHUnit = 2048;       // packed half-unit in LDS: ql 1024, qh 512, sc 256, d 256
+constexpr int kWStage = kUnits * kHUnit;
+constexpr int kWDma = 4;           // DMA instructions per half-unit
+constexpr int kXDma = kHalfBytes / 1024 / kWaves;  // token DMA instructions per wave per half
+constexpr int kLds = 2 * kHalfBytes + kWaves * 2 * kWStage;
+
+static_assert(kLds <= 160 * 1024, "LDS budget");
+
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ const uint8_t* sgpr_ptr(const uint8_t* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t*)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t voff, void* lds) {
+  __builtin_amdgcn_global_load_lds(sgpr_ptr(base) + voff, LDS_PTR(lds), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t voff, void* lds) {
+  __builtin_amdgcn_global_load_lds(sgpr_ptr(base) + voff, LDS_PTR(lds), 4, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Per-lane offsets of a Q6_K half-unit DMA (lane l: row l%16, chunk l/16).
+struct HalfUnitLane {
+  uint32_t ql, qh, sc, d;
+  __device__ __forceinline__ explicit HalfUnitLane(int lane) {
+    const int j = lane & 15, c = lane >> 4;
+    ql = opaque(kQlOff + j * 128 + 16 * c);
+    qh = opaque(kQhOff + j * 64 + 16 * (c & 1));
+    sc = opaque(kScOff + 4 * lane);
+    d = opaque(4 * (lane & 7));
+  }
+};
+
+// Issue the K half h of row group rg, K block kb of expert table (data, scales)
+// into ``st`` (kHUnit bytes). ql: chunks 4h..4h+3 of each row (slot c*16+j);
+// qh: chunks 2h, 2h+1 (32 lanes); sub-scales and d of the 16 rows.
+__device__ __forceinline__ void issue_half_unit(const uint8_t* data, const uint8_t* scales, int kbs, int rg,
+                                                int kb, int h, const HalfUnitLane& L, int lane, uint8_t* st) {
+  const int64_t t = (int64_t)(rg >> 2) * kbs + kb;
+  const int r0 = (rg & 3) * 16;
+  const uint8_t* tile = data + t * kTileBytes;
+  dma16(tile + r0 * 128 + 64 * h, L.ql, st);
+  if (lane < 32) dma16(tile + r0 * 64 + 32 * h, L.qh, st + 1024);
+  dma4(tile + r0 * 16, L.sc, st + 1536);
+  dma4(scales + t * 128 + r0 * 2, L.d, st + 1792);
+}
+
+// The 4 A fragments of K half h (f = 4h..4h+3) from a half-unit in LDS.
+__device__ __forceinline__ void decode_half(const uint8_t* st, int h, int lane, u32x4 a[4]) {
+  const int j = lane & 15, jA = lane >> 4;
+  const u32x4 ql = *reinterpret_cast<const u32x4*>(st + 16 * (jA * 16 + j));
+  const u32x4 qh = *reinterpret_cast<const u32x4*>(st + 1024 + 16 * ((jA & 1) * 16 + j));
+  const u32x4 sc = *reinterpret_cast<const u32x4*>(st + 1536 + 16 * j);
+  const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(st + 1792 + 2 * j));
+  const int q0 = jA >> 1, sh = 8 * jA;
+#pragma unroll
+  for (int gg = 0; gg < 2; ++gg) {
+    const int g = 2 * h + gg;
+    const int scv = (int)(int8_t)((sc[g] >> sh) & 0xff);
+    const float ds = d * (float)scv;
+    const float nds = -32.f * ds;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t h0 = qh[2 * e] >> (2 * q0), h1 = qh[2 * e + 1] >> (2 * q0);
+      uint32_t c0, c1;
+      if (gg) {
+        c0 = q6_codes_hi(ql[2 * e], h0);
+        c1 = q6_codes_hi(ql[2 * e + 1], h1);
+      } else {
+        c0 = q6_codes_lo(ql[2 * e], h0);
+        c1 = q6_codes_lo(ql[2 * e + 1], h1);
+      }
+      a[2 * gg + e] = q6_frag(c0, c1, ds, nds);
+    }
+  }
+}
+
+// LDS byte offset of token-tile granule (token t, 8-column granule c) of a K half.
+__device__ __forceinline__ int xgran(int t, int c) { return (t * 16 + (c ^ (t & 15))) * 16; }
+
+// Granule of the x operand of fragment f (within its K half) for k-group jA.
+__device__ __forceinline__ int xfrag_gran(int f, int jA) {
+  const int g = f >> 1, e = f & 1;
+  return 4 * ((jA >> 1) + 2 * (g & 1)) + 2 * (jA & 1) + e;
+}
+
+struct Tile {
+  int64_t expert;
+  int r0, nv;  // first route position, valid routes (<= kM)
+};
+
+__device__ __forceinline__ bool tile_info(const MoeWs& ws, int tile, Tile& T) {
+  if (tile >= ws.hdr[2]) return false;
+  const int slot = ws.tile_slot[tile];
+  const int a0 = ws.act_off[slot], a1 = ws.act_off[slot + 1];
+  T.expert = ws.active[slot];
+  T.r0 = a0 + (tile - ws.tile_off[slot]) * kM;
+  T.nv = a1 - T.r0 < kM ? a1 - T.r0 : kM;
+  return true;
+}
+
+// The streaming core shared by both kernels. ``rows(u)`` gives unit u's row
+// group; ``xrow(t)`` the row of token-tile row t in the [*, K] BF16 matrix x.
+template <typename RowFn>
+__device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
+                                          const uint16_t* x, const uint32_t (&xoff)[kXDma], int K,
+                                          int64_t expert, f32x4 (&acc)[kUnits][kTG]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int j = lane & 15, jA = lane >> 4;
+  uint8_t* xbuf = smem;
+  uint8_t* wbuf = smem + 2 * kHalfBytes + wave * 2 * kWStage;
+  const int kbs = K / kQK;
+  const int S = 2 * kbs;
+  const HalfUnitLane L(lane);
+  const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
+  auto issue = [&](int s) {
+    const int kb = s >> 1, h = s & 1;
+    uint8_t* ws = wbuf + (s & 1) * kWStage;
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+      const Proj& p = projs[unit_proj[u]];
+      issue_half_unit(p.data + expert * p.dstride, p.scales + expert * p.sstride, kbs, rg_of(u), kb, h, L, lane,
+                      ws + u * kHUnit);
+    }
+    uint8_t* xs = xbuf + (s & 1) * kHalfBytes + wave * kXDma * 1024;
+#pragma unroll
+    for (int i = 0; i < kXDma; ++i) dma16(xb + (int64_t)(kb * kQK + h * 128) * 2, xoff[i], xs + i * 1024);
+  };
+  constexpr int kOps = kUnits * kWDma + kXDma;  // DMA instructions per half-step per wave
+  issue(0);
+  if (S > 1) issue(1);
+  for (int s = 0; s < S; ++s) {
+    if (s + 1 < S)
+      wait_vm<kOps>();
+    else
+      wait_vm<0>();
+    __syncthreads();  // every wave's share of this half's token tile has landed
+    const int h = s & 1;
+    const uint8_t* xs = xbuf + (s & 1) * kHalfBytes;
+    const uint8_t* ws = wbuf + (s & 1) * kWStage;
+    u32x4 a[kUnits][4];
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) decode_half(ws + u * kHUnit, h, lane, a[u]);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int c = xfrag_gran(f, jA);
+#pragma unroll
+      for (int tg = 0; tg < kTG; ++tg) {
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + xgran(tg * 16 + j, c));
+#pragma unroll
+        for (int u = 0; u < kUnits; ++u) acc[u][tg] = mfma16(a[u][f], xv, acc[u][tg]);
+      }
+    }
+    __syncthreads();  // every wave is done with this stage
+    if (s + 2 < S) issue(s + 2);
+  }
+}
+
+// Per-lane token-tile DMA offsets: instruction i of this wave fills granules
+// (wave*kXDma + i)*64 + lane, i.e. token t = that/16, swizzled granule l%16.
+template <typename RowOf>
+__device__ __forceinline__ void x_offsets(uint32_t (&xoff)[kXDma], int K, RowOf row_of) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < kXDma; ++i) {
+    const int p = (wave * kXDma + i) * 64 + lane;
+    const int t = p >> 4, c = (p & 15) ^ (t & 15);
+    xoff[i] = opaque((uint32_t)((row_of(t) * K + c * 8) * 2));
+  }
+}
+
+}  // namespace pf
+
+__global__ void __launch_bounds__(256, 1)
+    moe_pf_gate_up_kernel(Proj gate, Proj up, MoeWs ws, const uint16_t* __restrict__ x, int hidden,
+                          uint16_t* __restrict__ act, int inter) {
+  using namespace pf;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  Tile T;
+  if (!tile_info(ws, blockIdx.y, T)) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int jA = lane >> 4, j = lane & 15;
+  const int rgb = blockIdx.x * 8 + 2 * wave;  // this wave's two row groups
+  uint32_t xoff[kXDma];
+  x_offsets(xoff, hidden, [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; });
+  const Proj projs[2] = {gate, up};
+  const int unit_proj[kUnits] = {0, 0, 1, 1};
+  f32x4 acc[kUnits][kTG];
+#pragma unroll
+  for (int u = 0; u < kUnits; ++u)
+#pragma unroll
+    for (int t = 0; t < kTG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  pf_stream(smem, projs, unit_proj, [&](int u) { return rgb + (u & 1); }, x, xoff, hidden, T.expert, acc);
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int row = (rgb + p) * 16 + 4 * jA;
+#pragma unroll
+    for (int tg = 0; tg < kTG; ++tg) {
+      const int q = tg * 16 + j;
+      if (q < T.nv) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float g = bf16_round(acc[p][tg][i]);
+          const float u = bf16_round(acc[2 + p][tg][i]);
+          v[i] = bf16_round(g * sigmoid_acc(g)) * u;
+        }
+        u32x2 o;
+        o[0] = pack_bf16x2(v[0], v[1]);
+        o[1] = pack_bf16x2(v[2], v[3]);
+        *reinterpret_cast<u32x2*>(act + (int64_t)(T.r0 + q) * inter + row) = o;
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256, 1)
+    moe_pf_down_kernel(Proj down, MoeWs ws, const uint16_t* __restrict__ act, int inter,
+                       uint16_t* __restrict__ y, int hidden) {
+  using namespace pf;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  Tile T;
+  if (!tile_info(ws, blockIdx.y, T)) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int jA = lane >> 4, j = lane & 15;
+  const int rgb = blockIdx.x * 16 + 4 * wave;  // this wave's four row groups
+  uint32_t xoff[kXDma];
+  x_offsets(xoff, inter, [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); });
+  const Proj projs[1] = {down};
+  const int unit_proj[kUnits] = {0, 0, 0, 0};
+  f32x4 acc[kUnits][kTG];
+#pragma unroll
+  for (int u = 0; u < kUnits; ++u)
+#pragma unroll
+    for (int t = 0; t < kTG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  pf_stream(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, xoff, inter, T.expert, acc);
+#pragma unroll
+  for (int u = 0; u < kUnits; ++u) {
+    const int row = (rgb + u) * 16 + 4 * jA;
+#pragma unroll
+    for (int tg = 0; tg < kTG; ++tg) {
+      const int q = tg * 16 + j;
+      if (q < T.nv) {
+        u32x2 o;
+        o[0] = pack_bf16x2(acc[u][tg][0], acc[u][tg][1]);
+        o[1] = pack_bf16x2(acc[u][tg][2], acc[u][tg][3]);
+        *reinterpret_cast<u32x2*>(y + (int64_t)(T.r0 + q) * hidden + row) = o;
+      }
+    }
+  }
+}
+
+bool pf_supported(int fmt, int64_t H, int64_t I) {
+  return fmt == FMT_Q6 && H % 256 == 0 && I % 256 == 0;
+}
+
+int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
+                       const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up) {
+  static bool attr_done = false;
+  if (!attr_done) {
+    hipFuncSetAttribute((const void*)moe_pf_gate_up_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
+    hipFuncSetAttribute((const void*)moe_pf_down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
+    attr_done = true;
+  }
+  hipLaunchKernelGGL(moe_pf_gate_up_kernel, dim3((unsigned)(I / 128), (unsigned)max_tiles), dim3(256), pf::kLds,
+                     s, g, u, ws, x, H, ws.act, I);
+  if (after_gate_up) hipEventRecord((hipEvent_t)after_gate_up, s);
+  hipLaunchKernelGGL(moe_pf_down_kernel, dim3((unsigned)(H / 256), (unsigned)max_tiles), dim3(256), pf::kLds, s,
+                     d, ws, ws.act, I, ws.y, H);
+  return Q6MOE_OK;
+}
+
+}  // namespace q6moe
