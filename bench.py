@@ -14,8 +14,12 @@ weights stream from HBM. The metric is algorithmic bytes per step (active
 experts' packed weights + activations + routing inputs + output) / time.
 
 Output: one JSON line (rank 0) with the ``roofline`` of the dominant kernel
-(moe_gate_up_kernel, timed with HIP events on its own stream) and the
-``cpu_baseline`` (the NumPy oracle on this host, one step, one thread).
+(moe_dec_gate_up_kernel, timed with HIP events on the stream it runs on), the
+``cpu_baseline`` (the NumPy oracle on this host, one step, one thread) and a
+``prefill`` block: the same layer shapes with 4096 tokens, skewed routing
+(per-expert logit bias N(0, 0.5)), seed 2, whose FLOPs (2 * 4096 * 8 * 3 *
+2048 * 768) over the step time give TFLOP/s against the 2.5 PFLOP/s dense
+BF16 MFMA peak.
 """
 
 import argparse
@@ -32,7 +36,10 @@ for _p in (str(ROOT), str(ROOT / "data-synth-tpu_amd")):
 
 METRIC = "Q6 expert-GEMM HBM GB/s (decode) + TFLOP/s (prefill), % of MI355X roofline"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0
 EXPERTS, TOP_K, HIDDEN, INTER, TOKENS, SEED = 128, 8, 2048, 768, 8, 1
+PREFILL_TOKENS, PREFILL_SEED, PREFILL_BIAS = 4096, 2, 0.5
+PREFILL_FLOPS = 2 * PREFILL_TOKENS * TOP_K * 3 * HIDDEN * INTER
 Q6_PROJ_BYTES = 1_277_952 + 12_288  # one 768x2048 (or 2048x768) Q6_K projection, SoA planes
 
 
@@ -50,9 +57,72 @@ def step_bytes(active, routes):
 
 
 def gate_up_bytes(active, routes):
-    """Algorithmic bytes of one moe_gate_up_kernel launch: gate+up of the active
+    """Algorithmic bytes of one moe_dec_gate_up_kernel launch: gate+up of the active
     experts, the token activations it reads and the SwiGLU rows it writes."""
     return active * 2 * Q6_PROJ_BYTES + TOKENS * HIDDEN * 2 + routes * INTER * 2
+
+
+def measure_prefill(dev, steps, warmup):
+    """Prefill step (routing, gate/up, down, combine) on the seed-2 4096-token layer."""
+    import numpy as np
+    import torch
+
+    from q6moe.experts import expert_parallel, pack_experts
+    from q6moe.synth import moe_layer
+
+    L = moe_layer(seed=PREFILL_SEED, experts=EXPERTS, top_k=TOP_K, hidden=HIDDEN, intermediate=INTER,
+                  tokens=PREFILL_TOKENS, bias_sigma=PREFILL_BIAS, pack=False)
+    tabs = [pack_experts(L[n], "Q6_K", INTER if n != "down" else HIDDEN, HIDDEN if n != "down" else INTER, dev)
+            for n in ("gate", "up", "down")]
+    x = torch.from_numpy(L["x"]).to(dev).to(torch.bfloat16)
+    ids = torch.from_numpy(L["ids"]).to(dev)
+    w = torch.from_numpy(L["weights"]).to(dev).to(torch.bfloat16)
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q6_K", hidden=HIDDEN,
+                         intermediate=INTER)
+    ws = torch.empty(fn.workspace_bytes(PREFILL_TOKENS, TOP_K, EXPERTS), dtype=torch.uint8, device=dev)
+    out = torch.empty((PREFILL_TOKENS, HIDDEN), dtype=torch.bfloat16, device=dev)
+    for _ in range(warmup):
+        fn(*tabs, x, ids, w, workspace=ws, out=out)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        fn(*tabs, x, ids, w, workspace=ws, out=out)
+    b.record()
+    torch.cuda.synchronize()
+    step_us = a.elapsed_time(b) / steps * 1e3
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
+    for row in evs:
+        for ev in row:
+            ev.record()
+    torch.cuda.synchronize()
+    for i in range(steps):
+        fn(*tabs, x, ids, w, workspace=ws, out=out, events=evs[i])
+    torch.cuda.synchronize()
+    ph = np.array([[row[j].elapsed_time(row[j + 1]) for j in range(4)] for row in evs]).mean(0) * 1e3
+    gu_flops = PREFILL_FLOPS * 2 / 3
+    gu_tflops = gu_flops / (ph[1] * 1e-6) / 1e12
+    tflops = PREFILL_FLOPS / (step_us * 1e-6) / 1e12
+    return {
+        "workload": "moe_prefill_q6k_e128_top8_h2048_i768_t4096_skew0.5",
+        "value": round(tflops, 1),
+        "unit": "TFLOP/s",
+        "us_per_step": round(step_us, 1),
+        "mfma_fraction": round(tflops / MFMA_PEAK_TFLOPS, 4),
+        "flops_per_step": PREFILL_FLOPS,
+        "phases_us": {k: round(float(v), 1) for k, v in zip(("route", "gate_up", "down", "combine"), ph)},
+        "roofline": {
+            "kernel": "moe_pf_gate_up_kernel",
+            "bound": "mfma",
+            "achieved": round(gu_tflops, 1),
+            "peak": MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gu_tflops / MFMA_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "flops_per_launch": int(gu_flops),
+            "avg_launch_us": round(float(ph[1]), 1),
+        },
+    }
 
 
 def cpu_baseline(L):
@@ -75,6 +145,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -171,7 +242,7 @@ def main():
         "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
         "phases_us": {k: round(float(v), 2) for k, v in zip(("pre", "gate_up", "down", "combine"), ph)},
         "roofline": {
-            "kernel": "moe_gate_up_kernel",
+            "kernel": "moe_dec_gate_up_kernel",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
@@ -182,6 +253,9 @@ def main():
             "avg_launch_us": round(float(ph[1]), 3),
         },
     }
+    if not args.no_prefill:
+        log("timing the prefill step (4096 tokens, seed 2) ...")
+        result["prefill"] = measure_prefill(dev, steps=10, warmup=2)
     if not args.no_cpu_baseline:
         log("timing the CPU oracle on one step (one thread) ...")
         secs = cpu_baseline(L)

@@ -433,7 +433,7 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
   return L;
 }
 
-constexpr int64_t kPrefillTile = 128;
+constexpr int64_t kPrefillTile = 128;  // routes per prefill tile (moe_prefill.hip kM)
 
 static Proj make_proj(const q6moe_table& t, int rows, int k) {
   Proj p;
@@ -633,6 +633,10 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   // The tiled MFMA path addresses token rows with 32-bit byte offsets.
   const bool tiled = pf_supported(fmt, H, I) && B * H * 2 < (1ll << 31) && B * K * I * 2 < (1ll << 31);
   if (tiled) {
+    if (pf_tile_routes() != kPrefillTile) {
+      set_error("moe_forward: prefill tile size mismatch");
+      return Q6MOE_ERR_HIP;
+    }
     const int max_tiles = (int)(E + B * K / kPrefillTile + 1);
     launch_moe_prefill(g, u, d, ws, max_tiles, a->x, (int)H, (int)I, s, a->events ? a->events[2] : nullptr);
   } else if (a->gate.qtype == Q6MOE_Q6_K) {

@@ -81,6 +81,7 @@ int launch_moe_decode(int fmt, const DecArgs& A, hipStream_t s);
 
 // Prefill grouped GEMM (Q6_K, hidden and intermediate multiples of 256).
 bool pf_supported(int fmt, int64_t H, int64_t I);
+int64_t pf_tile_routes();
 int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
                        const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up);
 

@@ -10,9 +10,10 @@
 //   moe_pf_down_kernel     256 hidden rows per workgroup; y = RNE(a Wd^T)
 //        (experts.py:108). The combine kernel in moe.hip sums f32(y)*f32(r).
 //
-// Each of the 4 waves owns 4 units (16 weight rows x one 256-wide K block)
-// per K block and decodes them straight into MFMA A operands; decoded
-// weights never leave registers. The 128 token rows of the current K half
+// Each of the 8 waves (two per SIMD, so one wave's decode overlaps the
+// other's MFMAs) owns 2 units (16 weight rows x one 256-wide K block) per K
+// block and decodes them straight into MFMA A operands; decoded weights
+// never leave registers. The 128 token rows of the current K half
 // sit in LDS (double-buffered, XOR-swizzled so the 16 token columns of an
 // MFMA read hit distinct banks) and every wave multiplies them against its
 // own rows. Both the token half-tiles and the packed weight half-units come
@@ -28,10 +29,10 @@ namespace q6moe {
 
 namespace pf {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kM = 128;            // routes per tile (MFMA column groups of 16)
 constexpr int kTG = kM / 16;       // token groups
-constexpr int kUnits = 4;          // units per wave per K block
+constexpr int kUnits = 2;          // units per wave per K block
 constexpr int kHalfBytes = kM * 128 * 2;  // one K half of the token tile (32 KB)
 constexpr int kHUnit = 2048;       // packed half-unit in LDS: ql 1024, qh 512, sc 256, d 256
 constexpr int kWStage = kUnits * kHUnit;
@@ -65,6 +66,11 @@ __device__ __forceinline__ void dma16(const uint8_t* base, uint32_t voff, void* 
 __device__ __forceinline__ void dma4(const uint8_t* base, uint32_t voff, void* lds) {
   __builtin_amdgcn_global_load_lds(sgpr_ptr(base) + voff, LDS_PTR(lds), 4, 0, 0);
 }
+// Workgroup barrier without the memory fence of __syncthreads (whose release
+// would wait for every outstanding DMA, including the ones prefetching the
+// next stage). LDS visibility comes from each wave's own vmcnt wait before it.
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -186,7 +192,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
       wait_vm<kOps>();
     else
       wait_vm<0>();
-    __syncthreads();  // every wave's share of this half's token tile has landed
+    wg_barrier();  // every wave's share of this half's token tile has landed
     const int h = s & 1;
     const uint8_t* xs = xbuf + (s & 1) * kHalfBytes;
     const uint8_t* ws = wbuf + (s & 1) * kWStage;
@@ -203,7 +209,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
         for (int u = 0; u < kUnits; ++u) acc[u][tg] = mfma16(a[u][f], xv, acc[u][tg]);
       }
     }
-    __syncthreads();  // every wave is done with this stage
+    wg_barrier();  // every wave is done with this stage
     if (s + 2 < S) issue(s + 2);
   }
 }
@@ -223,7 +229,7 @@ __device__ __forceinline__ void x_offsets(uint32_t (&xoff)[kXDma], int K, RowOf 
 
 }  // namespace pf
 
-__global__ void __launch_bounds__(256, 1)
+__global__ void __launch_bounds__(512, 2)
     moe_pf_gate_up_kernel(Proj gate, Proj up, MoeWs ws, const uint16_t* __restrict__ x, int hidden,
                           uint16_t* __restrict__ act, int inter) {
   using namespace pf;
@@ -232,41 +238,38 @@ __global__ void __launch_bounds__(256, 1)
   if (!tile_info(ws, blockIdx.y, T)) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
-  const int rgb = blockIdx.x * 8 + 2 * wave;  // this wave's two row groups
+  const int rgb = blockIdx.x * 8 + wave;  // this wave's row group (gate and up)
   uint32_t xoff[kXDma];
   x_offsets(xoff, hidden, [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; });
   const Proj projs[2] = {gate, up};
-  const int unit_proj[kUnits] = {0, 0, 1, 1};
+  const int unit_proj[kUnits] = {0, 1};
   f32x4 acc[kUnits][kTG];
 #pragma unroll
   for (int u = 0; u < kUnits; ++u)
 #pragma unroll
     for (int t = 0; t < kTG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  pf_stream(smem, projs, unit_proj, [&](int u) { return rgb + (u & 1); }, x, xoff, hidden, T.expert, acc);
+  pf_stream(smem, projs, unit_proj, [&](int) { return rgb; }, x, xoff, hidden, T.expert, acc);
+  const int row = rgb * 16 + 4 * jA;
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int row = (rgb + p) * 16 + 4 * jA;
+  for (int tg = 0; tg < kTG; ++tg) {
+    const int q = tg * 16 + j;
+    if (q < T.nv) {
+      float v[4];
 #pragma unroll
-    for (int tg = 0; tg < kTG; ++tg) {
-      const int q = tg * 16 + j;
-      if (q < T.nv) {
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float g = bf16_round(acc[p][tg][i]);
-          const float u = bf16_round(acc[2 + p][tg][i]);
-          v[i] = bf16_round(g * sigmoid_acc(g)) * u;
-        }
-        u32x2 o;
-        o[0] = pack_bf16x2(v[0], v[1]);
-        o[1] = pack_bf16x2(v[2], v[3]);
-        *reinterpret_cast<u32x2*>(act + (int64_t)(T.r0 + q) * inter + row) = o;
+      for (int i = 0; i < 4; ++i) {
+        const float g = bf16_round(acc[0][tg][i]);
+        const float u = bf16_round(acc[1][tg][i]);
+        v[i] = bf16_round(g * sigmoid_acc(g)) * u;
       }
+      u32x2 o;
+      o[0] = pack_bf16x2(v[0], v[1]);
+      o[1] = pack_bf16x2(v[2], v[3]);
+      *reinterpret_cast<u32x2*>(act + (int64_t)(T.r0 + q) * inter + row) = o;
     }
   }
 }
 
-__global__ void __launch_bounds__(256, 1)
+__global__ void __launch_bounds__(512, 2)
     moe_pf_down_kernel(Proj down, MoeWs ws, const uint16_t* __restrict__ act, int inter,
                        uint16_t* __restrict__ y, int hidden) {
   using namespace pf;
@@ -275,11 +278,11 @@ __global__ void __launch_bounds__(256, 1)
   if (!tile_info(ws, blockIdx.y, T)) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
-  const int rgb = blockIdx.x * 16 + 4 * wave;  // this wave's four row groups
+  const int rgb = blockIdx.x * 16 + 2 * wave;  // this wave's two row groups
   uint32_t xoff[kXDma];
   x_offsets(xoff, inter, [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); });
   const Proj projs[1] = {down};
-  const int unit_proj[kUnits] = {0, 0, 0, 0};
+  const int unit_proj[kUnits] = {0, 0};
   f32x4 acc[kUnits][kTG];
 #pragma unroll
   for (int u = 0; u < kUnits; ++u)
@@ -306,6 +309,8 @@ bool pf_supported(int fmt, int64_t H, int64_t I) {
   return fmt == FMT_Q6 && H % 256 == 0 && I % 256 == 0;
 }
 
+int64_t pf_tile_routes() { return pf::kM; }
+
 int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
                        const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up) {
   static bool attr_done = false;
@@ -314,10 +319,10 @@ int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs&
     hipFuncSetAttribute((const void*)moe_pf_down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
     attr_done = true;
   }
-  hipLaunchKernelGGL(moe_pf_gate_up_kernel, dim3((unsigned)(I / 128), (unsigned)max_tiles), dim3(256), pf::kLds,
+  hipLaunchKernelGGL(moe_pf_gate_up_kernel, dim3((unsigned)(I / 128), (unsigned)max_tiles), dim3(64 * pf::kWaves), pf::kLds,
                      s, g, u, ws, x, H, ws.act, I);
   if (after_gate_up) hipEventRecord((hipEvent_t)after_gate_up, s);
-  hipLaunchKernelGGL(moe_pf_down_kernel, dim3((unsigned)(H / 256), (unsigned)max_tiles), dim3(256), pf::kLds, s,
+  hipLaunchKernelGGL(moe_pf_down_kernel, dim3((unsigned)(H / 256), (unsigned)max_tiles), dim3(64 * pf::kWaves), pf::kLds, s,
                      d, ws, ws.act, I, ws.y, H);
   return Q6MOE_OK;
 }
