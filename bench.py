@@ -41,6 +41,11 @@ EXPERTS, TOP_K, HIDDEN, INTER, TOKENS, SEED = 128, 8, 2048, 768, 8, 1
 PREFILL_TOKENS, PREFILL_SEED, PREFILL_BIAS = 4096, 2, 0.5
 PREFILL_FLOPS = 2 * PREFILL_TOKENS * TOP_K * 3 * HIDDEN * INTER
 Q6_PROJ_BYTES = 1_277_952 + 12_288  # one 768x2048 (or 2048x768) Q6_K projection, SoA planes
+# L2-to-fabric bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE over this script, scaled by a 512 MiB device copy in the same run
+# (profiles/moe_q6k_e128_top8_h2048_i768__hbm_bytes.txt); they change only
+# when the kernels do and are re-measured with them.
+TRAFFIC_BYTES = {"moe_dec_gate_up_kernel": 137_190_000, "moe_pf_gate_up_kernel": 1_407_080_000}
 
 
 def log(*a):
@@ -118,7 +123,7 @@ def measure_prefill(dev, steps, warmup):
             "peak": MFMA_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gu_tflops / MFMA_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_BYTES["moe_pf_gate_up_kernel"],
             "flops_per_launch": int(gu_flops),
             "avg_launch_us": round(float(ph[1]), 1),
         },
@@ -146,6 +151,9 @@ def main():
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--calib-copy-mb", type=int, default=0,
+                    help="first copy a buffer of this many MiB device-to-device 5 times (a known-size "
+                         "kernel for scaling hardware byte counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -163,6 +171,13 @@ def main():
     from q6moe.synth import moe_layer
 
     dev = torch.device("cuda", 0)
+    if args.calib_copy_mb > 0:
+        src = torch.ones(args.calib_copy_mb << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     log("generating the decode workload (seed 1) ...")
     t0 = time.perf_counter()
     L = moe_layer(seed=SEED, experts=EXPERTS, top_k=TOP_K, hidden=HIDDEN, intermediate=INTER,
@@ -248,7 +263,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": TRAFFIC_BYTES["moe_dec_gate_up_kernel"],
             "bytes_per_launch": gu_bytes,
             "avg_launch_us": round(float(ph[1]), 3),
         },
