@@ -106,9 +106,136 @@ __global__ void kv_read_scalar_kernel(KvParams p, int64_t total) {
     reinterpret_cast<float*>(p.out)[i] = v;
 }
 
+// ---------------------------------------------------------------------------
+// Quantise and write (quantize / write_quantized, attention_cache.py:15-43).
+// One thread per (row, group): max|g|, the scale, then the group's codes.
+// ---------------------------------------------------------------------------
+struct KvQuant {
+  const void* x;
+  int x_bf16;
+  int64_t chans, group, groups;
+  int scale_bf16;
+};
+
+__device__ __forceinline__ float kv_x(const KvQuant& q, int64_t i) {
+  return q.x_bf16 ? bf16_to_float(reinterpret_cast<const uint16_t*>(q.x)[i])
+                  : reinterpret_cast<const float*>(q.x)[i];
+}
+
+// Quantise group g of row r into codes (chans-strided destination) and
+// return the stored scale value (FP32 holding the BF16 or FP32 scale).
+__device__ __forceinline__ float kv_quant_group(const KvQuant& q, int64_t r, int64_t g, int8_t* dst) {
+  const int64_t base = r * q.chans + g * q.group;
+  float m = 0.f;
+  for (int64_t c = 0; c < q.group; ++c) m = fmaxf(m, fabsf(kv_x(q, base + c)));
+  float scale = m / 127.f;
+  if (q.scale_bf16) scale = bf16_round(scale);
+  const float divisor = scale == 0.f ? 1.f : scale;
+  for (int64_t c = 0; c < q.group; ++c) {
+    float v = __builtin_rintf(kv_x(q, base + c) / divisor);
+    v = fminf(fmaxf(v, -127.f), 127.f);
+    dst[c] = (int8_t)(int)v;
+  }
+  return scale;
+}
+
+__device__ __forceinline__ void kv_store_scale(void* scales, int bf16, int64_t idx, float v) {
+  if (bf16)
+    reinterpret_cast<uint16_t*>(scales)[idx] = bf16_bits(v);
+  else
+    reinterpret_cast<float*>(scales)[idx] = v;
+}
+
+__global__ void __launch_bounds__(256) kv_quantize_kernel(KvQuant q, int64_t rows, int8_t* codes, void* scales) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * q.groups) return;
+  const int64_t r = i / q.groups, g = i % q.groups;
+  const float s = kv_quant_group(q, r, g, codes + r * q.chans + g * q.group);
+  kv_store_scale(scales, q.scale_bf16, i, s);
+}
+
+struct KvWrite {
+  int8_t* codes;
+  void* scales;
+  int scale_plane;
+  const int32_t* table;
+  int64_t pool_pages, pps, page, cap;
+  const int32_t* indices;
+  const uint8_t* active;
+};
+
+__global__ void __launch_bounds__(256) kv_write_kernel(KvQuant q, KvWrite w, int64_t batch) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= batch * q.groups) return;
+  const int64_t b = i / q.groups, g = i % q.groups;
+  if (w.active && !w.active[b]) return;
+  int64_t t = w.indices[b];
+  if (t < 0) t += w.cap;
+  if (t < 0 || t >= w.cap) return;  // out-of-bounds scatter updates are dropped
+  int64_t row = b * w.cap + t;
+  if (w.table) {
+    const int64_t pg = w.table[b * w.pps + t / w.page];
+    if (pg < 0 || pg >= w.pool_pages) return;
+    row = pg * w.page + t % w.page;
+  }
+  const float s = kv_quant_group(q, b, g, w.codes + row * q.chans + g * q.group);
+  const int64_t idx = w.scale_plane ? (b * q.groups + g) * w.cap + t : row * q.groups + g;
+  kv_store_scale(w.scales, q.scale_bf16, idx, s);
+}
+
 }  // namespace q6moe
 
 using namespace q6moe;
+
+extern "C" int q6moe_kv_quantize(const void* x, int x_dtype, int64_t rows, int64_t chans, int64_t group,
+                                 int8_t* codes, void* scales, int scale_dtype, void* stream) {
+  Q6MOE_REQUIRE(x && codes && scales, "kv_quantize: null pointer");
+  Q6MOE_REQUIRE(rows >= 1 && chans >= 1 && group >= 1 && chans % group == 0,
+                "kv_quantize: rows, chans must be positive and group must divide chans");
+  Q6MOE_REQUIRE(x_dtype == Q6MOE_BF16 || x_dtype == Q6MOE_F32, "kv_quantize: x dtype");
+  Q6MOE_REQUIRE(scale_dtype == Q6MOE_BF16 || scale_dtype == Q6MOE_F32, "kv_quantize: scale dtype");
+  KvQuant q{x, x_dtype == Q6MOE_BF16, chans, group, chans / group, scale_dtype == Q6MOE_BF16};
+  const int64_t n = rows * q.groups;
+  hipLaunchKernelGGL(kv_quantize_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, (hipStream_t)stream, q,
+                     rows, codes, scales);
+  return check_launch("kv_quantize");
+}
+
+extern "C" int q6moe_kv_write(const q6moe_kv_write_args* a, void* stream) {
+  Q6MOE_REQUIRE(a, "kv_write: null args");
+  Q6MOE_REQUIRE(a->x && a->codes && a->scales && a->indices, "kv_write: null pointer");
+  Q6MOE_REQUIRE(a->batch >= 1 && a->kv_heads >= 1 && a->head_dim >= 1,
+                "kv_write: batch, kv_heads and head_dim must be positive");
+  const int64_t chans = a->kv_heads * a->head_dim;
+  Q6MOE_REQUIRE(a->group >= 1 && chans % a->group == 0, "kv_write: group must divide kv_heads*head_dim");
+  Q6MOE_REQUIRE(a->x_dtype == Q6MOE_BF16 || a->x_dtype == Q6MOE_F32, "kv_write: x dtype");
+  Q6MOE_REQUIRE(a->scale_dtype == Q6MOE_BF16 || a->scale_dtype == Q6MOE_F32, "kv_write: scale dtype");
+  Q6MOE_REQUIRE(a->scale_layout == 0 || a->scale_layout == 1, "kv_write: scale layout");
+  KvWrite w;
+  w.codes = a->codes;
+  w.scales = a->scales;
+  w.scale_plane = a->scale_layout == 0;
+  w.table = a->page_table;
+  w.pool_pages = a->pool_pages;
+  w.pps = a->pages_per_seq;
+  w.page = a->page_size;
+  w.indices = a->indices;
+  w.active = a->active;
+  if (a->page_table) {
+    Q6MOE_REQUIRE(a->pages_per_seq >= 1 && a->page_size >= 1 && a->pool_pages >= 1,
+                  "kv_write: paged cache needs pages_per_seq, page_size, pool_pages >= 1");
+    Q6MOE_REQUIRE(a->scale_layout == 1, "kv_write: paged cache uses token-major scales");
+    w.cap = a->pages_per_seq * a->page_size;
+  } else {
+    Q6MOE_REQUIRE(a->capacity >= 1, "kv_write: capacity must be positive");
+    w.cap = a->capacity;
+  }
+  KvQuant q{a->x, a->x_dtype == Q6MOE_BF16, chans, a->group, chans / a->group, a->scale_dtype == Q6MOE_BF16};
+  const int64_t n = a->batch * q.groups;
+  hipLaunchKernelGGL(kv_write_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, (hipStream_t)stream, q, w,
+                     a->batch);
+  return check_launch("kv_write");
+}
 
 extern "C" int q6moe_kv_read(const q6moe_kv_args* a, void* stream) {
   Q6MOE_REQUIRE(a, "kv_read: null args");

@@ -83,6 +83,28 @@ class KvArgs(ctypes.Structure):
     ]
 
 
+class KvWriteArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", _vp),
+        ("x_dtype", _int),
+        ("codes", _vp),
+        ("scales", _vp),
+        ("scale_dtype", _int),
+        ("scale_layout", _int),
+        ("page_table", _vp),
+        ("pool_pages", _i64),
+        ("pages_per_seq", _i64),
+        ("page_size", _i64),
+        ("indices", _vp),
+        ("active", _vp),
+        ("batch", _i64),
+        ("capacity", _i64),
+        ("kv_heads", _i64),
+        ("head_dim", _i64),
+        ("group", _i64),
+    ]
+
+
 # name -> (restype, argtypes); exactly the entry points of include/q6moe.h
 SIGNATURES = {
     "q6moe_version": (_int, []),
@@ -94,6 +116,8 @@ SIGNATURES = {
     "q6moe_moe_workspace_size": (_size, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "q6moe_moe_forward": (_int, [ctypes.POINTER(MoeArgs), _vp]),
     "q6moe_kv_read": (_int, [ctypes.POINTER(KvArgs), _vp]),
+    "q6moe_kv_quantize": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _vp]),
+    "q6moe_kv_write": (_int, [ctypes.POINTER(KvWriteArgs), _vp]),
 }
 
 _lib = None

@@ -1,16 +1,18 @@
-"""INT8 KV cache reads on the GPU: ``read_quantized`` and the paged variant.
+"""INT8 KV cache on the GPU: ``quantize``, ``write_quantized``, ``read_quantized``
+and the paged variants.
 
-Mirrors kaggle/qwen38_tpu/attention_cache.py:46-81:
+Mirrors kaggle/qwen38_tpu/attention_cache.py:15-81:
 
 * dense reference cache: ``cache[name]`` int8 [B, T, KVH*D], ``cache[name +
   "_scale"]`` BF16 [B*G, T] with G = KVH*D/cache_group; ``indices`` [B, S]
   follow JAX gather rules (negative adds T, then clamp);
 * result ``compute_cast(f32(code) * f32(scale), dtype)``, i.e. RNE to BF16.
 
-``read_paged`` is the paged generalisation (page tables per sequence, FP32
-per-token-per-head scales). Both run the HIP kernel ``q6moe_kv_read``.
-``quantize`` / ``gather_scale_plane`` keep the reference contract and error
-messages.
+``read_paged`` / ``write_paged`` are the paged generalisation (page tables
+per sequence, FP32 per-token-per-head scales). Reads run the HIP kernel
+``q6moe_kv_read``; ``quantize`` runs ``q6moe_kv_quantize`` and the writes
+``q6moe_kv_write``. ``gather_scale_plane`` keeps the reference contract and
+error messages.
 """
 
 import ctypes
@@ -35,6 +37,90 @@ def _run(args, device):
     _lib.check(rc, "kv_read")
 
 
+def _group_of(c):
+    return getattr(c, "cache_group", None) or getattr(c, "group")
+
+
+def quantize(x, group, scale_dtype=torch.bfloat16):
+    """attention_cache.py:15-23 on the GPU: x [..., C] (BF16/FP32) -> (int8 codes
+    [..., C], scale [..., C // group]). A BF16 scale is RNE_bf16(max|g| / 127)
+    and is also the divisor (1 for an all-zero group); FP32 keeps the quotient."""
+    if not isinstance(x, torch.Tensor) or x.device.type != "cuda":
+        raise ValueError("x must be a GPU tensor")
+    if x.shape[-1] % group:
+        raise ValueError("group must divide the last dimension")
+    xx = x.contiguous()
+    rows, chans = xx.numel() // x.shape[-1], x.shape[-1]
+    codes = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    scale = torch.empty((*x.shape[:-1], chans // group), dtype=scale_dtype, device=x.device)
+    lib = _lib.load()
+    with torch.cuda.device(x.device):
+        rc = lib.q6moe_kv_quantize(xx.data_ptr(), _dtype_code(xx.dtype), rows, chans, group, codes.data_ptr(),
+                                   scale.data_ptr(), _dtype_code(scale_dtype), _lib.stream_handle(x.device))
+    _lib.check(rc, "kv_quantize")
+    return codes, scale
+
+
+def _write(x, codes, scales, *, layout, indices, active, batch, capacity, heads, dim, group, table=None,
+           pool_pages=0, pages_per_seq=0, page_size=0):
+    xx = x.reshape(batch, heads * dim).contiguous()
+    idx = indices.to(device=codes.device, dtype=torch.int32).contiguous()
+    if idx.numel() != batch:
+        raise ValueError("indices must hold one token slot per row")
+    act = None
+    if active is not None:
+        act = active.to(device=codes.device).reshape(batch).to(torch.uint8).contiguous()
+    a = _lib.KvWriteArgs()
+    a.x, a.x_dtype = xx.data_ptr(), _dtype_code(xx.dtype)
+    a.codes, a.scales = codes.data_ptr(), scales.data_ptr()
+    a.scale_dtype, a.scale_layout = _dtype_code(scales.dtype), layout
+    a.page_table = None if table is None else table.data_ptr()
+    a.pool_pages, a.pages_per_seq, a.page_size = pool_pages, pages_per_seq, page_size
+    a.indices = idx.data_ptr()
+    a.active = None if act is None else act.data_ptr()
+    a.batch, a.capacity = batch, capacity
+    a.kv_heads, a.head_dim, a.group = heads, dim, group
+    lib = _lib.load()
+    with torch.cuda.device(codes.device):
+        rc = lib.q6moe_kv_write(ctypes.byref(a), _lib.stream_handle(codes.device))
+    _lib.check(rc, "kv_write")
+
+
+def write_quantized(cache, key, value, indices, active, c):
+    """attention_cache.py:26-43: quantise the new token's key/value rows
+    ([B, kv_heads*head_dim] or [B, kv_heads, head_dim]) and store codes at
+    cache[name][b, indices[b]] and scales at cache[name + "_scale"][b*G + g,
+    indices[b]] for rows with ``active[b]``. The cache tensors are updated in
+    place (the reference's functional update with buffer donation) and the
+    dict is returned."""
+    group = _group_of(c)
+    for name, token in (("k", key), ("v", value)):
+        codes, plane = cache[name], cache[name + "_scale"]
+        if codes.dtype != torch.int8 or codes.ndim != 3 or codes.shape[2] != c.kv_heads * c.head_dim:
+            raise ValueError("cache codes must be int8 [batch, time, kv_heads * head_dim]")
+        if not codes.is_contiguous() or not plane.is_contiguous():
+            raise ValueError("cache tensors must be contiguous")
+        batch, time, chans = codes.shape
+        if plane.shape != (batch * (chans // group), time):
+            raise ValueError("Scale plane must be [batch * groups, time]")
+        _write(token, codes, plane, layout=0, indices=indices, active=active, batch=batch, capacity=time,
+               heads=c.kv_heads, dim=c.head_dim, group=group)
+    return cache
+
+
+def write_paged(pool, scales, page_table, x, indices, *, page_size, kv_heads, head_dim, group=None, active=None):
+    """Paged write: quantise x [B, kv_heads*head_dim] and store row b at token
+    slot indices[b] of sequence b (page page_table[b, t // page_size])."""
+    group = head_dim if group is None else group
+    if pool.dtype != torch.int8 or pool.ndim < 3 or pool.shape[1] != page_size or not pool.is_contiguous():
+        raise ValueError("pool must be contiguous int8 [pages, page_size, ...]")
+    table = page_table.to(device=pool.device, dtype=torch.int32).contiguous()
+    batch, pps = table.shape
+    _write(x, pool, scales, layout=1, indices=indices, active=active, batch=batch, capacity=pps * page_size,
+           heads=kv_heads, dim=head_dim, group=group, table=table, pool_pages=pool.shape[0],
+           pages_per_seq=pps, page_size=page_size)
+
+
 def read_quantized(cache, name, indices, c, dtype=torch.bfloat16, *, scale_gather=None):
     """Gather + dequantize cached tokens -> dtype [B, S, kv_heads, head_dim].
 
@@ -47,7 +133,7 @@ def read_quantized(cache, name, indices, c, dtype=torch.bfloat16, *, scale_gathe
     codes = cache[name]
     plane = cache[name + "_scale"]
     heads, dim = c.kv_heads, c.head_dim
-    group = getattr(c, "cache_group", None) or getattr(c, "group")
+    group = _group_of(c)
     if codes.dtype != torch.int8 or codes.ndim != 3 or codes.shape[2] != heads * dim:
         raise ValueError("cache codes must be int8 [batch, time, kv_heads * head_dim]")
     batch, time, chans = codes.shape

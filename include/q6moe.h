@@ -22,6 +22,8 @@
  *                         kaggle/qwen38_tpu/grouped_experts.py:21-163
  *  - q6moe_kv_read        kaggle/qwen38_tpu/attention_cache.py:71-81 (read_quantized)
  *                         kaggle/qwen38_tpu/attention_cache.py:46-68 (gather_scale_plane)
+ *  - q6moe_kv_quantize    kaggle/qwen38_tpu/attention_cache.py:15-23 (quantize)
+ *  - q6moe_kv_write       kaggle/qwen38_tpu/attention_cache.py:26-43 (write_quantized)
  */
 #ifndef Q6MOE_H
 #define Q6MOE_H
@@ -157,6 +159,48 @@ typedef struct q6moe_kv_args {
 } q6moe_kv_args;
 
 int q6moe_kv_read(const q6moe_kv_args* args, void* stream);
+
+/*
+ * INT8 block quantisation of KV rows (quantize, kaggle/qwen38_tpu/attention_cache.py:15-23):
+ * x [rows, chans] (BF16 or F32 values) in groups of ``group`` channels ->
+ * codes int8 [rows, chans] and scales [rows, chans/group]. With a BF16 scale,
+ * scale = RNE_bf16(max|g| / 127) and the rounded scale is the divisor; with an
+ * F32 scale the FP32 quotient is both. An all-zero group stores scale 0 and
+ * divides by 1. codes = clip(rint(g / divisor), -127, 127).
+ */
+int q6moe_kv_quantize(const void* x, int x_dtype, int64_t rows, int64_t chans, int64_t group,
+                      int8_t* codes, void* scales, int scale_dtype, void* stream);
+
+/*
+ * write_quantized (kaggle/qwen38_tpu/attention_cache.py:26-43): quantise row b of x
+ * (one new token per sequence) and store its codes at token slot indices[b] of the
+ * dense cache [B, T, KVH*D] (page_table NULL) or of the paged pool [pages, P, KVH*D],
+ * and its scales in the plane [B*G, T] (scale_layout 0, dense only) or token-major
+ * [rows, G] (scale_layout 1). Rows with active[b] == 0 are left unchanged. A slot
+ * index below zero adds T; slots outside [0, T) and unmapped pages are not written
+ * (JAX scatter drops out-of-bounds updates).
+ */
+typedef struct q6moe_kv_write_args {
+  const void* x;            /* [B, KVH*D] */
+  int x_dtype;              /* Q6MOE_BF16 or Q6MOE_F32 */
+  int8_t* codes;            /* dense: [B, T, KVH*D]; paged: [pages, page_size, KVH*D] */
+  void* scales;             /* see scale_layout */
+  int scale_dtype;          /* Q6MOE_BF16 (reference) or Q6MOE_F32 */
+  int scale_layout;         /* 0: plane [B*G, T]; 1: token-major [rows, G] */
+  const int32_t* page_table;/* NULL: dense cache; else [B, pages_per_seq] */
+  int64_t pool_pages;
+  int64_t pages_per_seq;
+  int64_t page_size;
+  const int32_t* indices;   /* [B] token slot per row */
+  const uint8_t* active;    /* [B] nonzero: write the row; NULL: every row */
+  int64_t batch;            /* B */
+  int64_t capacity;         /* T (dense) -- paged: pages_per_seq * page_size */
+  int64_t kv_heads;
+  int64_t head_dim;
+  int64_t group;            /* channels per scale; divides KVH*D */
+} q6moe_kv_write_args;
+
+int q6moe_kv_write(const q6moe_kv_write_args* args, void* stream);
 
 #ifdef __cplusplus
 }
