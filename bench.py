@@ -130,6 +130,121 @@ def measure_prefill(dev, steps, warmup):
     }
 
 
+def _time_calls(fn, calls, warmup=3):
+    """Mean device time (us) of ``calls`` back-to-back invocations of fn(i)."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(calls):
+        fn(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / calls * 1e3
+
+
+def measure_projection(dev):
+    """Single packed-Q6 projection, x bf16 [8, 2048] x W [2048 -> 768], seed 0, BF16 output.
+    Hot: the same 1.3 MB weights every call (us per call, cache-resident). Cold:
+    640 distinct weight copies (826 MB, over 3x the Infinity Cache) in rotation."""
+    import torch
+
+    from q6moe import pack_q6
+    from q6moe.kernel import q6_matmul
+    from q6moe.synth import projection
+
+    w = projection(seed=0)
+    packed = pack_q6(w["raw"], 2048)
+    data = torch.from_numpy(packed.data).to(dev)
+    scales = torch.from_numpy(packed.scales).to(dev)
+    x = torch.from_numpy(w["x"]).to(dev).to(torch.bfloat16)
+    hot = _time_calls(lambda i: q6_matmul(x, data, scales, output_features=768, out_dtype=torch.bfloat16), 200)
+    copies = 640
+    datas = data.repeat(copies, 1)
+    scaless = scales.repeat(copies, 1)
+    cold = _time_calls(lambda i: q6_matmul(x, datas[i % copies], scaless[i % copies], output_features=768,
+                                           out_dtype=torch.bfloat16), copies)
+    nbytes = 1_290_240 + 32_768 + 12_288
+    return {"workload": "q6_projection_x8x2048_w2048to768", "hot_us_per_call": round(hot, 2),
+            "cold_us_per_call": round(cold, 2), "cold_GBps": round(nbytes / (cold * 1e-6) / 1e9, 1),
+            "bytes_per_call": nbytes, "cold_copies": copies}
+
+
+def measure_q4_shared(dev):
+    """Q4_K decode with an always-on shared expert: 64 experts, top-6, H 4096, I 1024,
+    shared I 4096, N(0, 0.015), seed 3; tokens 1, 8, 64. Weight tables rotate over
+    enough copies that the active bytes of one rotation exceed 3x the Infinity Cache."""
+    import numpy as np
+    import torch
+
+    from q6moe.experts import expert_parallel, pack_experts
+    from q6moe.synth import moe_layer
+
+    H4, I4, E4, K4, IS = 4096, 1024, 64, 6, 4096
+    L = moe_layer(seed=3, experts=E4, top_k=K4, hidden=H4, intermediate=I4, tokens=64, sigma=0.015,
+                  qtype="Q4_K", shared_intermediate=IS, pack=False)
+    base = [pack_experts(L[n], "Q4_K", I4 if n != "down" else H4, H4 if n != "down" else I4, dev)
+            for n in ("gate", "up", "down")]
+    sh = L["shared"]
+    shared = dict(gate=pack_experts(sh["gate"][None], "Q4_K", IS, H4, dev),
+                  up=pack_experts(sh["up"][None], "Q4_K", IS, H4, dev),
+                  down=pack_experts(sh["down"][None], "Q4_K", H4, IS, dev))
+    fn = expert_parallel(None, gate_type="Q4_K", up_type="Q4_K", down_type="Q4_K", hidden=H4, intermediate=I4)
+    per_expert, shared_bytes = 7_077_888, 28_311_552
+    out = {"workload": "moe_decode_q4k_e64_top6_h4096_i1024_shared4096", "batches": {}}
+    layers = [base]
+    for b in (1, 8, 64):
+        active = len(np.unique(L["ids"][:b]))
+        nbytes = active * per_expert + shared_bytes + 2 * b * H4 * 2
+        want = min(12, max(2, -(-3 * 256 * 2**20 // nbytes)))
+        while len(layers) < want:
+            layers.append([type(t)(t.qtype, t.data.clone(), None, t.rows, t.width) for t in base])
+        x = torch.from_numpy(L["x"][:b]).to(dev).to(torch.bfloat16)
+        ids = torch.from_numpy(L["ids"][:b]).to(dev)
+        w = torch.from_numpy(L["weights"][:b]).to(dev).to(torch.bfloat16)
+        ws = torch.empty(fn.workspace_bytes(b, K4, E4, IS), dtype=torch.uint8, device=dev)
+        o = torch.empty((b, H4), dtype=torch.bfloat16, device=dev)
+        us = _time_calls(lambda i: fn(*layers[i % want], x, ids, w, shared=shared, workspace=ws, out=o), 100)
+        out["batches"][str(b)] = {"us_per_step": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                  "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                  "active_experts": active, "bytes_per_step": nbytes, "layer_copies": want}
+    return out
+
+
+def measure_kv_gather(dev):
+    """Paged INT8 KV gather + dequant of every cached token: batch 8, 4 KV heads x 128,
+    32768 tokens per sequence in pages of 256, FP32 per-token-per-head scales, seed 4.
+    One call reads K and V (codes, scales, page tables) and writes BF16 [8, 32768, 4, 128]
+    for each; three pool copies rotate so the 276 MB of codes are not cache-resident."""
+    import torch
+
+    from q6moe.attention_cache import read_paged
+    from q6moe.synth import kv_pages
+
+    K = kv_pages(seed=4)
+    P, H, D = K["page_size"], K["kv_heads"], K["head_dim"]
+    table = torch.from_numpy(K["page_table"]).to(dev)
+    pools = []
+    for _ in range(3):
+        pools.append({n: torch.from_numpy(K[n]).to(dev) for n in ("k", "k_scale", "v", "v_scale")})
+    ok = torch.empty((8, K["context"], H, D), dtype=torch.bfloat16, device=dev)
+    ov = torch.empty_like(ok)
+
+    def call(i):
+        p = pools[i % 3]
+        read_paged(p["k"], p["k_scale"], table, page_size=P, kv_heads=H, head_dim=D, out=ok)
+        read_paged(p["v"], p["v_scale"], table, page_size=P, kv_heads=H, head_dim=D, out=ov)
+
+    us = _time_calls(call, 30)
+    nbytes = 813_699_072
+    return {"workload": "kv_paged_gather_b8_kvh4_d128_ctx32768_p256_f32scale", "us_per_call": round(us, 1),
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}
+
+
 def cpu_baseline(L):
     """The NumPy oracle (one thread) on one full decode step of the same workload."""
     from threadpoolctl import threadpool_limits
@@ -151,6 +266,8 @@ def main():
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the single-projection, Q4_K+shared and KV-gather measurements")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="first copy a buffer of this many MiB device-to-device 5 times (a known-size "
                          "kernel for scaling hardware byte counters)")
@@ -271,6 +388,10 @@ def main():
     if not args.no_prefill:
         log("timing the prefill step (4096 tokens, seed 2) ...")
         result["prefill"] = measure_prefill(dev, steps=10, warmup=2)
+    if not args.no_extras:
+        log("timing the single projection, the Q4_K + shared layer and the KV gather ...")
+        result["extras"] = {"projection": measure_projection(dev), "q4k_shared": measure_q4_shared(dev),
+                            "kv_gather": measure_kv_gather(dev)}
     if not args.no_cpu_baseline:
         log("timing the CPU oracle on one step (one thread) ...")
         secs = cpu_baseline(L)
