@@ -26,39 +26,49 @@ struct KvParams {
   int out_bf16;
 };
 
-// Cache row of (sequence b, token t) or -1 for an unmapped page.
-__device__ __forceinline__ int64_t kv_row(const KvParams& p, int64_t b, int64_t s, int64_t* tok) {
-  int64_t t = p.indices ? (int64_t)p.indices[b * p.sel + s] : s;
-  if (t < 0) t += p.cap;
-  t = t < 0 ? 0 : (t >= p.cap ? p.cap - 1 : t);
+// Cache row of (sequence b, token t) or -1 for an unmapped page. Idx is the
+// integer type of the index arithmetic (32-bit when every offset fits).
+template <typename Idx>
+__device__ __forceinline__ Idx kv_row(const KvParams& p, Idx b, Idx s, Idx* tok) {
+  const Idx cap = (Idx)p.cap;
+  int64_t t64 = p.indices ? (int64_t)p.indices[(int64_t)b * p.sel + s] : (int64_t)s;
+  if (t64 < 0) t64 += p.cap;
+  t64 = t64 < 0 ? 0 : (t64 >= p.cap ? p.cap - 1 : t64);
+  const Idx t = (Idx)t64;
   *tok = t;
-  if (!p.table) return b * p.cap + t;
-  const int64_t pg = p.table[b * p.pps + t / p.page];
-  if (pg < 0 || pg >= p.pool_pages) return -1;
-  return pg * p.page + t % p.page;
+  if (!p.table) return b * cap + t;
+  const Idx page = (Idx)p.page;
+  const int64_t pg = p.table[(int64_t)b * p.pps + t / page];
+  if (pg < 0 || pg >= p.pool_pages) return (Idx)-1;
+  return (Idx)pg * page + t % page;
 }
 
-__device__ __forceinline__ float kv_scale(const KvParams& p, int64_t b, int64_t t, int64_t row, int64_t g) {
-  const int64_t idx = p.scale_plane ? (b * p.groups + g) * p.cap + t : row * p.groups + g;
+template <typename Idx>
+__device__ __forceinline__ float kv_scale(const KvParams& p, Idx b, Idx t, Idx row, Idx g) {
+  const Idx groups = (Idx)p.groups;
+  const Idx idx = p.scale_plane ? (b * groups + g) * (Idx)p.cap + t : row * groups + g;
   return p.scale_bf16 ? bf16_to_float(reinterpret_cast<const uint16_t*>(p.scales)[idx])
                       : reinterpret_cast<const float*>(p.scales)[idx];
 }
 
 // Vector path: chans % 16 == 0, group % 16 == 0, 16-byte aligned rows.
+template <typename Idx>
 __global__ void __launch_bounds__(256) kv_read_vec_kernel(KvParams p, int64_t units) {
-  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (u >= units) return;
-  const int64_t per_row = p.chans / 16;
-  const int64_t rs = u / per_row;  // (b, s) flattened
-  const int64_t c = (u % per_row) * 16;
-  const int64_t b = rs / p.sel, s = rs % p.sel;
-  int64_t t;
-  const int64_t row = kv_row(p, b, s, &t);
+  const int64_t u64 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u64 >= units) return;
+  const Idx u = (Idx)u64;
+  const Idx per_row = (Idx)(p.chans / 16);
+  const Idx rs = u / per_row;  // (b, s) flattened
+  const Idx c = (u - rs * per_row) * 16;
+  const Idx sel = (Idx)p.sel;
+  const Idx b = rs / sel, s = rs - b * sel;
+  Idx t;
+  const Idx row = kv_row<Idx>(p, b, s, &t);
   u32x4 codes = {0u, 0u, 0u, 0u};
   float sc = 0.f;
-  if (row >= 0) {
-    codes = ld16_stream(p.codes + row * p.chans + c);
-    sc = kv_scale(p, b, t, row, c / p.group);
+  if (row != (Idx)-1) {
+    codes = ld16_stream(p.codes + (int64_t)row * p.chans + c);
+    sc = kv_scale<Idx>(p, b, t, row, c / (Idx)p.group);
   }
   if (p.out_bf16) {
     u32x4 o0, o1;
@@ -75,11 +85,11 @@ __global__ void __launch_bounds__(256) kv_read_vec_kernel(KvParams p, int64_t un
         o1[2 * (i - 2) + 1] = pack_bf16x2(v2, v3);
       }
     }
-    uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + rs * p.chans + c;
+    uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + (int64_t)rs * p.chans + c;
     __builtin_nontemporal_store(o0, reinterpret_cast<u32x4*>(o));
     __builtin_nontemporal_store(o1, reinterpret_cast<u32x4*>(o + 8));
   } else {
-    float* o = reinterpret_cast<float*>(p.out) + rs * p.chans + c;
+    float* o = reinterpret_cast<float*>(p.out) + (int64_t)rs * p.chans + c;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t w = codes[i];
@@ -97,9 +107,9 @@ __global__ void kv_read_scalar_kernel(KvParams p, int64_t total) {
   const int64_t rs = i / p.chans, c = i % p.chans;
   const int64_t b = rs / p.sel, s = rs % p.sel;
   int64_t t;
-  const int64_t row = kv_row(p, b, s, &t);
+  const int64_t row = kv_row<int64_t>(p, b, s, &t);
   float v = 0.f;
-  if (row >= 0) v = (float)p.codes[row * p.chans + c] * kv_scale(p, b, t, row, c / p.group);
+  if (row >= 0) v = (float)p.codes[row * p.chans + c] * kv_scale<int64_t>(p, b, t, row, c / p.group);
   if (p.out_bf16)
     reinterpret_cast<uint16_t*>(p.out)[i] = bf16_bits(v);
   else
@@ -279,7 +289,14 @@ extern "C" int q6moe_kv_read(const q6moe_kv_args* a, void* stream) {
   const bool vec = chans % 16 == 0 && a->group % 16 == 0 && aligned(a->codes, 16) && aligned(a->out, 16);
   if (vec) {
     const int64_t units = total / 16;
-    hipLaunchKernelGGL(kv_read_vec_kernel, dim3((unsigned)cdiv(units, 256)), dim3(256), 0, s, p, units);
+    // 32-bit index arithmetic when every element offset and cache row fits
+    const int64_t rows = a->page_table ? a->pool_pages * a->page_size : a->batch * p.cap;
+    const bool small = total < (1ll << 31) && rows * chans < (1ll << 31) &&
+                       a->batch * p.groups * p.cap < (1ll << 31);
+    if (small)
+      hipLaunchKernelGGL(kv_read_vec_kernel<uint32_t>, dim3((unsigned)cdiv(units, 256)), dim3(256), 0, s, p, units);
+    else
+      hipLaunchKernelGGL(kv_read_vec_kernel<int64_t>, dim3((unsigned)cdiv(units, 256)), dim3(256), 0, s, p, units);
   } else {
     hipLaunchKernelGGL(kv_read_scalar_kernel, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, s, p, total);
   }
