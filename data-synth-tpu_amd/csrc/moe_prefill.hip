@@ -50,6 +50,10 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Wave index as a wave-uniform (SGPR) value, so that row groups and the
+// weight addresses derived from it stay in scalar registers.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   asm volatile("" : "+v"(v));
   return v;
@@ -163,7 +167,7 @@ template <typename RowFn>
 __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
                                           const uint16_t* x, const uint32_t (&xoff)[kXDma], int K,
                                           int64_t expert, f32x4 (&acc)[kUnits][kTG]) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = wave_id(), lane = threadIdx.x & 63;
   const int j = lane & 15, jA = lane >> 4;
   uint8_t* xbuf = smem;
   uint8_t* wbuf = smem + 2 * kHalfBytes + wave * 2 * kWStage;
@@ -218,7 +222,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
 // (wave*kXDma + i)*64 + lane, i.e. token t = that/16, swizzled granule l%16.
 template <typename RowOf>
 __device__ __forceinline__ void x_offsets(uint32_t (&xoff)[kXDma], int K, RowOf row_of) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = wave_id(), lane = threadIdx.x & 63;
 #pragma unroll
   for (int i = 0; i < kXDma; ++i) {
     const int p = (wave * kXDma + i) * 64 + lane;
@@ -236,7 +240,7 @@ __global__ void __launch_bounds__(512, 2)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   Tile T;
   if (!tile_info(ws, blockIdx.y, T)) return;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = wave_id(), lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
   const int rgb = blockIdx.x * 8 + wave;  // this wave's row group (gate and up)
   uint32_t xoff[kXDma];
@@ -276,7 +280,7 @@ __global__ void __launch_bounds__(512, 2)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   Tile T;
   if (!tile_info(ws, blockIdx.y, T)) return;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = wave_id(), lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
   const int rgb = blockIdx.x * 16 + 2 * wave;  // this wave's two row groups
   uint32_t xoff[kXDma];
