@@ -304,7 +304,7 @@ def main():
             for n in ("gate", "up", "down")]
     layers = [base]
     for _ in range(args.layers - 1):
-        layers.append([type(t)(t.qtype, t.data.clone(), t.scales.clone(), t.rows, t.width) for t in base])
+        layers.append([type(t)(t.qtype, t.data.clone(), None, t.rows, t.width) for t in base])
     x = torch.from_numpy(L["x"]).to(dev).to(torch.bfloat16)
     ids = torch.from_numpy(L["ids"]).to(dev)
     w = torch.from_numpy(L["weights"]).to(dev).to(torch.bfloat16)

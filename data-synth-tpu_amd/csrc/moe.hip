@@ -439,12 +439,15 @@ static Proj make_proj(const q6moe_table& t, int rows, int k) {
   Proj p;
   p.data = t.data;
   p.dstride = t.data_stride;
-  p.scales = t.scales;
-  p.sstride = t.scale_stride;
   p.rows = rows;
   p.k = k;
   p.kb = (int)cdiv(k, kQK);
   return p;
+}
+
+// Bytes of one expert's unit-major table.
+static int64_t unit_table_bytes(int qtype, int64_t rows, int64_t k) {
+  return cdiv(rows, 16) * cdiv(k, kQK) * (qtype == Q6MOE_Q6_K ? kQ6Unit : kQ4Unit);
 }
 
 static int validate_table(const q6moe_table& t, const char* name, int64_t rows, int64_t k, int64_t experts) {
@@ -453,24 +456,15 @@ static int validate_table(const q6moe_table& t, const char* name, int64_t rows, 
     set_error(n + ": null data");
     return Q6MOE_ERR_INVALID;
   }
-  if (t.qtype == Q6MOE_Q6_K) {
-    const int64_t need = cdiv(rows, 64) * cdiv(k, 256) * kTileBytes;
-    const int64_t sneed = cdiv(rows, 64) * cdiv(k, 256) * 128;
-    if (!t.scales || !aligned(t.data, 16) || !aligned(t.scales, 2) || (experts > 1 && t.data_stride % 16) ||
-        (experts > 1 && t.scale_stride % 2) || (experts > 1 && t.data_stride < need) ||
-        (experts > 1 && t.scale_stride < sneed)) {
-      set_error(n + ": Q6_K tables need 16-byte aligned SoA planes with strides covering one expert");
-      return Q6MOE_ERR_INVALID;
-    }
-  } else if (t.qtype == Q6MOE_Q4_K) {
-    const int64_t need = rows * cdiv(k, 256) * 144;
-    if (!aligned(t.data, 16) || (experts > 1 && (t.data_stride % 16 || t.data_stride < need))) {
-      set_error(n + ": Q4_K tables need 16-byte aligned GGUF rows with strides covering one expert");
-      return Q6MOE_ERR_INVALID;
-    }
-  } else {
-    set_error(n + ": qtype must be Q6_K (SoA) or Q4_K");
+  if (t.qtype != Q6MOE_Q6_K && t.qtype != Q6MOE_Q4_K) {
+    set_error(n + ": qtype must be Q6_K or Q4_K");
     return Q6MOE_ERR_UNSUPPORTED;
+  }
+  const int64_t need = unit_table_bytes(t.qtype, rows, k);
+  if (!aligned(t.data, 16) || (experts > 1 && (t.data_stride % 16 || t.data_stride < need))) {
+    set_error(n + ": expert tables must be 16-byte aligned unit-major tables (q6moe_moe_pack) "
+                  "with a stride covering one expert");
+    return Q6MOE_ERR_INVALID;
   }
   return Q6MOE_OK;
 }
@@ -497,9 +491,86 @@ static void launch_phases(const Proj& g, const Proj& u, const Proj& d, const Tok
   }
 }
 
+// GGUF expert tables [experts][rows][K blocks][block bytes] -> unit-major
+// tables (layout in moe_common.h). One thread per 4 bytes of expert
+// blockIdx.y's table; the byte map is a permutation of each row's block bytes
+// (Q6_K: ql at 0, qh at 128, sub-scales at 192, FP16 d at 208, 210 bytes;
+// Q4_K: 144 bytes), padded with zero rows to a multiple of 16.
+template <int FMT>
+__global__ void __launch_bounds__(256) moe_pack_kernel(const uint8_t* __restrict__ raw, int64_t raw_stride, int rows,
+                                                       int kbs, uint8_t* __restrict__ dst, int64_t dst_stride,
+                                                       int64_t words) {
+  constexpr int U = UnitBytes<FMT>::value, BS = FMT == FMT_Q6 ? 210 : 144;
+  const int64_t wi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (wi >= words) return;
+  const int64_t e = blockIdx.y, o = wi * 4;
+  const int64_t unit = o / U;
+  const int ob = (int)(o - unit * U);
+  const int rg = (int)(unit / kbs), kb = (int)(unit - (int64_t)rg * kbs);
+  uint32_t v = 0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int b = ob + t;
+    int row, src;  // row within the group, byte within that row's block
+    if (FMT == FMT_Q6) {
+      if (b < 2048) {
+        row = (b >> 4) & 15;
+        src = 16 * (b >> 8) + (b & 15);
+      } else if (b < 3072) {
+        const int q = b - 2048;
+        row = (q >> 4) & 15;
+        src = 128 + 16 * (q >> 8) + (q & 15);
+      } else if (b < 3328) {
+        const int q = b - 3072;
+        row = q >> 4;
+        src = 192 + (q & 15);
+      } else {
+        const int q = b - 3328;
+        row = q >> 1;
+        src = 208 + (q & 1);
+      }
+    } else {
+      row = (b >> 4) & 15;
+      src = 16 * (b >> 8) + (b & 15);
+    }
+    const int r = rg * 16 + row;
+    const uint32_t byte = r < rows ? raw[e * raw_stride + ((int64_t)r * kbs + kb) * BS + src] : 0u;
+    v |= byte << (8 * t);
+  }
+  *reinterpret_cast<uint32_t*>(dst + e * dst_stride + o) = v;
+}
+
 }  // namespace q6moe
 
 using namespace q6moe;
+
+extern "C" size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width) {
+  if ((qtype != Q6MOE_Q6_K && qtype != Q6MOE_Q4_K) || rows < 1 || width < 1 || rows > (1 << 24) ||
+      width > (1 << 24))
+    return 0;
+  return (size_t)unit_table_bytes(qtype, rows, width);
+}
+
+extern "C" int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, int64_t rows, int64_t width,
+                              uint8_t* dst, void* stream) {
+  Q6MOE_REQUIRE(raw && dst, "moe_pack: null pointer");
+  Q6MOE_REQUIRE(qtype == Q6MOE_Q6_K || qtype == Q6MOE_Q4_K, "moe_pack: qtype must be Q6_K or Q4_K");
+  Q6MOE_REQUIRE(experts >= 1 && experts <= 65535 && rows >= 1 && width >= 1 && rows <= (1 << 24) &&
+                    width <= (1 << 24),
+                "moe_pack: bad shape");
+  Q6MOE_REQUIRE(aligned(dst, 16), "moe_pack: dst must be 16-byte aligned");
+  const int kbs = (int)cdiv(width, kQK);
+  const int64_t bytes = unit_table_bytes(qtype, rows, width);
+  const int64_t words = bytes / 4;
+  const dim3 grid((unsigned)cdiv(words, 256), (unsigned)experts);
+  if (qtype == Q6MOE_Q6_K)
+    hipLaunchKernelGGL(moe_pack_kernel<FMT_Q6>, grid, dim3(256), 0, (hipStream_t)stream, raw, rows * kbs * 210,
+                       (int)rows, kbs, dst, bytes, words);
+  else
+    hipLaunchKernelGGL(moe_pack_kernel<FMT_Q4K>, grid, dim3(256), 0, (hipStream_t)stream, raw, rows * kbs * 144,
+                       (int)rows, kbs, dst, bytes, words);
+  return check_launch("moe_pack_kernel");
+}
 
 extern "C" size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_t experts, int64_t hidden,
                                            int64_t intermediate, int64_t shared_intermediate) {

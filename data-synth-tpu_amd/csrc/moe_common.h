@@ -7,14 +7,42 @@ namespace q6moe {
 
 enum { FMT_Q6 = 0, FMT_Q4K = 1 };
 
+// Expert tables of the routed-expert kernels are unit-major: a unit is 16
+// output rows x one 256-wide K block, stored exactly as a wave stages it in
+// LDS, and an expert's units are ordered [row group][K block] so that a wave
+// streaming one row group over K reads one contiguous run.
+//   Q6_K unit (3360 B): ql   [0, 2048)    16-byte chunk c (0..7) of row j at 16*(16c + j)
+//                       qh   [2048, 3072) chunk c (0..3) of row j at 2048 + 16*(16c + j)
+//                       sc   [3072, 3328) row j's 16 sub-scales at 3072 + 16j
+//                       d    [3328, 3360) row j's FP16 scale at 3328 + 2j
+//   Q4_K unit (2304 B): chunk c (0..8) of row j's 144-byte block at 16*(16c + j)
+// (GGUF block byte orders: kaggle/glm53_offload/gguf_quant.py:115-173). Rows
+// past the matrix are zero.
+constexpr int kQ6Unit = 3360;
+constexpr int kQ4Unit = 2304;
+
+template <int FMT>
+struct UnitBytes;
+template <>
+struct UnitBytes<0> {
+  static constexpr int value = kQ6Unit;
+};
+template <>
+struct UnitBytes<1> {
+  static constexpr int value = kQ4Unit;
+};
+
 // One projection's expert table: [rows x k] per expert.
 struct Proj {
-  const uint8_t* data;
+  const uint8_t* data;  // expert e's units at data + e * dstride
   int64_t dstride;
-  const uint8_t* scales;
-  int64_t sstride;
   int rows, k, kb;
 };
+
+template <int FMT>
+__device__ __forceinline__ const uint8_t* unit_ptr(const Proj& p, int64_t e, int rgroup, int kb) {
+  return p.data + e * p.dstride + ((int64_t)rgroup * p.kb + kb) * UnitBytes<FMT>::value;
+}
 
 // Workspace views written by the routing kernel and read by the GEMM kernels.
 struct MoeWs {
@@ -95,11 +123,14 @@ template <>
 struct Unit<FMT_Q6> {
   Q6Raw r;
   __device__ __forceinline__ void load(const Proj& p, int64_t e, int rgroup, int kb, int lane) {
-    const int tile = rgroup >> 2;
-    const int row = (rgroup & 3) * 16 + (lane & 15);
-    const int64_t t = (int64_t)tile * p.kb + kb;
-    q6_load(r, p.data + e * p.dstride + t * kTileBytes, p.scales + e * p.sstride + t * 128, row,
-            lane >> 4);
+    const uint8_t* u = unit_ptr<FMT_Q6>(p, e, rgroup, kb);
+    const int j = lane & 15, jA = lane >> 4;
+    r.qlA = ld16_stream(u + 16 * (16 * jA + j));
+    r.qlB = ld16_stream(u + 16 * (16 * (jA + 4) + j));
+    r.qhA = ld16_stream(u + 2048 + 16 * (16 * (jA & 1) + j));
+    r.qhB = ld16_stream(u + 2048 + 16 * (16 * ((jA & 1) + 2) + j));
+    r.sc = ld16_stream(u + 3072 + 16 * j);
+    r.d = *reinterpret_cast<const uint16_t*>(u + 3328 + 2 * j);
   }
   __device__ __forceinline__ void decode(u32x4 a[8], int lane) const {
     q6_decode_unit(r, lane >> 4, a);
@@ -107,21 +138,20 @@ struct Unit<FMT_Q6> {
   static __device__ __forceinline__ int xoff(int f, int jA) { return q6_xfrag_offset(f, jA); }
 };
 
-// GGUF Q4_K rows [rows, KB, 144] (16-byte aligned blocks). Lane (row l%16,
-// chunk jA = l/16) decodes qs bytes [32jA, 32jA+32): low nibbles are sub-block
-// 2jA (positions 64jA + l), high nibbles sub-block 2jA+1 (64jA + 32 + l)
+// Q4_K unit. Lane (row l%16, chunk jA = l/16) decodes qs bytes [32jA, 32jA+32)
+// of its row's block (chunks 1+2jA and 2+2jA): low nibbles are sub-block 2jA
+// (positions 64jA + l), high nibbles sub-block 2jA+1 (64jA + 32 + l)
 // (kaggle/glm53_offload/gguf_quant.py:115-157). w = fma(q, d*sc, -dmin*m),
 // one rounding of the exact value, then RNE to BF16.
 template <>
 struct Unit<FMT_Q4K> {
   u32x4 hdr, qa, qb;
   __device__ __forceinline__ void load(const Proj& p, int64_t e, int rgroup, int kb, int lane) {
-    int row = rgroup * 16 + (lane & 15);
-    row = row < p.rows ? row : p.rows - 1;  // stay in bounds; result row discarded
-    const uint8_t* blk = p.data + e * p.dstride + ((int64_t)row * p.kb + kb) * 144;
-    hdr = ld16_stream(blk);
-    qa = ld16_stream(blk + 16 + 32 * (lane >> 4));
-    qb = ld16_stream(blk + 32 + 32 * (lane >> 4));
+    const uint8_t* u = unit_ptr<FMT_Q4K>(p, e, rgroup, kb);
+    const int j = lane & 15, jA = lane >> 4;
+    hdr = ld16_stream(u + 16 * j);
+    qa = ld16_stream(u + 16 * (16 * (1 + 2 * jA) + j));
+    qb = ld16_stream(u + 16 * (16 * (2 + 2 * jA) + j));
   }
   __device__ __forceinline__ void decode(u32x4 a[8], int lane) const {
     const int jA = lane >> 4;

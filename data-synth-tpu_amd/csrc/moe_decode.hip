@@ -41,11 +41,9 @@ constexpr int kStages = 3;
 constexpr int kDownRows = 3;  // 16-row groups of down per wave
 constexpr int kPassTokens = 16;  // routes per weight pass (MFMA columns)
 
-// One unit in LDS. Q6_K: ql 2048 B and qh 1024 B chunk-major (slot = chunk*16 +
-// row), sub-scales 256 B and FP16 d 32 B (+ padding) row-major. Q4_K: 16 rows x
-// 9 chunks of 16 B, chunk-major in three 1 KB groups.
+// One ring stage holds a unit as it lies in the table (Q6_K 3360 B, Q4_K
+// 2304 B), the Q6_K FP16 scales repeated up to the stage's end.
 constexpr int kUnitBytes = 3584;
-constexpr int kUnitDma = 5;  // DMA instructions per unit (both formats)
 constexpr int kXLoads = 8;   // token-operand loads per K block (one per MFMA)
 
 static_assert(kStages * kUnitBytes >= 8 * kDecMaxEntries + 4 * kDecMaxExperts,
@@ -95,15 +93,15 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 // Vector-memory instructions issued for unit p of P per K block: the unit's
-// DMA, plus the next K block's token operands with unit 0.
-template <int P>
+// D DMA instructions, plus the next K block's token operands with unit 0.
+template <int P, int D>
 constexpr int unit_ops(int p) {
-  return kUnitDma + (p % P == 0 ? kXLoads : 0);
+  return D + (p % P == 0 ? kXLoads : 0);
 }
-template <int P>
+template <int P, int D>
 constexpr int younger_ops(int p, int ahead) {
   int s = 0;
-  for (int i = 1; i <= ahead; ++i) s += unit_ops<P>(p + i);
+  for (int i = 1; i <= ahead; ++i) s += unit_ops<P, D>(p + i);
   return s;
 }
 
@@ -114,30 +112,26 @@ struct WStream;
 
 template <>
 struct WStream<FMT_Q6> {
-  const uint8_t* data;
-  const uint8_t* scales;
+  static constexpr int kDma = 5;  // DMA instructions per unit
+  const uint8_t* data;            // the expert's units
   int kbs;
-  uint32_t v_ql, v_qh, v_sc, v_d;  // per-lane byte offsets
+  uint32_t v16, v4, v_d;  // per-lane byte offsets
   __device__ __forceinline__ WStream(const Proj& p, int64_t e, int lane) {
     data = p.data + e * p.dstride;
-    scales = p.scales + e * p.sstride;
     kbs = p.kb;
-    const int j = lane & 15, c = lane >> 4;
-    v_ql = opaque(kQlOff + j * 128 + 16 * c);
-    v_qh = opaque(kQhOff + j * 64 + 16 * c);
-    v_sc = opaque(kScOff + 4 * lane);
+    v16 = opaque(16 * lane);
+    v4 = opaque(4 * lane);
     v_d = opaque(4 * (lane & 7));
   }
-  // rows 16*(rg%4).. of tile row rg/4, K block kb
+  // unit (row group rg, K block kb): one contiguous 3360-byte block copied as
+  // it lies (the FP16 scales repeat eight times over the stage's last 256 B)
   __device__ __forceinline__ void issue(int rg, int kb, uint8_t* st) const {
-    const int64_t t = (int64_t)(rg >> 2) * kbs + kb;
-    const int r0 = (rg & 3) * 16;
-    const uint8_t* tile = data + t * kTileBytes;
-    dma16(tile + r0 * 128, v_ql, st);
-    dma16(tile + r0 * 128 + 64, v_ql, st + 1024);
-    dma16(tile + r0 * 64, v_qh, st + 2048);
-    dma4(tile + r0 * 16, v_sc, st + 3072);
-    dma4(scales + t * 128 + r0 * 2, v_d, st + 3328);
+    const uint8_t* u = data + ((int64_t)rg * kbs + kb) * kQ6Unit;
+    dma16(u, v16, st);
+    dma16(u + 1024, v16, st + 1024);
+    dma16(u + 2048, v16, st + 2048);
+    dma4(u + 3072, v4, st + 3072);
+    dma4(u + 3328, v_d, st + 3328);
   }
   static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {
     const int j = lane & 15, jA = lane >> 4;
@@ -154,34 +148,26 @@ struct WStream<FMT_Q6> {
 
 template <>
 struct WStream<FMT_Q4K> {
-  // 16 GGUF rows (144 B each) of K block kb: chunk c (16 B) of row j goes to
-  // group c/4, slot (c%4)*16 + j. Chunk 0 is the header, chunks 1-8 the codes.
+  static constexpr int kDma = 3;
   const uint8_t* data;
-  int rows, row_bytes, j;
-  uint32_t v_c;
+  int kbs;
+  uint32_t v16, v4;
   __device__ __forceinline__ WStream(const Proj& p, int64_t e, int lane) {
     data = p.data + e * p.dstride;
-    rows = p.rows;
-    row_bytes = p.kb * 144;
-    j = lane & 15;
-    v_c = 16 * (lane >> 4);
+    kbs = p.kb;
+    v16 = opaque(16 * lane);
+    v4 = opaque(4 * lane);
   }
+  // unit: chunks 0-7 (2 KB) and chunk 8 (256 B), copied as they lie
   __device__ __forceinline__ void issue(int rg, int kb, uint8_t* st) const {
-    int row = rg * 16 + j;
-    row = row < rows ? row : rows - 1;  // stay in bounds; result row discarded
-    const uint32_t vo = opaque((uint32_t)(row * row_bytes)), voc = opaque(vo + v_c);
-    const uint8_t* blk = data + kb * 144;
-    dma16(blk, voc, st);
-    dma16(blk + 64, voc, st + 1024);
-    dma16(blk + 128, vo, st + 2048);  // chunk 8 (each lane group repeats it)
-    dma4(blk, vo, st + 3072);         // keeps kUnitDma uniform; not read
-    dma4(blk, vo, st + 3328);
+    const uint8_t* u = data + ((int64_t)rg * kbs + kb) * kQ4Unit;
+    dma16(u, v16, st);
+    dma16(u + 1024, v16, st + 1024);
+    dma4(u + 2048, v4, st + 2048);
   }
   static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {
     const int jj = lane & 15, jA = lane >> 4;
-    auto chunk = [&](int c) -> u32x4 {
-      return *reinterpret_cast<const u32x4*>(st + 1024 * (c >> 2) + 16 * ((c & 3) * 16 + jj));
-    };
+    auto chunk = [&](int c) -> u32x4 { return *reinterpret_cast<const u32x4*>(st + 16 * (c * 16 + jj)); };
     Unit<FMT_Q4K> u;
     u.hdr = chunk(0);
     u.qa = chunk(1 + 2 * jA);
@@ -254,7 +240,7 @@ __device__ __forceinline__ void stream_units(uint8_t* ring, int kbs, const XStre
       const int u = kb * P + p;
       issue_w(pv, kb + dkb, stage(u + 2));
       if constexpr (pv == 0) xs.load(xo, kb + 1);
-      wait_vm<younger_ops<P>(p, 2)>();
+      wait_vm<younger_ops<P, WStream<FMT>::kDma>(p, 2)>();
       compute(pc, u, xc);
     });
   };
@@ -265,7 +251,7 @@ __device__ __forceinline__ void stream_units(uint8_t* ring, int kbs, const XStre
       constexpr int ahead = P - 1 - p < 2 ? P - 1 - p : 2;
       const int u = kb * P + p;
       if constexpr (p + 2 < P) issue_w(p + 2, kb, stage(u + 2));
-      wait_vm<younger_ops<P>(p, ahead)>();
+      wait_vm<younger_ops<P, WStream<FMT>::kDma>(p, ahead)>();
       compute(pc, u, xc);
     });
   };

@@ -81,30 +81,27 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Per-lane offsets of a Q6_K half-unit DMA (lane l: row l%16, chunk l/16).
+// Per-lane offsets of a half-unit DMA.
 struct HalfUnitLane {
-  uint32_t ql, qh, sc, d;
+  uint32_t v16, v4, vd;
   __device__ __forceinline__ explicit HalfUnitLane(int lane) {
-    const int j = lane & 15, c = lane >> 4;
-    ql = opaque(kQlOff + j * 128 + 16 * c);
-    qh = opaque(kQhOff + j * 64 + 16 * (c & 1));
-    sc = opaque(kScOff + 4 * lane);
-    d = opaque(4 * (lane & 7));
+    v16 = opaque(16 * lane);
+    v4 = opaque(4 * lane);
+    vd = opaque(4 * (lane & 7));
   }
 };
 
-// Issue the K half h of row group rg, K block kb of expert table (data, scales)
-// into ``st`` (kHUnit bytes). ql: chunks 4h..4h+3 of each row (slot c*16+j);
-// qh: chunks 2h, 2h+1 (32 lanes); sub-scales and d of the 16 rows.
-__device__ __forceinline__ void issue_half_unit(const uint8_t* data, const uint8_t* scales, int kbs, int rg,
-                                                int kb, int h, const HalfUnitLane& L, int lane, uint8_t* st) {
-  const int64_t t = (int64_t)(rg >> 2) * kbs + kb;
-  const int r0 = (rg & 3) * 16;
-  const uint8_t* tile = data + t * kTileBytes;
-  dma16(tile + r0 * 128 + 64 * h, L.ql, st);
-  if (lane < 32) dma16(tile + r0 * 64 + 32 * h, L.qh, st + 1024);
-  dma4(tile + r0 * 16, L.sc, st + 1536);
-  dma4(scales + t * 128 + r0 * 2, L.d, st + 1792);
+// Issue the K half h of unit (row group rg, K block kb) of an expert's units
+// into ``st`` (kHUnit bytes): ql chunks 4h..4h+3 (1 KB), qh chunks 2h, 2h+1
+// (512 B, 32 lanes), the 16 rows' sub-scales and FP16 scales -- four
+// contiguous pieces of the unit.
+__device__ __forceinline__ void issue_half_unit(const uint8_t* units, int kbs, int rg, int kb, int h,
+                                                const HalfUnitLane& L, int lane, uint8_t* st) {
+  const uint8_t* u = units + ((int64_t)rg * kbs + kb) * kQ6Unit;
+  dma16(u + 1024 * h, L.v16, st);
+  if (lane < 32) dma16(u + 2048 + 512 * h, L.v16, st + 1024);
+  dma4(u + 3072, L.v4, st + 1536);
+  dma4(u + 3328, L.vd, st + 1792);
 }
 
 // The 4 A fragments of K half h (f = 4h..4h+3) from a half-unit in LDS.
@@ -181,8 +178,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
       const Proj& p = projs[unit_proj[u]];
-      issue_half_unit(p.data + expert * p.dstride, p.scales + expert * p.sstride, kbs, rg_of(u), kb, h, L, lane,
-                      ws + u * kHUnit);
+      issue_half_unit(p.data + expert * p.dstride, kbs, rg_of(u), kb, h, L, lane, ws + u * kHUnit);
     }
     uint8_t* xs = xbuf + (s & 1) * kHalfBytes + wave * kXDma * 1024;
 #pragma unroll

@@ -16,8 +16,9 @@ down projection, deterministic combine).
 
 Expert tables are either ``ExpertTable`` objects from ``pack_experts`` or, as
 in the reference, raw GGUF byte tables ``uint8 [E, bytes_per_expert]`` on the
-GPU; raw Q6_K tables are repacked on the device to the SoA layout once and
-cached per tensor version.
+GPU; raw tables are repacked on the device to the unit-major layout of the
+kernels (16 rows x one 256-wide K block per contiguous unit, bytes permuted
+only) once and cached per tensor version.
 """
 
 import ctypes
@@ -28,7 +29,6 @@ import numpy as np
 import torch
 
 from . import _lib
-from .layout import plane_sizes
 from .quant import BLOCK_LAYOUTS
 
 EXPERT_ROW_TILE = 128
@@ -39,9 +39,8 @@ SUPPORTED = ("Q6_K", "Q4_K")
 class ExpertTable:
     """One projection for all experts, resident on the GPU.
 
-    Q6_K: ``data`` [E, tiles*blocks*13312] and ``scales`` [E, scale bytes] (SoA,
-    layout q6_k_soa_n64_k256_v1 per expert). Q4_K: ``data`` [E, rows*blocks*144]
-    GGUF rows, ``scales`` None.
+    ``data`` [E, q6moe_moe_table_bytes] unit-major tables (Q6_K or Q4_K); the
+    scales live inside the units, so ``scales`` is None.
     """
 
     qtype: str
@@ -88,30 +87,27 @@ def pack_experts(raw, qtype, rows, width, device=None):
     if raw.dtype != torch.uint8:
         raise TypeError("expert tables must have dtype uint8")
     device = torch.device(device) if device is not None else (raw.device if raw.is_cuda else torch.device("cuda"))
-    raw = _raw_view(raw.to(device), qtype, rows, width)
+    raw = _raw_view(raw.to(device), qtype, rows, width).contiguous()
     experts = raw.shape[0]
-    if qtype == "Q4_K":
-        return ExpertTable(qtype, raw.reshape(experts, -1).contiguous(), None, rows, width)
-    dsize, ssize = plane_sizes(rows, width)
-    data = torch.empty((experts, dsize), dtype=torch.uint8, device=device)
-    scales = torch.empty((experts, ssize), dtype=torch.uint8, device=device)
     lib = _lib.load()
-    raw = raw.contiguous()
+    code = _lib.QTYPE_CODES[qtype]
+    size = int(lib.q6moe_moe_table_bytes(code, rows, width))
+    if size == 0:
+        raise ValueError(f"cannot pack a {qtype} table of [{rows}, {width}]")
+    data = torch.empty((experts, size), dtype=torch.uint8, device=device)
     with torch.cuda.device(device):
-        stream = _lib.stream_handle(device)
-        for e in range(experts):
-            rc = lib.q6moe_q6_pack(_lib.ptr(raw[e]), rows, width, _lib.ptr(data[e]), _lib.ptr(scales[e]), stream)
-            _lib.check(rc, "q6_pack")
-    return ExpertTable(qtype, data, scales, rows, width)
+        rc = lib.q6moe_moe_pack(_lib.ptr(raw), code, experts, rows, width, _lib.ptr(data), _lib.stream_handle(device))
+        _lib.check(rc, "moe_pack")
+    return ExpertTable(qtype, data, None, rows, width)
 
 
-def stacked_table(data, scales, qtype, rows, width):
-    """Wrap already-packed device planes ([E, D] data, [E, S] scales or None)."""
-    return ExpertTable(qtype, data, scales, rows, width)
+def stacked_table(data, qtype, rows, width):
+    """Wrap an already-packed device table [E, q6moe_moe_table_bytes] (from ``q6moe_moe_pack``)."""
+    return ExpertTable(qtype, data, None, rows, width)
 
 
 class _PackCache:
-    """Device repack of raw Q6_K tables, keyed by (pointer, version, shape)."""
+    """Device repack of raw GGUF expert tables, keyed by (pointer, version, shape)."""
 
     def __init__(self):
         self.entries = {}
@@ -140,9 +136,6 @@ def _as_table(t, qtype, rows, width, name):
         raise ValueError(f"{name} must be an ExpertTable or a uint8 GPU tensor [experts, bytes]")
     if t.dtype != torch.uint8:
         raise TypeError("expert tables must have dtype uint8")
-    if qtype == "Q4_K":
-        raw = _raw_view(t, qtype, rows, width)
-        return ExpertTable(qtype, raw.reshape(raw.shape[0], -1), None, rows, width)
     return _CACHE.get(t, qtype, rows, width)
 
 

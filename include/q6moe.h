@@ -95,13 +95,30 @@ int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, int64_t width
 /* Routed SwiGLU expert FFN (expert_parallel / grouped_expert_parallel).     */
 /* ------------------------------------------------------------------------ */
 
+/*
+ * Expert tables of the routed FFN are unit-major, packed once from the GGUF
+ * tables the reference keeps per expert ([E, bytes_per_expert], raw Q6_K or
+ * Q4_K rows; kaggle/qwen38_tpu/parallel.py:40-87). A unit is 16 output rows x
+ * one 256-wide K block with the bytes of those 16 row blocks permuted into
+ * 16-byte chunks (Q6_K 3360 bytes, Q4_K 2304 bytes; rows padded with zeros to
+ * a multiple of 16); an expert's units run [row group][K block]. The
+ * permutation moves bytes only, so decoded values are those of the GGUF rows.
+ */
+size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width); /* per expert; 0 if invalid */
+
+/* raw [experts][rows][ceil(width/256)][210 or 144] -> dst [experts][table bytes]
+   (dst 16-byte aligned). No counterpart call in the reference, whose matmul
+   reads GGUF bytes directly; this is its one-time load-side preparation. */
+int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, int64_t rows, int64_t width,
+                   uint8_t* dst, void* stream);
+
 /* Weight tables of one projection for all experts. */
 typedef struct q6moe_table {
-  int qtype;                /* Q6MOE_Q6_K (SoA planes) or Q6MOE_Q4_K (raw GGUF rows) */
-  const uint8_t* data;      /* expert e starts at data + e * data_stride */
-  int64_t data_stride;      /* bytes between experts */
-  const uint8_t* scales;    /* Q6_K: FP16 scale plane of expert e at scales + e * scale_stride */
-  int64_t scale_stride;     /* Q4_K: unused (NULL / 0) */
+  int qtype;                /* Q6MOE_Q6_K or Q6MOE_Q4_K */
+  const uint8_t* data;      /* unit-major table of expert e at data + e * data_stride */
+  int64_t data_stride;      /* bytes between experts (>= q6moe_moe_table_bytes, multiple of 16) */
+  const uint8_t* scales;    /* unused (NULL): the scales live in the units */
+  int64_t scale_stride;     /* unused (0) */
 } q6moe_table;
 
 typedef struct q6moe_moe_args {

@@ -155,3 +155,35 @@ def test_route_weights_match_oracle_merging(device):
     r = oracle_routing.route_weights(ids, w, 2)
     assert r[0, 1] == 0.625 and r[1, 0] == 1.0
     assert_moe_close(got, _oracle(L, ids=ids, weights=w))
+
+
+def _unit_major(raw, qtype, rows, width):
+    """The unit-major expert table, restated with NumPy: units of 16 rows x one
+    256-wide K block ordered [row group][K block]; inside a unit, 16-byte chunk
+    c of row j at 16*(16c + j) (Q6_K: ql chunks, then qh chunks, then the rows'
+    16 sub-scales and FP16 scales row by row); rows padded with zeros."""
+    bs = 210 if qtype == "Q6_K" else 144
+    E, kbs, groups = raw.shape[0], -(-width // 256), -(-rows // 16)
+    pad = np.zeros((E, groups * 16, kbs, bs), np.uint8)
+    pad[:, :rows] = raw.reshape(E, rows, kbs, bs)
+    blk = pad.reshape(E, groups, 16, kbs, bs).transpose(0, 1, 3, 2, 4)  # [E, g, kb, row, bs]
+
+    def chunk_major(a, chunks):
+        return a.reshape(E, groups, kbs, 16, chunks, 16).transpose(0, 1, 2, 4, 3, 5).reshape(E, groups, kbs, -1)
+
+    if qtype == "Q6_K":
+        unit = np.concatenate([chunk_major(blk[..., :128], 8), chunk_major(blk[..., 128:192], 4),
+                               blk[..., 192:208].reshape(E, groups, kbs, 256),
+                               blk[..., 208:210].reshape(E, groups, kbs, 32)], axis=-1)
+    else:
+        unit = chunk_major(blk, 9)
+    return unit.reshape(E, -1)
+
+
+@pytest.mark.parametrize("qtype", ["Q6_K", "Q4_K"])
+@pytest.mark.parametrize("rows,width", [(40, 512), (16, 256), (33, 768)])
+def test_pack_is_the_unit_major_byte_permutation(device, qtype, rows, width):
+    bs = 210 if qtype == "Q6_K" else 144
+    raw = np.random.default_rng(rows + width).integers(0, 256, size=(3, rows * (width // 256) * bs), dtype=np.uint8)
+    table = pack_experts(raw, qtype, rows, width, device)
+    np.testing.assert_array_equal(table.data.cpu().numpy(), _unit_major(raw, qtype, rows, width))
