@@ -117,7 +117,7 @@ __device__ __forceinline__ void decode_half(const uint8_t* st, int h, int lane, 
     const int g = 2 * h + gg;
     const int scv = (int)(int8_t)((sc[g] >> sh) & 0xff);
     const float ds = d * (float)scv;
-    const float nds = -32.f * ds;
+    const float n1056 = -1056.f * ds;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const uint32_t h0 = qh[2 * e] >> (2 * q0), h1 = qh[2 * e + 1] >> (2 * q0);
@@ -129,7 +129,7 @@ __device__ __forceinline__ void decode_half(const uint8_t* st, int h, int lane, 
         c0 = q6_codes_lo(ql[2 * e], h0);
         c1 = q6_codes_lo(ql[2 * e + 1], h1);
       }
-      a[2 * gg + e] = q6_frag(c0, c1, ds, nds);
+      a[2 * gg + e] = q6_frag_mix(c0, c1, ds, n1056);
     }
   }
 }

@@ -79,6 +79,30 @@ __device__ __forceinline__ u32x4 q6_frag(uint32_t c0, uint32_t c1, float ds, flo
   return r;
 }
 
+// q6_frag for Q6_K codes with two VALU fewer per four weights: each code byte
+// c becomes the FP16 value 1024 + c (bits 0x6400 | c, exact, one v_perm per
+// two codes) and v_fma_mix_f32 computes (1024 + c) * ds + n1056 with
+// n1056 = -1056 * ds. ds = d * sc has at most 18 significant bits (11-bit FP16
+// significand, |sc| <= 128), so n1056 (x 33 * 32) is exact in FP32, and the
+// single rounding of the exact ds * (c - 32) returns it unchanged: the value
+// and the +0 for c = 32 match q6_frag bit for bit.
+__device__ __forceinline__ float h16_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)v); }
+__device__ __forceinline__ float h16_hi(uint32_t v) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+}
+__device__ __forceinline__ u32x4 q6_frag_mix(uint32_t c0, uint32_t c1, float ds, float n1056) {
+  const uint32_t h0 = __builtin_amdgcn_perm(0x64646464u, c0, 0x04010400u);  // codes 0, 1
+  const uint32_t h1 = __builtin_amdgcn_perm(0x64646464u, c0, 0x04030402u);  // codes 2, 3
+  const uint32_t h2 = __builtin_amdgcn_perm(0x64646464u, c1, 0x04010400u);
+  const uint32_t h3 = __builtin_amdgcn_perm(0x64646464u, c1, 0x04030402u);
+  u32x4 r;
+  r[0] = pack_bf16x2(__builtin_fmaf(h16_lo(h0), ds, n1056), __builtin_fmaf(h16_hi(h0), ds, n1056));
+  r[1] = pack_bf16x2(__builtin_fmaf(h16_lo(h1), ds, n1056), __builtin_fmaf(h16_hi(h1), ds, n1056));
+  r[2] = pack_bf16x2(__builtin_fmaf(h16_lo(h2), ds, n1056), __builtin_fmaf(h16_hi(h2), ds, n1056));
+  r[3] = pack_bf16x2(__builtin_fmaf(h16_lo(h3), ds, n1056), __builtin_fmaf(h16_hi(h3), ds, n1056));
+  return r;
+}
+
 __device__ __forceinline__ u32x4 q6_frag_exact(uint32_t c0, uint32_t c1, float ds) {
   u32x4 r;
   r[0] = pack_bf16x2(ds * (ubyte_f(c0, 0) - 32.f), ds * (ubyte_f(c0, 1) - 32.f));
@@ -150,7 +174,7 @@ __device__ __forceinline__ void q6_decode_unit(const Q6Raw& r, int jA, u32x4 a[8
   for (int g = 0; g < 4; ++g) {
     const int scv = (int)(int8_t)((r.sc[g] >> sh) & 0xff);
     const float ds = d * (float)scv;
-    const float nds = -32.f * ds;
+    const float n1056 = -1056.f * ds;
     const u32x4& ql = (g >> 1) ? r.qlB : r.qlA;
     const u32x4& qh = (g >> 1) ? r.qhB : r.qhA;
 #pragma unroll
@@ -164,7 +188,7 @@ __device__ __forceinline__ void q6_decode_unit(const Q6Raw& r, int jA, u32x4 a[8
         c0 = q6_codes_lo(ql[2 * e], h0);
         c1 = q6_codes_lo(ql[2 * e + 1], h1);
       }
-      a[2 * g + e] = kExact ? q6_frag_exact(c0, c1, ds) : q6_frag(c0, c1, ds, nds);
+      a[2 * g + e] = kExact ? q6_frag_exact(c0, c1, ds) : q6_frag_mix(c0, c1, ds, n1056);
     }
   }
 }
