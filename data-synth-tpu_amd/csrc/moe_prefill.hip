@@ -2,22 +2,23 @@
 //
 // The routing kernel (moe.hip) groups the routes by expert (ascending id,
 // tokens ascending) and splits each expert's routes into tiles of 128. One
-// workgroup computes a 128-route tile against a block of output rows:
+// workgroup (4 waves, one per SIMD; two workgroups per CU) computes a
+// 128-route tile against a block of output rows:
 //
-//   moe_pf_gate_up_kernel  128 intermediate rows (gate and up) per workgroup;
+//   moe_pf_gate_up_kernel  64 intermediate rows (gate and up) per workgroup;
 //        g = RNE(x Wg^T), u = RNE(x Wu^T), a = RNE(RNE(g*sigmoid(g))*u)
 //        (kaggle/qwen38_tpu/experts.py:103-107, grouped_experts.py:96-101).
-//   moe_pf_down_kernel     256 hidden rows per workgroup; y = RNE(a Wd^T)
+//   moe_pf_down_kernel     128 hidden rows per workgroup; y = RNE(a Wd^T)
 //        (experts.py:108). The combine kernel in moe.hip sums f32(y)*f32(r).
 //
-// Each of the 8 waves (two per SIMD, so one wave's decode overlaps the
-// other's MFMAs) owns 2 units (16 weight rows x one 256-wide K block) per K
-// block and decodes them straight into MFMA A operands; decoded weights
-// never leave registers. The 128 token rows of the current K half
-// sit in LDS (double-buffered, XOR-swizzled so the 16 token columns of an
-// MFMA read hit distinct banks) and every wave multiplies them against its
-// own rows. Both the token half-tiles and the packed weight half-units come
-// in by direct global->LDS DMA, two K halves ahead of their use.
+// Each wave owns 2 units (16 weight rows x one 256-wide K block) per K block,
+// loads their bytes into registers one K half ahead and decodes them straight
+// into MFMA A operands; decoded weights never leave registers. The 128 token
+// rows of the current K half sit in LDS (double-buffered, XOR-swizzled so the
+// 16 token columns of an MFMA read hit distinct banks), filled by direct
+// global->LDS DMA, and every wave multiplies them against its own rows. The
+// two workgroups of a CU run out of step, so one's decode (VALU) overlaps the
+// other's MFMAs.
 #include <type_traits>
 
 #include "moe_common.h"
@@ -29,16 +30,17 @@ namespace q6moe {
 
 namespace pf {
 
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;
 constexpr int kM = 128;            // routes per tile (MFMA column groups of 16)
 constexpr int kTG = kM / 16;       // token groups
 constexpr int kUnits = 2;          // units per wave per K block
 constexpr int kHalfBytes = kM * 128 * 2;  // one K half of the token tile (32 KB)
-constexpr int kHUnit = 2048;       // packed half-unit in LDS: ql 1024, qh 512, sc 256, d 256
-constexpr int kWStage = kUnits * kHUnit;
-constexpr int kWDma = 4;           // DMA instructions per half-unit
 constexpr int kXDma = kHalfBytes / 1024 / kWaves;  // token DMA instructions per wave per half
-constexpr int kLds = 2 * kHalfBytes + kWaves * 2 * kWStage;
+constexpr int kAhead = 1;          // K halves in flight beyond the one being multiplied
+constexpr int kXStages = kAhead + 1;
+constexpr int kWLoads = 4;         // weight loads per unit per K half (ql, qh, sub-scales, d)
+constexpr int kStepOps = kUnits * kWLoads + kXDma;  // vector-memory instructions per K half per wave
+constexpr int kLds = kXStages * kHalfBytes;
 
 static_assert(kLds <= 160 * 1024, "LDS budget");
 
@@ -81,53 +83,45 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Per-lane offsets of a half-unit DMA.
-struct HalfUnitLane {
-  uint32_t v16, v4, vd;
-  __device__ __forceinline__ explicit HalfUnitLane(int lane) {
-    v16 = opaque(16 * lane);
-    v4 = opaque(4 * lane);
-    vd = opaque(4 * (lane & 7));
-  }
+// The weights of one unit for one K half, in the registers of the lane that
+// decodes them (row j = lane % 16, k-group jA = lane / 16): ql chunk 4h + jA,
+// qh chunk 2h + jA % 2, the row's 16 sub-scales and its FP16 scale.
+struct HalfRegs {
+  u32x4 ql, qh, sc;
+  uint32_t d;
 };
 
-// Issue the K half h of unit (row group rg, K block kb) of an expert's units
-// into ``st`` (kHUnit bytes): ql chunks 4h..4h+3 (1 KB), qh chunks 2h, 2h+1
-// (512 B, 32 lanes), the 16 rows' sub-scales and FP16 scales -- four
-// contiguous pieces of the unit.
-__device__ __forceinline__ void issue_half_unit(const uint8_t* units, int kbs, int rg, int kb, int h,
-                                                const HalfUnitLane& L, int lane, uint8_t* st) {
+__device__ __forceinline__ void load_half(const uint8_t* units, int kbs, int rg, int kb, int h, int lane,
+                                          HalfRegs& r) {
   const uint8_t* u = units + ((int64_t)rg * kbs + kb) * kQ6Unit;
-  dma16(u + 1024 * h, L.v16, st);
-  if (lane < 32) dma16(u + 2048 + 512 * h, L.v16, st + 1024);
-  dma4(u + 3072, L.v4, st + 1536);
-  dma4(u + 3328, L.vd, st + 1792);
+  const int j = lane & 15, jA = lane >> 4;
+  r.ql = ld16_stream(u + 1024 * h + 16 * lane);
+  r.qh = ld16_stream(u + 2048 + 512 * h + 16 * ((jA & 1) * 16 + j));
+  r.sc = ld16_stream(u + 3072 + 16 * j);
+  r.d = *reinterpret_cast<const uint16_t*>(u + 3328 + 2 * j);
 }
 
-// The 4 A fragments of K half h (f = 4h..4h+3) from a half-unit in LDS.
-__device__ __forceinline__ void decode_half(const uint8_t* st, int h, int lane, u32x4 a[4]) {
-  const int j = lane & 15, jA = lane >> 4;
-  const u32x4 ql = *reinterpret_cast<const u32x4*>(st + 16 * (jA * 16 + j));
-  const u32x4 qh = *reinterpret_cast<const u32x4*>(st + 1024 + 16 * ((jA & 1) * 16 + j));
-  const u32x4 sc = *reinterpret_cast<const u32x4*>(st + 1536 + 16 * j);
-  const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(st + 1792 + 2 * j));
+// The 4 A fragments of K half h (f = 4h..4h+3) of a unit.
+__device__ __forceinline__ void decode_half(const HalfRegs& w, int h, int lane, u32x4 a[4]) {
+  const int jA = lane >> 4;
+  const float d = half_bits_to_float(w.d);
   const int q0 = jA >> 1, sh = 8 * jA;
 #pragma unroll
   for (int gg = 0; gg < 2; ++gg) {
     const int g = 2 * h + gg;
-    const int scv = (int)(int8_t)((sc[g] >> sh) & 0xff);
+    const int scv = (int)(int8_t)((w.sc[g] >> sh) & 0xff);
     const float ds = d * (float)scv;
     const float n1056 = -1056.f * ds;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const uint32_t h0 = qh[2 * e] >> (2 * q0), h1 = qh[2 * e + 1] >> (2 * q0);
+      const uint32_t h0 = w.qh[2 * e] >> (2 * q0), h1 = w.qh[2 * e + 1] >> (2 * q0);
       uint32_t c0, c1;
       if (gg) {
-        c0 = q6_codes_hi(ql[2 * e], h0);
-        c1 = q6_codes_hi(ql[2 * e + 1], h1);
+        c0 = q6_codes_hi(w.ql[2 * e], h0);
+        c1 = q6_codes_hi(w.ql[2 * e + 1], h1);
       } else {
-        c0 = q6_codes_lo(ql[2 * e], h0);
-        c1 = q6_codes_lo(ql[2 * e + 1], h1);
+        c0 = q6_codes_lo(w.ql[2 * e], h0);
+        c1 = q6_codes_lo(w.ql[2 * e + 1], h1);
       }
       a[2 * gg + e] = q6_frag_mix(c0, c1, ds, n1056);
     }
@@ -148,6 +142,24 @@ struct Tile {
   int r0, nv;  // first route position, valid routes (<= kM)
 };
 
+// Work item of workgroup blockIdx.x: (tile, column block), column block
+// fastest. Workgroup i runs on XCD i % 8 (round-robin dispatch), so the items
+// are split into eight contiguous runs, one per XCD, each walked in dispatch
+// order: the workgroups that share a token tile (its column blocks) or an
+// expert's weights (its tiles) run on one XCD at the same time and share its
+// L2. Returns false past the last item.
+__device__ __forceinline__ bool pf_item(const MoeWs& ws, int ncol, int& tile, int& col) {
+  const int ntiles = ws.hdr[2];
+  const int items = ntiles * ncol;
+  const int run = (items + 7) >> 3;
+  const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int item = xcd * run + k;
+  if (k >= run || item >= items) return false;
+  tile = item / ncol;
+  col = item - tile * ncol;
+  return true;
+}
+
 __device__ __forceinline__ bool tile_info(const MoeWs& ws, int tile, Tile& T) {
   if (tile >= ws.hdr[2]) return false;
   const int slot = ws.tile_slot[tile];
@@ -158,47 +170,55 @@ __device__ __forceinline__ bool tile_info(const MoeWs& ws, int tile, Tile& T) {
   return true;
 }
 
-// The streaming core shared by both kernels. ``rows(u)`` gives unit u's row
-// group; ``xrow(t)`` the row of token-tile row t in the [*, K] BF16 matrix x.
+// The streaming core shared by both kernels. ``rg_of(u)`` gives unit u's row
+// group; the token tile's rows come in by DMA at the per-lane offsets xoff.
+// K half s (block s/2, half s%2) is step s. Each wave loads its own weights
+// into registers and DMAs its share of the token tile into LDS stage
+// s % kXStages, kAhead steps before it is multiplied; one workgroup barrier
+// per step makes every wave's share visible and frees the stage read in the
+// step before.
 template <typename RowFn>
 __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
                                           const uint16_t* x, const uint32_t (&xoff)[kXDma], int K,
                                           int64_t expert, f32x4 (&acc)[kUnits][kTG]) {
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int j = lane & 15, jA = lane >> 4;
-  uint8_t* xbuf = smem;
-  uint8_t* wbuf = smem + 2 * kHalfBytes + wave * 2 * kWStage;
   const int kbs = K / kQK;
   const int S = 2 * kbs;
-  const HalfUnitLane L(lane);
   const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
-  auto issue = [&](int s) {
-    const int kb = s >> 1, h = s & 1;
-    uint8_t* ws = wbuf + (s & 1) * kWStage;
+  const uint8_t* units[kUnits];
+  int rgs[kUnits];
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) {
-      const Proj& p = projs[unit_proj[u]];
-      issue_half_unit(p.data + expert * p.dstride, kbs, rg_of(u), kb, h, L, lane, ws + u * kHUnit);
-    }
-    uint8_t* xs = xbuf + (s & 1) * kHalfBytes + wave * kXDma * 1024;
+  for (int u = 0; u < kUnits; ++u) {
+    const Proj& p = projs[unit_proj[u]];
+    units[u] = p.data + expert * p.dstride;
+    rgs[u] = rg_of(u);
+  }
+  HalfRegs wr[kXStages][kUnits];
+  auto issue = [&](int s, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+    const int kb = s >> 1, h = s & 1;
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) load_half(units[u], kbs, rgs[u], kb, h, lane, wr[slot][u]);
+    uint8_t* xs = smem + slot * kHalfBytes + wave * kXDma * 1024;
 #pragma unroll
     for (int i = 0; i < kXDma; ++i) dma16(xb + (int64_t)(kb * kQK + h * 128) * 2, xoff[i], xs + i * 1024);
   };
-  constexpr int kOps = kUnits * kWDma + kXDma;  // DMA instructions per half-step per wave
-  issue(0);
-  if (S > 1) issue(1);
-  for (int s = 0; s < S; ++s) {
-    if (s + 1 < S)
-      wait_vm<kOps>();
-    else
-      wait_vm<0>();
-    wg_barrier();  // every wave's share of this half's token tile has landed
+  auto step = [&](int s, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;
+    // this step's loads have landed once at most the younger steps' remain
+    const int younger = S - 1 - s < kAhead - 1 ? S - 1 - s : kAhead - 1;
+    static_for<0, kAhead>([&](auto yc) {
+      constexpr int y = decltype(yc)::value;
+      if (younger == y) wait_vm<y * kStepOps>();
+    });
+    wg_barrier();  // every wave's share of this step's tile is in LDS; the oldest stage is free
+    if (s + kAhead < S) issue(s + kAhead, std::integral_constant<int, (slot + kAhead) % kXStages>{});
     const int h = s & 1;
-    const uint8_t* xs = xbuf + (s & 1) * kHalfBytes;
-    const uint8_t* ws = wbuf + (s & 1) * kWStage;
+    const uint8_t* xs = smem + slot * kHalfBytes;
     u32x4 a[kUnits][4];
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) decode_half(ws + u * kHUnit, h, lane, a[u]);
+    for (int u = 0; u < kUnits; ++u) decode_half(wr[slot][u], h, lane, a[u]);
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
       const int c = xfrag_gran(f, jA);
@@ -209,8 +229,14 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
         for (int u = 0; u < kUnits; ++u) acc[u][tg] = mfma16(a[u][f], xv, acc[u][tg]);
       }
     }
-    wg_barrier();  // every wave is done with this stage
-    if (s + 2 < S) issue(s + 2);
+  };
+  static_for<0, kAhead>([&](auto ic) {
+    if (decltype(ic)::value < S) issue(decltype(ic)::value, ic);
+  });
+  for (int s0 = 0; s0 < S; s0 += kXStages) {
+    static_for<0, kXStages>([&](auto ic) {
+      if (s0 + decltype(ic)::value < S) step(s0 + decltype(ic)::value, ic);
+    });
   }
 }
 
@@ -229,16 +255,17 @@ __device__ __forceinline__ void x_offsets(uint32_t (&xoff)[kXDma], int K, RowOf 
 
 }  // namespace pf
 
-__global__ void __launch_bounds__(512, 2)
+__global__ void __launch_bounds__(64 * pf::kWaves, 2)
     moe_pf_gate_up_kernel(Proj gate, Proj up, MoeWs ws, const uint16_t* __restrict__ x, int hidden,
                           uint16_t* __restrict__ act, int inter) {
   using namespace pf;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   Tile T;
-  if (!tile_info(ws, blockIdx.y, T)) return;
+  int tile, col;
+  if (!pf_item(ws, inter / (16 * kWaves), tile, col) || !tile_info(ws, tile, T)) return;
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
-  const int rgb = blockIdx.x * 8 + wave;  // this wave's row group (gate and up)
+  const int rgb = col * kWaves + wave;  // this wave's row group (gate and up)
   uint32_t xoff[kXDma];
   x_offsets(xoff, hidden, [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; });
   const Proj projs[2] = {gate, up};
@@ -269,16 +296,17 @@ __global__ void __launch_bounds__(512, 2)
   }
 }
 
-__global__ void __launch_bounds__(512, 2)
+__global__ void __launch_bounds__(64 * pf::kWaves, 2)
     moe_pf_down_kernel(Proj down, MoeWs ws, const uint16_t* __restrict__ act, int inter,
                        uint16_t* __restrict__ y, int hidden) {
   using namespace pf;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   Tile T;
-  if (!tile_info(ws, blockIdx.y, T)) return;
+  int tile, col;
+  if (!pf_item(ws, hidden / (32 * kWaves), tile, col) || !tile_info(ws, tile, T)) return;
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
-  const int rgb = blockIdx.x * 16 + 2 * wave;  // this wave's two row groups
+  const int rgb = col * 2 * kWaves + 2 * wave;  // this wave's two row groups
   uint32_t xoff[kXDma];
   x_offsets(xoff, inter, [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); });
   const Proj projs[1] = {down};
@@ -319,10 +347,11 @@ int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs&
     hipFuncSetAttribute((const void*)moe_pf_down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
     attr_done = true;
   }
-  hipLaunchKernelGGL(moe_pf_gate_up_kernel, dim3((unsigned)(I / 128), (unsigned)max_tiles), dim3(64 * pf::kWaves), pf::kLds,
+  const auto grid = [&](int ncol) { return dim3((unsigned)(((int64_t)ncol * max_tiles + 7) / 8 * 8)); };
+  hipLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds,
                      s, g, u, ws, x, H, ws.act, I);
   if (after_gate_up) hipEventRecord((hipEvent_t)after_gate_up, s);
-  hipLaunchKernelGGL(moe_pf_down_kernel, dim3((unsigned)(H / 256), (unsigned)max_tiles), dim3(64 * pf::kWaves), pf::kLds, s,
+  hipLaunchKernelGGL(moe_pf_down_kernel, grid(H / (32 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds, s,
                      d, ws, ws.act, I, ws.y, H);
   return Q6MOE_OK;
 }
