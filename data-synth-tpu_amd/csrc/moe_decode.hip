@@ -211,22 +211,22 @@ struct XStream {
   }
 };
 
-// Streams P units per K block over kbs K blocks through the wave's ring:
-// unit (kb, p) is DMA'd by issue_w(p, kb, stage) and multiplied into acc[p].
+// Streams P units per K block over the kbs K blocks kb0.. through the wave's
+// ring: unit (kb, p) is DMA'd by issue_w(p, kb, stage) and multiplied into acc[p].
 // The token operands of K block kb are loaded with unit (kb, 0), one K block
 // ahead of their use, into the register set of kb's parity. The steady-state
 // loop issues unconditionally so that the compiler's own wait counts for the
 // token operands stay exact across the back edge.
 template <int FMT, bool kFullK, int P, typename IssueW>
-__device__ __forceinline__ void stream_units(uint8_t* ring, int kbs, const XStream<FMT, kFullK>& xs,
+__device__ __forceinline__ void stream_units(uint8_t* ring, int kb0, int kbs, const XStream<FMT, kFullK>& xs,
                                              IssueW&& issue_w, f32x4 (&acc)[P]) {
   static_assert(kStages == 3 && P >= kStages - 1, "one K block of token operands in flight");
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   u32x4 xA[8], xB[8];
   auto stage = [&](int u) { return ring + (u % kStages) * kUnitBytes; };
   auto compute = [&](auto pc, int u, u32x4(&xc)[8]) {
     constexpr int p = decltype(pc)::value;
-    if constexpr (p == 0) xs.mask(xc, u / P);
+    if constexpr (p == 0) xs.mask(xc, kb0 + u / P);
     u32x4 a[8];
     WStream<FMT>::decode(stage(u), lane, a);
 #pragma unroll
@@ -238,8 +238,8 @@ __device__ __forceinline__ void stream_units(uint8_t* ring, int kbs, const XStre
       constexpr int p = decltype(pc)::value;
       constexpr int pv = (p + 2) % P, dkb = (p + 2) / P;
       const int u = kb * P + p;
-      issue_w(pv, kb + dkb, stage(u + 2));
-      if constexpr (pv == 0) xs.load(xo, kb + 1);
+      issue_w(pv, kb0 + kb + dkb, stage(u + 2));
+      if constexpr (pv == 0) xs.load(xo, kb0 + kb + 1);
       wait_vm<younger_ops<P, WStream<FMT>::kDma>(p, 2)>();
       compute(pc, u, xc);
     });
@@ -250,14 +250,14 @@ __device__ __forceinline__ void stream_units(uint8_t* ring, int kbs, const XStre
       constexpr int p = decltype(pc)::value;
       constexpr int ahead = P - 1 - p < 2 ? P - 1 - p : 2;
       const int u = kb * P + p;
-      if constexpr (p + 2 < P) issue_w(p + 2, kb, stage(u + 2));
+      if constexpr (p + 2 < P) issue_w(p + 2, kb0 + kb, stage(u + 2));
       wait_vm<younger_ops<P, WStream<FMT>::kDma>(p, ahead)>();
       compute(pc, u, xc);
     });
   };
-  issue_w(0, 0, stage(0));
-  xs.load(xA, 0);
-  issue_w(1, 0, stage(1));  // P >= 2: unit (0, 1)
+  issue_w(0, kb0, stage(0));
+  xs.load(xA, kb0);
+  issue_w(1, kb0, stage(1));  // P >= 2: unit (0, 1)
   int kb = 0;
   for (; kb + 2 < kbs; kb += 2) {
     steady(kb, xA, xB);
@@ -281,7 +281,7 @@ struct SlotRoute {
 
 __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTables& T, uint8_t* scratch,
                           int* tok, SlotRoute& out) {
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int n = R.B * R.K;
   int* s_ids = reinterpret_cast<int*>(scratch);
   float* s_r = reinterpret_cast<float*>(scratch + 4 * kDecMaxEntries);
@@ -407,26 +407,63 @@ __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTa
   return live;
 }
 
+// K split: a workgroup of NS waves (blockDim.x / 64) computes one item; wave
+// w streams K blocks [w*kbs/NS, (w+1)*kbs/NS) through its own ring and the
+// partial sums meet in LDS, added in wave order by wave 0. NS > 1 when the
+// items alone would leave SIMDs idle (few tokens or experts).
+constexpr int kWaveLds = kStages * kUnitBytes + 4 * kDecMaxTokens;  // ring + token list per wave
+
+__device__ __forceinline__ int split_waves() { return __builtin_amdgcn_readfirstlane(blockDim.x >> 6); }
+__device__ __forceinline__ int split_wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Sums the P accumulators of all waves into wave 0's (wave order); every wave
+// passes its barriers. The other waves' rings are free when this is called.
+template <int P>
+__device__ __forceinline__ void split_reduce(uint8_t* smem, int ns, int wave, f32x4 (&acc)[P]) {
+  if (ns == 1) return;
+  const int lane = threadIdx.x & 63;
+  __syncthreads();
+  if (wave > 0) {
+    float* red = reinterpret_cast<float*>(smem + wave * kWaveLds);
+#pragma unroll
+    for (int p = 0; p < P; ++p) *reinterpret_cast<f32x4*>(red + (p * 64 + lane) * 4) = acc[p];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    for (int w = 1; w < ns; ++w) {
+      const float* red = reinterpret_cast<const float*>(smem + w * kWaveLds);
+#pragma unroll
+      for (int p = 0; p < P; ++p) acc[p] += *reinterpret_cast<const f32x4*>(red + (p * 64 + lane) * 4);
+    }
+  }
+  __syncthreads();
+}
+
 template <int FMT, bool kFullK>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     moe_dec_gate_up_kernel(Proj gate, Proj up, DecRoute R, DecTables T, const uint16_t* __restrict__ x,
                            int hidden, uint16_t* __restrict__ act, int inter) {
-  __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kUnitBytes];
-  __shared__ int tok[kDecMaxTokens];
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int ns = split_waves(), wave = split_wave();
+  uint8_t* ring = smem + wave * kWaveLds;
+  int* tok = reinterpret_cast<int*>(ring + kStages * kUnitBytes);
   const int rg = blockIdx.x, slot = blockIdx.y;
-  const int lane = threadIdx.x, jA = lane >> 4, j = lane & 15;
+  const int lane = threadIdx.x & 63, jA = lane >> 4, j = lane & 15;
   SlotRoute sr;
-  if (!dec_route(R, slot, rg == 0, T, ring, tok, sr)) return;
+  if (!dec_route(R, slot, rg == 0 && wave == 0, T, ring, tok, sr)) return;
   const WStream<FMT> wg(gate, sr.expert, lane), wu(up, sr.expert, lane);
+  const int kb0 = wave * gate.kb / ns, kb1 = (wave + 1) * gate.kb / ns;
   for (int tc = 0; tc < sr.cnt; tc += kPassTokens) {
     const int nt = sr.cnt - tc < kPassTokens ? sr.cnt - tc : kPassTokens;
     if (tc) wait_vm<0>();  // the previous pass's stores
     const XStream<FMT, kFullK> xs(x, R.B, hidden, tok[tc + (j < nt ? j : nt - 1)], lane);
     f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    stream_units<FMT, kFullK, 2>(
-        ring, gate.kb, xs, [&](int p, int kb, uint8_t* st) { (p ? wu : wg).issue(rg, kb, st); }, acc);
+    if (kb1 > kb0)
+      stream_units<FMT, kFullK, 2>(
+          ring, kb0, kb1 - kb0, xs, [&](int p, int kb, uint8_t* st) { (p ? wu : wg).issue(rg, kb, st); }, acc);
+    split_reduce<2>(smem, ns, wave, acc);
     // lane holds rows 4*(lane/16)+q, token column lane%16 of both accumulators
-    if (j < nt) {
+    if (wave == 0 && j < nt) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int row = rg * 16 + 4 * jA + q;
@@ -442,17 +479,20 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
 }
 
 template <int FMT, bool kFullK>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     moe_dec_down_kernel(Proj down, DecTables T, const uint16_t* __restrict__ act, int inter,
                         float* __restrict__ contrib, int hidden) {
-  __shared__ __attribute__((aligned(16))) uint8_t ring[kStages * kUnitBytes];
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int ns = split_waves(), wave = split_wave();
+  uint8_t* ring = smem + wave * kWaveLds;
   const int slot = blockIdx.y;
   if (slot >= T.hdr[0]) return;
   const int t0 = T.slot_t0[slot], cnt = T.slot_cnt[slot];
-  const int lane = threadIdx.x, jA = lane >> 4, j = lane & 15;
+  const int lane = threadIdx.x & 63, jA = lane >> 4, j = lane & 15;
   const WStream<FMT> wd(down, T.slot_e[slot], lane);
   const int groups = (hidden + 15) / 16;
   const int rg0 = blockIdx.x * kDownRows;
+  const int kb0 = wave * down.kb / ns, kb1 = (wave + 1) * down.kb / ns;
   for (int tc = 0; tc < cnt; tc += kPassTokens) {
     const int nt = cnt - tc < kPassTokens ? cnt - tc : kPassTokens;
     if (tc) wait_vm<0>();
@@ -463,14 +503,16 @@ __global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(3)))
 #pragma unroll
     for (int r = 0; r < kDownRows; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
     const XStream<FMT, kFullK> xs(act, T.hdr[1], inter, pos, lane);
-    stream_units<FMT, kFullK, kDownRows>(
-        ring, down.kb, xs,
-        [&](int p, int kb, uint8_t* st) {
-          const int rg = rg0 + p < groups ? rg0 + p : groups - 1;  // clamped rows are discarded
-          wd.issue(rg, kb, st);
-        },
-        acc);
-    if (j < nt) {
+    if (kb1 > kb0)
+      stream_units<FMT, kFullK, kDownRows>(
+          ring, kb0, kb1 - kb0, xs,
+          [&](int p, int kb, uint8_t* st) {
+            const int rg = rg0 + p < groups ? rg0 + p : groups - 1;  // clamped rows are discarded
+            wd.issue(rg, kb, st);
+          },
+          acc);
+    split_reduce<kDownRows>(smem, ns, wave, acc);
+    if (wave == 0 && j < nt) {
 #pragma unroll
       for (int r = 0; r < kDownRows; ++r) {
         const int row = (rg0 + r) * 16 + 4 * jA;
@@ -531,14 +573,40 @@ __global__ void __launch_bounds__(64)
   *reinterpret_cast<u32x2*>(out + (int64_t)b * hidden + h) = o;
 }
 
+// Waves per workgroup (K split) for a launch of ``items`` workgroups at most:
+// enough to give every SIMD of the device about two waves, at most 4.
+static int split_for(int64_t items) {
+  static int simds = 0;
+  if (!simds) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    simds = 4 * cus;
+  }
+  int ns = 1;
+  while (ns < 4 && items * ns * 2 <= 2 * (int64_t)simds) ns *= 2;
+  return ns;
+}
+
 template <int FMT, bool kFullK>
 static int launch(const DecArgs& A, hipStream_t s) {
   const int groups_i = (int)cdiv(A.I, 16), groups_h = (int)cdiv(A.H, 16);
-  hipLaunchKernelGGL((moe_dec_gate_up_kernel<FMT, kFullK>), dim3((unsigned)groups_i, A.max_slots), dim3(64), 0,
-                     s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I);
+  static bool attr_done = false;
+  if (!attr_done) {
+    hipFuncSetAttribute((const void*)moe_dec_gate_up_kernel<FMT, kFullK>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        4 * kWaveLds);
+    hipFuncSetAttribute((const void*)moe_dec_down_kernel<FMT, kFullK>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        4 * kWaveLds);
+    attr_done = true;
+  }
+  const int dn_x = (int)cdiv(groups_h, kDownRows);
+  const int ns_gu = split_for((int64_t)groups_i * A.max_slots), ns_dn = split_for((int64_t)dn_x * A.max_slots);
+  hipLaunchKernelGGL((moe_dec_gate_up_kernel<FMT, kFullK>), dim3((unsigned)groups_i, A.max_slots), dim3(64 * ns_gu),
+                     ns_gu * kWaveLds, s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I);
   if (A.after_gate_up) hipEventRecord((hipEvent_t)A.after_gate_up, s);
-  hipLaunchKernelGGL((moe_dec_down_kernel<FMT, kFullK>), dim3((unsigned)cdiv(groups_h, kDownRows), A.max_slots),
-                     dim3(64), 0, s, A.down, A.T, A.act, A.I, A.contrib, A.H);
+  hipLaunchKernelGGL((moe_dec_down_kernel<FMT, kFullK>), dim3((unsigned)dn_x, A.max_slots), dim3(64 * ns_dn),
+                     ns_dn * kWaveLds, s, A.down, A.T, A.act, A.I, A.contrib, A.H);
   if (A.after_down) hipEventRecord((hipEvent_t)A.after_down, s);
   hipLaunchKernelGGL(moe_dec_combine_kernel, dim3(A.R.B, (unsigned)cdiv(A.H, 256)), dim3(64), 0, s, A.T,
                      A.contrib, A.H, A.R.K, A.sh_y, A.sh_scale, A.out);
