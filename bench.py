@@ -175,8 +175,9 @@ def measure_projection(dev):
 
 def measure_q4_shared(dev):
     """Q4_K decode with an always-on shared expert: 64 experts, top-6, H 4096, I 1024,
-    shared I 4096, N(0, 0.015), seed 3; tokens 1, 8, 64. Weight tables rotate over
-    enough copies that the active bytes of one rotation exceed 3x the Infinity Cache."""
+    shared I 4096, N(0, 0.015), seed 3; tokens 1, 8, 64. The routed and shared weight tables
+    rotate over enough copies that the active bytes of one rotation exceed 3x the Infinity
+    Cache."""
     import numpy as np
     import torch
 
@@ -186,12 +187,11 @@ def measure_q4_shared(dev):
     H4, I4, E4, K4, IS = 4096, 1024, 64, 6, 4096
     L = moe_layer(seed=3, experts=E4, top_k=K4, hidden=H4, intermediate=I4, tokens=64, sigma=0.015,
                   qtype="Q4_K", shared_intermediate=IS, pack=False)
+    sh = L["shared"]
     base = [pack_experts(L[n], "Q4_K", I4 if n != "down" else H4, H4 if n != "down" else I4, dev)
             for n in ("gate", "up", "down")]
-    sh = L["shared"]
-    shared = dict(gate=pack_experts(sh["gate"][None], "Q4_K", IS, H4, dev),
-                  up=pack_experts(sh["up"][None], "Q4_K", IS, H4, dev),
-                  down=pack_experts(sh["down"][None], "Q4_K", H4, IS, dev))
+    base += [pack_experts(sh["gate"][None], "Q4_K", IS, H4, dev), pack_experts(sh["up"][None], "Q4_K", IS, H4, dev),
+             pack_experts(sh["down"][None], "Q4_K", H4, IS, dev)]
     fn = expert_parallel(None, gate_type="Q4_K", up_type="Q4_K", down_type="Q4_K", hidden=H4, intermediate=I4)
     per_expert, shared_bytes = 7_077_888, 28_311_552
     out = {"workload": "moe_decode_q4k_e64_top6_h4096_i1024_shared4096", "batches": {}}
@@ -207,7 +207,11 @@ def measure_q4_shared(dev):
         w = torch.from_numpy(L["weights"][:b]).to(dev).to(torch.bfloat16)
         ws = torch.empty(fn.workspace_bytes(b, K4, E4, IS), dtype=torch.uint8, device=dev)
         o = torch.empty((b, H4), dtype=torch.bfloat16, device=dev)
-        us = _time_calls(lambda i: fn(*layers[i % want], x, ids, w, shared=shared, workspace=ws, out=o), 100)
+        def call(i):
+            g, u, d, sg, su, sd = layers[i % want]
+            fn(g, u, d, x, ids, w, shared=dict(gate=sg, up=su, down=sd), workspace=ws, out=o)
+
+        us = _time_calls(call, 100)
         out["batches"][str(b)] = {"us_per_step": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
                                   "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                                   "active_experts": active, "bytes_per_step": nbytes, "layer_copies": want}
