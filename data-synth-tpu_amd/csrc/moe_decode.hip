@@ -38,7 +38,7 @@ constexpr int kDecMaxEntries = 1024;  // tokens * top_k handled by the decode pa
 constexpr int kDecMaxTokens = 256;    // tokens handled by the decode path
 constexpr int kDecMaxExperts = 256;
 constexpr int kStages = 3;
-constexpr int kDownRows = 3;  // 16-row groups of down per wave
+constexpr int kDownRows = 4;  // 16-row groups of down per wave
 constexpr int kPassTokens = 16;  // routes per weight pass (MFMA columns)
 
 // One ring stage holds a unit as it lies in the table (Q6_K 3360 B, Q4_K
