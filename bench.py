@@ -40,12 +40,12 @@ MFMA_PEAK_TFLOPS = 2500.0
 EXPERTS, TOP_K, HIDDEN, INTER, TOKENS, SEED = 128, 8, 2048, 768, 8, 1
 PREFILL_TOKENS, PREFILL_SEED, PREFILL_BIAS = 4096, 2, 0.5
 PREFILL_FLOPS = 2 * PREFILL_TOKENS * TOP_K * 3 * HIDDEN * INTER
-Q6_PROJ_BYTES = 1_277_952 + 12_288  # one 768x2048 (or 2048x768) Q6_K projection, SoA planes
+Q6_PROJ_BYTES = 768 * 8 * 210  # one 768x2048 (or 2048x768) Q6_K projection: 210 bytes per 256 weights
 # L2-to-fabric bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE over this script, scaled by a 512 MiB device copy in the same run
 # (profiles/moe_q6k_e128_top8_h2048_i768__hbm_bytes.txt); they change only
 # when the kernels do and are re-measured with them.
-TRAFFIC_BYTES = {"moe_dec_gate_up_kernel": 137_190_000, "moe_pf_gate_up_kernel": 1_407_080_000}
+TRAFFIC_BYTES = {"moe_dec_gate_up_kernel": 129_960_000, "moe_pf_gate_up_kernel": 909_990_000}
 
 
 def log(*a):
