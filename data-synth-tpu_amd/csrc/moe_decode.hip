@@ -279,10 +279,117 @@ struct SlotRoute {
   int expert, t0, cnt;
 };
 
+// Routing for at most 64 entries (tokens * top_k <= 64), one entry per lane,
+// with cross-lane reads instead of LDS loops: only the expert bit mask (LDS
+// atomics) and the token list touch LDS, and no workgroup barrier is needed,
+// since every wave works in its own scratch.
+__device__ __forceinline__ uint64_t token_lanes(int b, int K) {
+  const uint64_t m = K >= 64 ? ~0ull : (1ull << K) - 1ull;
+  return m << (b * K);
+}
+
+__device__ bool dec_route_small(const DecRoute& R, int slot, bool publish, const DecTables& T, uint8_t* scratch,
+                                int* tok, SlotRoute& out) {
+  const int lane = threadIdx.x & 63;
+  const int n = R.B * R.K;
+  uint32_t* s_mask = reinterpret_cast<uint32_t*>(scratch);  // one bit per expert
+  if (lane < kDecMaxExperts / 32) s_mask[lane] = 0u;
+  int id = -1;
+  float rw = 0.f;
+  if (lane < n) {
+    id = R.ids[lane];
+    rw = bf16_to_float(R.wts[lane]);
+  }
+  const int b = lane / R.K, kk = lane - b * R.K;
+  // Merged weight (experts.py:66-73): the first occurrence of an id in its
+  // token carries the sum, in position order, of the token's weights for it.
+  bool first = lane < n && id >= 0 && id < R.E;
+  float s = 0.f;
+  for (int k0 = 0; k0 < R.K; k0 += 8) {
+    int id2[8];
+    float r2[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int src = b * R.K + (k0 + q < R.K ? k0 + q : 0);
+      id2[q] = __shfl(id, src);
+      r2[q] = __shfl(rw, src);
+    }
+    // branch-free: terms that do not match add +0, which leaves the sum as is
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int k2 = k0 + q;
+      const bool same = id2[q] == id;
+      first = first && !(k2 < kk && same);
+      s += (k2 >= kk && k2 < R.K && same) ? r2[q] : 0.f;
+    }
+  }
+  float r = first ? bf16_round(s) : 0.f;
+  r = r != 0.f ? r : 0.f;
+  const bool live = r != 0.f;
+  if (live) atomicOr(&s_mask[id >> 5], 1u << (id & 31));
+  static_assert(kDecMaxExperts == 256, "mask read as two 16-byte words");
+  const u32x4 mA = *reinterpret_cast<const u32x4*>(s_mask), mB = *reinterpret_cast<const u32x4*>(s_mask + 4);
+  uint32_t m[kDecMaxExperts / 32];
+  int total = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    m[q] = __builtin_amdgcn_readfirstlane(mA[q]);
+    m[q + 4] = __builtin_amdgcn_readfirstlane(mB[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < kDecMaxExperts / 32; ++q) total += __builtin_popcount(m[q]);
+  const uint64_t lm = __ballot(live);
+  if (publish && slot == 0) {
+    if (lane == 0) {
+      T.hdr[0] = total;
+      T.hdr[1] = __popcll(lm);
+    }
+    if (lane < R.B) T.tok_n[lane] = __popcll(lm & token_lanes(lane, R.K));
+  }
+  const bool alive = slot < total;
+  if (alive) {
+    // the slot's expert: the slot-th set bit of the mask (ascending id)
+    int e = 0, rem = slot;
+#pragma unroll
+    for (int q = 0; q < kDecMaxExperts / 32; ++q) {
+      const int c = __builtin_popcount(m[q]);
+      if (rem >= 0 && rem < c) {
+        uint32_t w = m[q];
+        for (int i = 0; i < rem; ++i) w &= w - 1u;
+        e = 32 * q + __builtin_ctz(w);
+      }
+      rem -= c;
+    }
+    const uint64_t below = __ballot(live && id < e);
+    const uint64_t mine = __ballot(live && id == e);
+    const int t0 = __popcll(below), cnt = __popcll(mine);
+    if (live && id == e) {
+      const int rank = __popcll(mine & ((1ull << lane) - 1ull));
+      tok[rank] = b;
+      if (publish) {
+        T.route_w[t0 + rank] = r;
+        T.route_dst[t0 + rank] = b * R.K + __popcll(below & token_lanes(b, R.K));
+      }
+    }
+    if (publish && lane == 0) {
+      T.slot_e[slot] = e;
+      T.slot_t0[slot] = t0;
+      T.slot_cnt[slot] = cnt;
+    }
+    out = SlotRoute{e, t0, cnt};
+  }
+  // Stores must not count against the ring's wait counts, and the mask (in the
+  // ring's first stage) and token list must be read and written before the ring fills.
+  wait_vm<0>();
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  return alive;
+}
+
 __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTables& T, uint8_t* scratch,
                           int* tok, SlotRoute& out) {
   const int lane = threadIdx.x & 63;
   const int n = R.B * R.K;
+  if (n <= 64) return dec_route_small(R, slot, publish, T, scratch, tok, out);
   int* s_ids = reinterpret_cast<int*>(scratch);
   float* s_r = reinterpret_cast<float*>(scratch + 4 * kDecMaxEntries);
   int* s_cnt = reinterpret_cast<int*>(scratch + 8 * kDecMaxEntries);

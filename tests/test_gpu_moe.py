@@ -75,7 +75,7 @@ def _oracle(L, shared=None, weights=None, ids=None):
 
 
 @pytest.mark.parametrize("qtype", ["Q6_K", "Q4_K"])
-@pytest.mark.parametrize("tokens,experts,top_k", [(1, 8, 2), (8, 16, 4), (20, 12, 3), (70, 6, 2)])
+@pytest.mark.parametrize("tokens,experts,top_k", [(1, 8, 2), (8, 16, 4), (20, 12, 3), (33, 16, 4), (70, 6, 2)])
 def test_small_layers_match_oracle(device, qtype, tokens, experts, top_k):
     L = moe_layer(seed=tokens + experts, experts=experts, top_k=top_k, hidden=512, intermediate=256,
                   tokens=tokens, qtype=qtype, pack=False)
