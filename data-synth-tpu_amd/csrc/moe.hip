@@ -492,10 +492,23 @@ static void launch_phases(const Proj& g, const Proj& u, const Proj& d, const Tok
 }
 
 // GGUF expert tables [experts][rows][K blocks][block bytes] -> unit-major
-// tables (layout in moe_common.h). One thread per 4 bytes of expert
-// blockIdx.y's table; the byte map is a permutation of each row's block bytes
-// (Q6_K: ql at 0, qh at 128, sub-scales at 192, FP16 d at 208, 210 bytes;
-// Q4_K: 144 bytes), padded with zero rows to a multiple of 16.
+// tables (layout in moe_common.h), expert blockIdx.y per grid row.
+// Six-bit code of position p (0..255) of a GGUF Q6_K block
+// (kaggle/glm53_offload/gguf_quant.py:159-167): low nibble from ql, high two
+// bits from qh.
+__device__ __forceinline__ uint32_t q6_code_at(const uint8_t* blk, int p) {
+  const int n = p >> 7, q = (p >> 5) & 3, l = p & 31;
+  const uint32_t ql = blk[64 * n + l + 32 * (q & 1)];
+  const uint32_t qh = blk[128 + 32 * n + l];
+  return ((q >= 2 ? ql >> 4 : ql) & 15u) | (((qh >> (2 * q)) & 3u) << 4);
+}
+
+// One 4-byte word of a unit-major table per thread. Q6_K units are
+// bit-planar (see q6p_decode): code word g of chunk c of lane l (row l % 16,
+// sub-block 4g + l / 16) at 1024c + 16l + 4g, the lane's four sub-scales at
+// 3072 + 4l, the rows' FP16 scales at 3328. Q4_K units are the rows' 144-byte
+// blocks in 16-byte chunks (chunk c of row j at 16 * (16c + j)). Rows past the
+// projection's are zero.
 template <int FMT>
 __global__ void __launch_bounds__(256) moe_pack_kernel(const uint8_t* __restrict__ raw, int64_t raw_stride, int rows,
                                                        int kbs, uint8_t* __restrict__ dst, int64_t dst_stride,
@@ -507,35 +520,48 @@ __global__ void __launch_bounds__(256) moe_pack_kernel(const uint8_t* __restrict
   const int64_t unit = o / U;
   const int ob = (int)(o - unit * U);
   const int rg = (int)(unit / kbs), kb = (int)(unit - (int64_t)rg * kbs);
+  auto block = [&](int row) { return raw + e * raw_stride + ((int64_t)(rg * 16 + row) * kbs + kb) * BS; };
   uint32_t v = 0;
+  if (FMT == FMT_Q6 && ob < 3072) {
+    const int c = ob >> 10, l = (ob >> 4) & 63, g = (ob >> 2) & 3;
+    const int j = l & 15, jA = l >> 4;
+    if (rg * 16 + j < rows) {
+      const uint8_t* blk = block(j);
+      const int p0 = 64 * g + 16 * jA;  // the sub-block; pair k holds positions p0 + 2k, p0 + 2k + 1
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int b = ob + t;
-    int row, src;  // row within the group, byte within that row's block
-    if (FMT == FMT_Q6) {
-      if (b < 2048) {
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) v |= q6_code_at(blk, p0 + 2 * (2 * c + t) + h) << (4 + 6 * t + 16 * h);
+        if (c < 2) {
+          v |= (q6_code_at(blk, p0 + 2 * (6 + c) + h) & 15u) << (16 * h);
+        } else {
+#pragma unroll
+          for (int t = 0; t < 2; ++t) v |= (q6_code_at(blk, p0 + 2 * (6 + t) + h) >> 4) << (2 * t + 16 * h);
+        }
+      }
+    }
+  } else if (FMT == FMT_Q6 && ob < 3328) {
+    const int l = (ob - 3072) >> 2, j = l & 15, jA = l >> 4;
+    if (rg * 16 + j < rows) {
+      const uint8_t* blk = block(j);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) v |= (uint32_t)blk[192 + 4 * g + jA] << (8 * g);
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int b = ob + t;
+      int row, src;  // row within the group, byte within that row's block
+      if (FMT == FMT_Q6) {
+        row = (b - 3328) >> 1;
+        src = 208 + (b & 1);
+      } else {
         row = (b >> 4) & 15;
         src = 16 * (b >> 8) + (b & 15);
-      } else if (b < 3072) {
-        const int q = b - 2048;
-        row = (q >> 4) & 15;
-        src = 128 + 16 * (q >> 8) + (q & 15);
-      } else if (b < 3328) {
-        const int q = b - 3072;
-        row = q >> 4;
-        src = 192 + (q & 15);
-      } else {
-        const int q = b - 3328;
-        row = q >> 1;
-        src = 208 + (q & 1);
       }
-    } else {
-      row = (b >> 4) & 15;
-      src = 16 * (b >> 8) + (b & 15);
+      const uint32_t byte = rg * 16 + row < rows ? block(row)[src] : 0u;
+      v |= byte << (8 * t);
     }
-    const int r = rg * 16 + row;
-    const uint32_t byte = r < rows ? raw[e * raw_stride + ((int64_t)r * kbs + kb) * BS + src] : 0u;
-    v |= byte << (8 * t);
   }
   *reinterpret_cast<uint32_t*>(dst + e * dst_stride + o) = v;
 }

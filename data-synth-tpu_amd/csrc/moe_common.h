@@ -10,14 +10,17 @@ enum { FMT_Q6 = 0, FMT_Q4K = 1 };
 // Expert tables of the routed-expert kernels are unit-major: a unit is 16
 // output rows x one 256-wide K block, stored exactly as a wave stages it in
 // LDS, and an expert's units are ordered [row group][K block] so that a wave
-// streaming one row group over K reads one contiguous run.
-//   Q6_K unit (3360 B): ql   [0, 2048)    16-byte chunk c (0..7) of row j at 16*(16c + j)
-//                       qh   [2048, 3072) chunk c (0..3) of row j at 2048 + 16*(16c + j)
-//                       sc   [3072, 3328) row j's 16 sub-scales at 3072 + 16j
-//                       d    [3328, 3360) row j's FP16 scale at 3328 + 2j
+// streaming one row group over K reads one contiguous run. Lane l of the wave
+// decoding a unit owns row j = l % 16 and the K positions 64g + 16jA + [0, 16)
+// (jA = l / 16, g = 0..3: sub-block 4g + jA).
+//   Q6_K unit (3360 B), bit-planar (the same 6 bits per weight, rearranged):
+//     codes [0, 3072)    code word g of chunk c (0..2) of lane l at 1024c + 16l + 4g
+//                        (bit map in q6moe_device.h, q6p_decode)
+//     sc    [3072, 3328) lane l's sub-scales of sub-blocks 4g + jA at 3072 + 4l + g
+//     d     [3328, 3360) row j's FP16 scale at 3328 + 2j
 //   Q4_K unit (2304 B): chunk c (0..8) of row j's 144-byte block at 16*(16c + j)
-// (GGUF block byte orders: kaggle/glm53_offload/gguf_quant.py:115-173). Rows
-// past the matrix are zero.
+// (GGUF block formats: kaggle/glm53_offload/gguf_quant.py:115-173). Rows past
+// the matrix are zero.
 constexpr int kQ6Unit = 3360;
 constexpr int kQ4Unit = 2304;
 
@@ -121,20 +124,18 @@ struct Unit;
 
 template <>
 struct Unit<FMT_Q6> {
-  Q6Raw r;
+  u32x4 c0, c1, c2;  // the lane's code words (bit-planar, group g = word g)
+  uint32_t sc;       // the lane's sub-scales: byte g = sub-block 4g + jA
+  uint32_t d;        // FP16 bits of the row's block scale
   __device__ __forceinline__ void load(const Proj& p, int64_t e, int rgroup, int kb, int lane) {
     const uint8_t* u = unit_ptr<FMT_Q6>(p, e, rgroup, kb);
-    const int j = lane & 15, jA = lane >> 4;
-    r.qlA = ld16_stream(u + 16 * (16 * jA + j));
-    r.qlB = ld16_stream(u + 16 * (16 * (jA + 4) + j));
-    r.qhA = ld16_stream(u + 2048 + 16 * (16 * (jA & 1) + j));
-    r.qhB = ld16_stream(u + 2048 + 16 * (16 * ((jA & 1) + 2) + j));
-    r.sc = ld16_stream(u + 3072 + 16 * j);
-    r.d = *reinterpret_cast<const uint16_t*>(u + 3328 + 2 * j);
+    c0 = ld16_stream(u + 16 * lane);
+    c1 = ld16_stream(u + 1024 + 16 * lane);
+    c2 = ld16_stream(u + 2048 + 16 * lane);
+    sc = *reinterpret_cast<const uint32_t*>(u + 3072 + 4 * lane);
+    d = *reinterpret_cast<const uint16_t*>(u + 3328 + 2 * (lane & 15));
   }
-  __device__ __forceinline__ void decode(u32x4 a[8], int lane) const {
-    q6_decode_unit(r, lane >> 4, a);
-  }
+  __device__ __forceinline__ void decode(u32x4 a[8], int lane) const { q6p_decode(c0, c1, c2, sc, d, a); }
   static __device__ __forceinline__ int xoff(int f, int jA) { return q6_xfrag_offset(f, jA); }
 };
 

@@ -134,15 +134,12 @@ struct WStream<FMT_Q6> {
     dma4(u + 3328, v_d, st + 3328);
   }
   static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {
-    const int j = lane & 15, jA = lane >> 4;
-    Q6Raw r;
-    r.qlA = *reinterpret_cast<const u32x4*>(st + 16 * (jA * 16 + j));
-    r.qlB = *reinterpret_cast<const u32x4*>(st + 1024 + 16 * (jA * 16 + j));
-    r.qhA = *reinterpret_cast<const u32x4*>(st + 2048 + 16 * ((jA & 1) * 16 + j));
-    r.qhB = *reinterpret_cast<const u32x4*>(st + 2048 + 16 * (((jA & 1) + 2) * 16 + j));
-    r.sc = *reinterpret_cast<const u32x4*>(st + 3072 + 16 * j);
-    r.d = *reinterpret_cast<const uint16_t*>(st + 3328 + 2 * j);
-    q6_decode_unit(r, jA, a);
+    const u32x4 c0 = *reinterpret_cast<const u32x4*>(st + 16 * lane);
+    const u32x4 c1 = *reinterpret_cast<const u32x4*>(st + 1024 + 16 * lane);
+    const u32x4 c2 = *reinterpret_cast<const u32x4*>(st + 2048 + 16 * lane);
+    const uint32_t sc = *reinterpret_cast<const uint32_t*>(st + 3072 + 4 * lane);
+    const uint32_t d = *reinterpret_cast<const uint16_t*>(st + 3328 + 2 * (lane & 15));
+    q6p_decode(c0, c1, c2, sc, d, a);
   }
 };
 

@@ -84,48 +84,31 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 // The weights of one unit for one K half, in the registers of the lane that
-// decodes them (row j = lane % 16, k-group jA = lane / 16): ql chunk 4h + jA,
-// qh chunk 2h + jA % 2, the row's 16 sub-scales and its FP16 scale.
+// decodes them (row j = lane % 16, k-group jA = lane / 16): code words 2h and
+// 2h+1 of each of the three code chunks (bit-planar layout), the lane's
+// sub-scale word and the row's FP16 scale.
 struct HalfRegs {
-  u32x4 ql, qh, sc;
-  uint32_t d;
+  u32x2 c0, c1, c2;
+  uint32_t sc, d;
 };
 
 __device__ __forceinline__ void load_half(const uint8_t* units, int kbs, int rg, int kb, int h, int lane,
                                           HalfRegs& r) {
-  const uint8_t* u = units + ((int64_t)rg * kbs + kb) * kQ6Unit;
-  const int j = lane & 15, jA = lane >> 4;
-  r.ql = ld16_stream(u + 1024 * h + 16 * lane);
-  r.qh = ld16_stream(u + 2048 + 512 * h + 16 * ((jA & 1) * 16 + j));
-  r.sc = ld16_stream(u + 3072 + 16 * j);
-  r.d = *reinterpret_cast<const uint16_t*>(u + 3328 + 2 * j);
+  const uint8_t* u = units + ((int64_t)rg * kbs + kb) * kQ6Unit + 16 * lane + 8 * h;
+  r.c0 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(u));
+  r.c1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(u + 1024));
+  r.c2 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(u + 2048));
+  const uint8_t* v = units + ((int64_t)rg * kbs + kb) * kQ6Unit;
+  r.sc = *reinterpret_cast<const uint32_t*>(v + 3072 + 4 * lane);
+  r.d = *reinterpret_cast<const uint16_t*>(v + 3328 + 2 * (lane & 15));
 }
 
 // The 4 A fragments of K half h (f = 4h..4h+3) of a unit.
 __device__ __forceinline__ void decode_half(const HalfRegs& w, int h, int lane, u32x4 a[4]) {
-  const int jA = lane >> 4;
   const float d = half_bits_to_float(w.d);
-  const int q0 = jA >> 1, sh = 8 * jA;
 #pragma unroll
-  for (int gg = 0; gg < 2; ++gg) {
-    const int g = 2 * h + gg;
-    const int scv = (int)(int8_t)((w.sc[g] >> sh) & 0xff);
-    const float ds = d * (float)scv;
-    const float n1056 = -1056.f * ds;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const uint32_t h0 = w.qh[2 * e] >> (2 * q0), h1 = w.qh[2 * e + 1] >> (2 * q0);
-      uint32_t c0, c1;
-      if (gg) {
-        c0 = q6_codes_hi(w.ql[2 * e], h0);
-        c1 = q6_codes_hi(w.ql[2 * e + 1], h1);
-      } else {
-        c0 = q6_codes_lo(w.ql[2 * e], h0);
-        c1 = q6_codes_lo(w.ql[2 * e + 1], h1);
-      }
-      a[2 * gg + e] = q6_frag_mix(c0, c1, ds, n1056);
-    }
-  }
+  for (int gg = 0; gg < 2; ++gg)
+    q6p_group(w.c0[gg], w.c1[gg], w.c2[gg], q6p_ds(d, w.sc, 2 * h + gg), a[2 * gg], a[2 * gg + 1]);
 }
 
 // LDS byte offset of token-tile granule (token t, 8-column granule c) of a K half.

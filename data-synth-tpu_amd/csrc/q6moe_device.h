@@ -103,6 +103,58 @@ __device__ __forceinline__ u32x4 q6_frag_mix(uint32_t c0, uint32_t c1, float ds,
   return r;
 }
 
+// ---------------------------------------------------------------------------
+// Bit-planar Q6_K lane layout (the MoE unit tables). A lane holds 64 weights
+// as four groups of one 16-wide sub-block each; a group is three 32-bit code
+// words w0, w1, w2 laid out so that the FP16 form of every code pair of an
+// MFMA operand comes out of one word with one or two v_bitop3 (gfx950's
+// three-input bitwise op): about 200 VALU instructions per unit instead of the
+// 232 of the byte assembly + v_perm_b32 path of q6_decode_unit.
+//   pair k (sub-block positions 2k, 2k+1; low half / high half):
+//   k = 0..5  the 6-bit codes at bits [4,10) and [20,26) of word k/2 after a
+//             right shift by 6*(k%2), taken as FP16 0x6400 | code << 4, i.e.
+//             1024 + 16c, so w = fma(h, ds/16, -96*ds);
+//   k = 6, 7  the low nibbles at bits [0,4) and [16,20) of word k-6, the high
+//             two bits at bits [2(k-6), 2(k-6)+2) and 16 above in word 2;
+//             FP16 0x6400 | code = 1024 + c, so w = fma(h, ds, -1056*ds).
+// Both forms give ds*(c-32) exactly (ds has at most 18 significant bits), so
+// the BF16 weights equal those of q6_frag_mix bit for bit.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t b3_fmt(uint32_t r, uint32_t m, uint32_t k) {
+  return __builtin_amdgcn_bitop3_b32(r, m, k, 0xEA);  // (r & m) | k
+}
+__device__ __forceinline__ uint32_t b3_sel(uint32_t a, uint32_t b, uint32_t m) {
+  return __builtin_amdgcn_bitop3_b32(a, b, m, 0xE4);  // (a & m) | (b & ~m)
+}
+__device__ __forceinline__ uint32_t mix_pair(uint32_t h, float s, float n) {
+  return pack_bf16x2(__builtin_fmaf(h16_lo(h), s, n), __builtin_fmaf(h16_hi(h), s, n));
+}
+// One group: fragment fa = sub-block positions 0..7, fb = 8..15.
+__device__ __forceinline__ void q6p_group(uint32_t w0, uint32_t w1, uint32_t w2, float ds, u32x4& fa, u32x4& fb) {
+  const uint32_t M4 = 0x03F003F0u, M0 = 0x003F003Fu, MN = 0x000F000Fu, K = 0x64006400u;
+  const float s4 = ds * 0.0625f, n4 = -96.f * ds, n0 = -1056.f * ds;
+  fa[0] = mix_pair(b3_fmt(w0, M4, K), s4, n4);
+  fa[1] = mix_pair(b3_fmt(w0 >> 6, M4, K), s4, n4);
+  fa[2] = mix_pair(b3_fmt(w1, M4, K), s4, n4);
+  fa[3] = mix_pair(b3_fmt(w1 >> 6, M4, K), s4, n4);
+  fb[0] = mix_pair(b3_fmt(w2, M4, K), s4, n4);
+  fb[1] = mix_pair(b3_fmt(w2 >> 6, M4, K), s4, n4);
+  fb[2] = mix_pair(b3_fmt(b3_sel(w0, w2 << 4, MN), M0, K), ds, n0);
+  fb[3] = mix_pair(b3_fmt(b3_sel(w1, w2 << 2, MN), M0, K), ds, n0);
+}
+// Sub-scale of group g from the lane's scale word (byte g, signed).
+__device__ __forceinline__ float q6p_ds(float d, uint32_t scw, int g) {
+  return d * (float)(int)(int8_t)(scw >> (8 * g));
+}
+// The lane's 8 A fragments: fragment 2g+e covers unit positions
+// 64g + 16jA + 8e + [0, 8) (the same positions as q6_decode_unit).
+__device__ __forceinline__ void q6p_decode(const u32x4& c0, const u32x4& c1, const u32x4& c2, uint32_t scw,
+                                           uint32_t dbits, u32x4 a[8]) {
+  const float d = half_bits_to_float(dbits);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) q6p_group(c0[g], c1[g], c2[g], q6p_ds(d, scw, g), a[2 * g], a[2 * g + 1]);
+}
+
 __device__ __forceinline__ u32x4 q6_frag_exact(uint32_t c0, uint32_t c1, float ds) {
   u32x4 r;
   r[0] = pack_bf16x2(ds * (ubyte_f(c0, 0) - 32.f), ds * (ubyte_f(c0, 1) - 32.f));

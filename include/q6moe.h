@@ -99,10 +99,12 @@ int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, int64_t width
  * Expert tables of the routed FFN are unit-major, packed once from the GGUF
  * tables the reference keeps per expert ([E, bytes_per_expert], raw Q6_K or
  * Q4_K rows; kaggle/qwen38_tpu/parallel.py:40-87). A unit is 16 output rows x
- * one 256-wide K block with the bytes of those 16 row blocks permuted into
- * 16-byte chunks (Q6_K 3360 bytes, Q4_K 2304 bytes; rows padded with zeros to
- * a multiple of 16); an expert's units run [row group][K block]. The
- * permutation moves bytes only, so decoded values are those of the GGUF rows.
+ * one 256-wide K block (Q6_K 3360 bytes, Q4_K 2304 bytes; rows padded with
+ * zeros to a multiple of 16); an expert's units run [row group][K block].
+ * Q4_K units hold the rows' block bytes in 16-byte chunks. Q6_K units are
+ * bit-planar: the same 6-bit codes, sub-scales and FP16 scales, rearranged per
+ * decoding lane (map in csrc/moe_common.h and csrc/q6moe_device.h). Either
+ * way the repack is lossless, so decoded values are those of the GGUF rows.
  */
 size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width); /* per expert; 0 if invalid */
 

@@ -157,26 +157,54 @@ def test_route_weights_match_oracle_merging(device):
     assert_moe_close(got, _oracle(L, ids=ids, weights=w))
 
 
+def _q6_codes(blk):
+    """Six-bit codes [..., 256] of GGUF Q6_K blocks [..., 210] (gguf_quant.py:159-167)."""
+    ql, qh = blk[..., :128].astype(np.uint32), blk[..., 128:192].astype(np.uint32)
+    p = np.arange(256)
+    n, q, l = p >> 7, (p >> 5) & 3, p & 31
+    lo = ql[..., 64 * n + l + 32 * (q & 1)]
+    nib = np.where(q >= 2, lo >> 4, lo) & 15
+    return (nib | (((qh[..., 32 * n + l] >> (2 * q)) & 3) << 4)).astype(np.uint32)
+
+
 def _unit_major(raw, qtype, rows, width):
     """The unit-major expert table, restated with NumPy: units of 16 rows x one
-    256-wide K block ordered [row group][K block]; inside a unit, 16-byte chunk
-    c of row j at 16*(16c + j) (Q6_K: ql chunks, then qh chunks, then the rows'
-    16 sub-scales and FP16 scales row by row); rows padded with zeros."""
+    256-wide K block ordered [row group][K block], rows padded with zeros.
+    Q4_K: 16-byte chunk c of row j at 16*(16c + j). Q6_K (bit-planar): lane l
+    (row j = l % 16, jA = l // 16) holds sub-blocks 4g + jA; its code word g of
+    chunk c sits at 1024c + 16l + 4g with pair k (positions 2k, 2k+1, low/high
+    16 bits) at bits 4+6(k%2) of word k//2 for k < 6, and for k = 6, 7 the low
+    nibbles in word k-6 bits 0-3 and the high two bits in word 2 bits 2(k-6);
+    then the lanes' sub-scales (3072 + 4l + g) and the rows' FP16 scales."""
     bs = 210 if qtype == "Q6_K" else 144
     E, kbs, groups = raw.shape[0], -(-width // 256), -(-rows // 16)
     pad = np.zeros((E, groups * 16, kbs, bs), np.uint8)
     pad[:, :rows] = raw.reshape(E, rows, kbs, bs)
     blk = pad.reshape(E, groups, 16, kbs, bs).transpose(0, 1, 3, 2, 4)  # [E, g, kb, row, bs]
+    if qtype != "Q6_K":
+        return blk.reshape(E, groups, kbs, 16, 9, 16).transpose(0, 1, 2, 4, 3, 5).reshape(E, -1)
+    codes = _q6_codes(blk)  # [E, g, kb, row, 256]
+    lane = np.arange(64)
+    j, jA = lane % 16, lane // 16
+    pos = 64 * np.arange(4)[None, :, None] + 16 * jA[:, None, None] + np.arange(16)[None, None, :]
+    c = codes[..., j[:, None, None], pos]  # [E, g, kb, lane, group, 16]
 
-    def chunk_major(a, chunks):
-        return a.reshape(E, groups, kbs, 16, chunks, 16).transpose(0, 1, 2, 4, 3, 5).reshape(E, groups, kbs, -1)
+    def pair(k, h):
+        return c[..., 2 * k + h]
 
-    if qtype == "Q6_K":
-        unit = np.concatenate([chunk_major(blk[..., :128], 8), chunk_major(blk[..., 128:192], 4),
-                               blk[..., 192:208].reshape(E, groups, kbs, 256),
-                               blk[..., 208:210].reshape(E, groups, kbs, 32)], axis=-1)
-    else:
-        unit = chunk_major(blk, 9)
+    words = np.zeros(c.shape[:-1] + (3,), np.uint32)
+    for h in range(2):
+        for w in range(3):
+            words[..., w] |= (pair(2 * w, h) << (4 + 16 * h)) | (pair(2 * w + 1, h) << (10 + 16 * h))
+        for t in range(2):
+            words[..., t] |= (pair(6 + t, h) & 15) << (16 * h)
+            words[..., 2] |= (pair(6 + t, h) >> 4) << (2 * t + 16 * h)
+    # words [E, g, kb, lane, group, chunk] -> bytes at 1024*chunk + 16*lane + 4*group
+    code_bytes = np.ascontiguousarray(words.transpose(0, 1, 2, 5, 3, 4).astype("<u4"))
+    code_bytes = code_bytes.view(np.uint8).reshape(E, groups, kbs, 3072)
+    sc = blk[..., 192:208][..., j[:, None], 4 * np.arange(4)[None, :] + jA[:, None]]  # [E, g, kb, lane, 4]
+    d = blk[..., 208:210].reshape(E, groups, kbs, 32)
+    unit = np.concatenate([code_bytes, sc.reshape(E, groups, kbs, 256), d], axis=-1)
     return unit.reshape(E, -1)
 
 
