@@ -26,6 +26,24 @@ constexpr int kChunkWords = kChunk / 32;
 
 __device__ __forceinline__ bool is_route(float r) { return r != 0.f || r != r; }
 
+// Copies n (>= 1) consecutive values of src into LDS, converted by cv. Eight
+// loads per lane are in flight at once (clamped in-range addresses, stores
+// masked), so a chunk's rows arrive in one or two memory round trips.
+template <typename D, typename S, typename Cv>
+__device__ __forceinline__ void stage_chunk(D* dst, const S* __restrict__ src, int n, Cv cv) {
+  for (int i0 = threadIdx.x; i0 < n; i0 += 8 * kChunk) {
+    S v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kChunk;
+      v[u] = src[i < n ? i : n - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (i0 + u * kChunk < n) dst[i0 + u * kChunk] = cv(v[u]);
+  }
+}
+
 // Routing, pass 1 (one workgroup per chunk of kChunk tokens, one lane per
 // token): merged BF16 weight of each first occurrence of an id in a token
 // (experts.py:66-73; 0 for repeats and out-of-range ids) and the chunk's
@@ -34,53 +52,65 @@ __global__ void __launch_bounds__(kChunk)
     moe_route_count_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B, int K,
                            int E, MoeWs ws, int* __restrict__ chunk_cnt) {
   extern __shared__ int sm[];
-  int* s_ids = sm;                                  // [kChunk * K]
-  float* s_w = reinterpret_cast<float*>(sm + kChunk * K);
+  int* s_ids = sm;                                            // [kChunk * K]
+  float* s_w = reinterpret_cast<float*>(sm + kChunk * K);     // [kChunk * K] weights, then merged weights
   __shared__ int cnt[kRouteMaxExperts];
   const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
   const int nb = B - b0 < kChunk ? B - b0 : kChunk;
+  const int64_t e0 = (int64_t)b0 * K;
   for (int e = tid; e < E; e += kChunk) cnt[e] = 0;
-  for (int i = tid; i < nb * K; i += kChunk) {
-    s_ids[i] = ids[(int64_t)b0 * K + i];
-    s_w[i] = bf16_to_float(wts[(int64_t)b0 * K + i]);
-  }
+  stage_chunk(s_ids, ids + e0, nb * K, [](int v) { return v; });
+  stage_chunk(s_w, wts + e0, nb * K, [](uint16_t v) { return bf16_to_float(v); });
   __syncthreads();
   if (tid < nb) {
     const int* id = s_ids + tid * K;
-    const float* w = s_w + tid * K;
+    float* w = s_w + tid * K;
+    // The sum for entry kk reads weights kk..K-1 only, so entry kk's merged
+    // weight can replace its raw weight in place.
     for (int kk = 0; kk < K; ++kk) {
       const int e = id[kk];
       bool first = e >= 0 && e < E;
       for (int k2 = 0; k2 < kk && first; ++k2) first = id[k2] != e;
-      float r = 0.f;
+      float m = 0.f;
       if (first) {
         float sum = 0.f;
         for (int k2 = kk; k2 < K; ++k2)
           if (id[k2] == e) sum += w[k2];
-        r = bf16_round(sum);
-        if (is_route(r)) atomicAdd(&cnt[e], 1);
+        m = bf16_round(sum);
+        if (is_route(m)) atomicAdd(&cnt[e], 1);
       }
-      ws.ent_r[(int64_t)(b0 + tid) * K + kk] = is_route(r) ? r : 0.f;
+      w[kk] = is_route(m) ? m : 0.f;
     }
   }
   __syncthreads();
+  for (int i = tid; i < nb * K; i += kChunk) ws.ent_r[e0 + i] = s_w[i];
   for (int e = tid; e < E; e += kChunk) chunk_cnt[(int64_t)blockIdx.x * E + e] = cnt[e];
 }
 
 // Routing, pass 2 (one workgroup, one lane per expert): active experts in
 // ascending id (experts.py:74-76), each expert's first route position, the
-// 128-route prefill tiles, and each chunk's first position per expert
-// (chunk_cnt is rewritten in place as absolute positions).
+// 128-route prefill tiles, each chunk's first position per expert relative to
+// the expert's first (chunk_cnt is rewritten in place) and, in row nchunks of
+// chunk_cnt, each expert's first position.
 __global__ void __launch_bounds__(kRouteMaxExperts)
     moe_route_scan_kernel(int E, int nchunks, int mtile, MoeWs ws, int* __restrict__ chunk_cnt) {
   __shared__ int s_a[kRouteMaxExperts], s_c[kRouteMaxExperts], s_t[kRouteMaxExperts];
   const int e = threadIdx.x;
   int total = 0;
   if (e < E) {
-    for (int c = 0; c < nchunks; ++c) {
-      const int v = chunk_cnt[(int64_t)c * E + e];
-      chunk_cnt[(int64_t)c * E + e] = total;
-      total += v;
+    for (int c0 = 0; c0 < nchunks; c0 += 8) {
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int c = c0 + u < nchunks ? c0 + u : nchunks - 1;
+        v[u] = chunk_cnt[(int64_t)c * E + e];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (c0 + u < nchunks) {
+          chunk_cnt[(int64_t)(c0 + u) * E + e] = total;
+          total += v[u];
+        }
     }
   }
   const int act = total > 0, nt = (total + mtile - 1) / mtile;
@@ -99,7 +129,7 @@ __global__ void __launch_bounds__(kRouteMaxExperts)
   }
   const int slot = s_a[e] - act, base = s_c[e] - total, t0 = s_t[e] - nt;
   if (e < E) {
-    for (int c = 0; c < nchunks; ++c) chunk_cnt[(int64_t)c * E + e] += base;
+    chunk_cnt[(int64_t)nchunks * E + e] = base;
     if (act) {
       ws.active[slot] = e;
       ws.act_off[slot] = base;
@@ -118,38 +148,43 @@ __global__ void __launch_bounds__(kRouteMaxExperts)
 }
 
 // Routing, pass 3 (one workgroup per chunk): a route's position is its
-// chunk's first position for the expert plus the number of earlier tokens of
-// the chunk routed to that expert (per-expert token bitmaps), so routes are
-// grouped by expert with tokens ascending. Per token, its positions in
-// ascending expert id feed the combine.
+// expert's first position, plus its chunk's first position within the
+// expert, plus the number of earlier tokens of the chunk routed to that expert
+// (per-expert token bitmaps), so routes are grouped by expert with tokens
+// ascending. Per token, its positions in ascending expert id feed the combine.
 __global__ void __launch_bounds__(kChunk)
-    moe_route_scatter_kernel(const int32_t* __restrict__ ids, int B, int K, int E, MoeWs ws,
+    moe_route_scatter_kernel(const int32_t* __restrict__ ids, int B, int K, int E, int nchunks, MoeWs ws,
                              const int* __restrict__ chunk_pos) {
+  extern __shared__ int sm[];
+  int* s_ids = sm;                                          // [kChunk * K]
+  float* s_r = reinterpret_cast<float*>(sm + kChunk * K);   // [kChunk * K]
+  int* s_tp = sm + 2 * kChunk * K;                          // [kChunk * K]
   __shared__ uint32_t bits[kRouteMaxExperts][kChunkWords];
+  __shared__ int s_pos[kRouteMaxExperts];
   const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
   const int nb = B - b0 < kChunk ? B - b0 : kChunk;
+  const int64_t e0 = (int64_t)b0 * K;
   for (int i = tid; i < E * kChunkWords; i += kChunk) bits[i / kChunkWords][i % kChunkWords] = 0u;
+  for (int e = tid; e < E; e += kChunk)
+    s_pos[e] = chunk_pos[(int64_t)nchunks * E + e] + chunk_pos[(int64_t)blockIdx.x * E + e];
+  stage_chunk(s_ids, ids + e0, nb * K, [](int v) { return v; });
+  stage_chunk(s_r, ws.ent_r + e0, nb * K, [](float v) { return v; });
   __syncthreads();
-  const int b = b0 + tid;
   if (tid < nb)
-    for (int kk = 0; kk < K; ++kk) {
-      const int64_t i = (int64_t)b * K + kk;
-      if (is_route(ws.ent_r[i])) atomicOr(&bits[ids[i]][tid >> 5], 1u << (tid & 31));
-    }
+    for (int kk = 0; kk < K; ++kk)
+      if (is_route(s_r[tid * K + kk])) atomicOr(&bits[s_ids[tid * K + kk]][tid >> 5], 1u << (tid & 31));
   __syncthreads();
   if (tid < nb) {
-    int* tp = ws.tok_pos + (int64_t)b * K;
+    int* tp = s_tp + tid * K;
     int m = 0;
     for (int kk = 0; kk < K; ++kk) {
-      const int64_t i = (int64_t)b * K + kk;
-      const float r = ws.ent_r[i];
-      int pos = -1;
+      const float r = s_r[tid * K + kk];
       if (is_route(r)) {
-        const int e = ids[i];
+        const int e = s_ids[tid * K + kk];
         int rank = __popc(bits[e][tid >> 5] & ((1u << (tid & 31)) - 1u));
         for (int w = 0; w < (tid >> 5); ++w) rank += __popc(bits[e][w]);
-        pos = chunk_pos[(int64_t)blockIdx.x * E + e] + rank;
-        ws.route_tok[pos] = b;
+        const int pos = s_pos[e] + rank;
+        ws.route_tok[pos] = b0 + tid;
         ws.route_w[pos] = r;
         // positions are expert-major: keep the token's list sorted (insertion)
         int q = m++;
@@ -159,10 +194,11 @@ __global__ void __launch_bounds__(kChunk)
         }
         tp[q] = pos;
       }
-      ws.ent_pos[i] = pos;
     }
     for (int q = m; q < K; ++q) tp[q] = -1;
   }
+  __syncthreads();
+  for (int i = tid; i < nb * K; i += kChunk) ws.tok_pos[e0 + i] = s_tp[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -392,7 +428,7 @@ __global__ void __launch_bounds__(256)
 // Host side
 // ---------------------------------------------------------------------------
 struct WsLayout {
-  size_t hdr, active, act_off, tile_off, tile_slot, ent_r, ent_pos, route_tok, route_w, tok_pos, act,
+  size_t hdr, active, act_off, tile_off, tile_slot, ent_r, route_tok, route_w, tok_pos, act,
       y, sh_act, sh_y, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, chunk_cnt, total;
 };
 
@@ -414,7 +450,6 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
   L.tile_off = take(4 * (E + 1));
   L.tile_slot = take(4 * (E + n / mtile + 1));
   L.ent_r = take(4 * n);
-  L.ent_pos = take(4 * n);
   L.route_tok = take(4 * n);
   L.route_w = take(4 * n);
   L.tok_pos = take(4 * n);
@@ -428,7 +463,7 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
   L.tok_n = take(4 * B);
   L.route_dst = take(4 * n);
   L.contrib = take(4 * n * H);
-  L.chunk_cnt = take(4 * cdiv(B, kChunk) * E);
+  L.chunk_cnt = take(4 * (cdiv(B, kChunk) + 1) * E);
   L.total = o;
   return L;
 }
@@ -647,7 +682,6 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   ws.tile_off = reinterpret_cast<int*>(w + L.tile_off);
   ws.tile_slot = reinterpret_cast<int*>(w + L.tile_slot);
   ws.ent_r = reinterpret_cast<float*>(w + L.ent_r);
-  ws.ent_pos = reinterpret_cast<int*>(w + L.ent_pos);
   ws.route_tok = reinterpret_cast<int*>(w + L.route_tok);
   ws.route_w = reinterpret_cast<float*>(w + L.route_w);
   ws.tok_pos = reinterpret_cast<int*>(w + L.tok_pos);
@@ -710,14 +744,22 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   }
   mark(0);
   {
+    static bool attr_done = false;
+    if (!attr_done) {  // top_k <= 32: at most 64 KB and 96 KB of staged rows
+      (void)hipFuncSetAttribute((const void*)moe_route_count_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kChunk * 32 * 8);
+      (void)hipFuncSetAttribute((const void*)moe_route_scatter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kChunk * 32 * 12);
+      attr_done = true;
+    }
     const int nchunks = (int)cdiv(B, kChunk);
     int* chunk_cnt = reinterpret_cast<int*>(w + L.chunk_cnt);
     hipLaunchKernelGGL(moe_route_count_kernel, dim3(nchunks), dim3(kChunk), (size_t)kChunk * K * 8, s, a->ids,
                        a->weights, (int)B, (int)K, (int)E, ws, chunk_cnt);
     hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3(kRouteMaxExperts), 0, s, (int)E, nchunks,
                        (int)kPrefillTile, ws, chunk_cnt);
-    hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nchunks), dim3(kChunk), 0, s, a->ids, (int)B, (int)K,
-                       (int)E, ws, chunk_cnt);
+    hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nchunks), dim3(kChunk), (size_t)kChunk * K * 12, s, a->ids,
+                       (int)B, (int)K, (int)E, nchunks, ws, chunk_cnt);
     if ((rc = check_launch("moe routing kernels"))) return rc;
   }
   mark(1);

@@ -55,7 +55,6 @@ struct MoeWs {
   int* tile_off;     // [E+1] first prefill tile of each slot
   int* tile_slot;    // [max tiles] slot of each prefill tile
   float* ent_r;      // [B*k] merged BF16 route weight of an entry (0: no route)
-  int* ent_pos;      // [B*k] route position of an entry (-1: none)
   int* route_tok;    // [routes] token of each route, grouped by expert, tokens ascending
   float* route_w;    // [routes] its BF16 weight as FP32
   int* tok_pos;      // [B*k] per token: route positions in ascending expert id, -1 padded

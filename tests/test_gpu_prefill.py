@@ -74,3 +74,19 @@ def test_prefill_workload_full_size_sampled(device):
         fn.mode = 0
     np.testing.assert_array_equal(got, again)
     assert torch.isfinite(torch.from_numpy(got)).all()
+
+
+def test_prefill_routing_wide_top_k(device):
+    # Three routing chunks (256 + 256 + 88 tokens) with 24 routes per token:
+    # the staged id/weight rows span several copy rounds per chunk, and the
+    # duplicated, out-of-range and zero-weight entries go through the merge.
+    L = moe_layer(seed=23, experts=48, top_k=24, hidden=256, intermediate=256, tokens=600, pack=False)
+    ids = L["ids"].copy()
+    w = L["weights"].copy()
+    ids[::5, 2] = ids[::5, 0]
+    ids[::7, 3] = 48 + 5
+    w[100:110, :] = 0
+    w[200:260, 5] = 0
+    got, _ = _run(L, device, mode=2, ids=ids, weights=w)
+    assert np.all(got[100:110] == 0)
+    assert_moe_close(got, _oracle(L, ids=ids, weights=w))
