@@ -38,7 +38,7 @@ constexpr int kHalfBytes = kM * 128 * 2;  // one K half of the token tile (32 KB
 constexpr int kXDma = kHalfBytes / 1024 / kWaves;  // token DMA instructions per wave per half
 constexpr int kAhead = 1;          // K halves in flight beyond the one being multiplied
 constexpr int kXStages = kAhead + 1;
-constexpr int kWLoads = 4;         // weight loads per unit per K half (ql, qh, sub-scales, d)
+constexpr int kWLoads = 5;         // weight loads per unit per K half (3 code chunks, sub-scales, d)
 constexpr int kStepOps = kUnits * kWLoads + kXDma;  // vector-memory instructions per K half per wave
 constexpr int kLds = kXStages * kHalfBytes;
 
@@ -159,7 +159,10 @@ __device__ __forceinline__ bool tile_info(const MoeWs& ws, int tile, Tile& T) {
 // into registers and DMAs its share of the token tile into LDS stage
 // s % kXStages, kAhead steps before it is multiplied; one workgroup barrier
 // per step makes every wave's share visible and frees the stage read in the
-// step before.
+// step before. The next step's loads go out in four parts, one after each
+// fragment's MFMAs (unit 0, unit 1, then the two halves of the token DMA), so
+// that the four waves of a workgroup do not all queue their vector-memory
+// instructions at once right after the barrier.
 template <typename RowFn>
 __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
                                           const uint16_t* x, const uint32_t (&xoff)[kXDma], int K,
@@ -178,14 +181,22 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     rgs[u] = rg_of(u);
   }
   HalfRegs wr[kXStages][kUnits];
-  auto issue = [&](int s, auto slot_c) {
+  // part p < kUnits: unit p's weights; the remaining parts split the token DMA
+  auto issue_part = [&](int s, auto slot_c, auto part_c) {
     constexpr int slot = decltype(slot_c)::value;
+    constexpr int part = decltype(part_c)::value;
     const int kb = s >> 1, h = s & 1;
+    if constexpr (part < kUnits) {
+      load_half(units[part], kbs, rgs[part], kb, h, lane, wr[slot][part]);
+    } else {
+      constexpr int np = 4 - kUnits, per = kXDma / np, i0 = (part - kUnits) * per;
+      uint8_t* xs = smem + slot * kHalfBytes + wave * kXDma * 1024;
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) load_half(units[u], kbs, rgs[u], kb, h, lane, wr[slot][u]);
-    uint8_t* xs = smem + slot * kHalfBytes + wave * kXDma * 1024;
-#pragma unroll
-    for (int i = 0; i < kXDma; ++i) dma16(xb + (int64_t)(kb * kQK + h * 128) * 2, xoff[i], xs + i * 1024);
+      for (int i = i0; i < i0 + per; ++i) dma16(xb + (int64_t)(kb * kQK + h * 128) * 2, xoff[i], xs + i * 1024);
+    }
+  };
+  auto issue = [&](int s, auto slot_c) {
+    static_for<0, 4>([&](auto pc) { issue_part(s, slot_c, pc); });
   };
   auto step = [&](int s, auto slot_c) {
     constexpr int slot = decltype(slot_c)::value;
@@ -196,14 +207,22 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
       if (younger == y) wait_vm<y * kStepOps>();
     });
     wg_barrier();  // every wave's share of this step's tile is in LDS; the oldest stage is free
-    if (s + kAhead < S) issue(s + kAhead, std::integral_constant<int, (slot + kAhead) % kXStages>{});
+    // The wait above covered this step's weight registers. Re-define them here
+    // so that the compiler does not also wait, after the next step's loads are
+    // issued, for everything in flight before decoding them.
+#pragma unroll
+    for (int u = 0; u < kUnits; ++u) {
+      HalfRegs& w = wr[slot][u];
+      asm volatile("" : "+v"(w.c0), "+v"(w.c1), "+v"(w.c2), "+v"(w.sc), "+v"(w.d));
+    }
+    const bool more = s + kAhead < S;
     const int h = s & 1;
     const uint8_t* xs = smem + slot * kHalfBytes;
     u32x4 a[kUnits][4];
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) decode_half(wr[slot][u], h, lane, a[u]);
-#pragma unroll
-    for (int f = 0; f < 4; ++f) {
+    static_for<0, 4>([&](auto fc) {
+      constexpr int f = decltype(fc)::value;
       const int c = xfrag_gran(f, jA);
 #pragma unroll
       for (int tg = 0; tg < kTG; ++tg) {
@@ -211,7 +230,10 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
 #pragma unroll
         for (int u = 0; u < kUnits; ++u) acc[u][tg] = mfma16(a[u][f], xv, acc[u][tg]);
       }
-    }
+      __builtin_amdgcn_sched_barrier(0);
+      if (more) issue_part(s + kAhead, std::integral_constant<int, (slot + kAhead) % kXStages>{}, fc);
+      __builtin_amdgcn_sched_barrier(0);
+    });
   };
   static_for<0, kAhead>([&](auto ic) {
     if (decltype(ic)::value < S) issue(decltype(ic)::value, ic);
@@ -326,14 +348,14 @@ int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs&
                        const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up) {
   static bool attr_done = false;
   if (!attr_done) {
-    hipFuncSetAttribute((const void*)moe_pf_gate_up_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
-    hipFuncSetAttribute((const void*)moe_pf_down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
+    (void)hipFuncSetAttribute((const void*)moe_pf_gate_up_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
+    (void)hipFuncSetAttribute((const void*)moe_pf_down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
     attr_done = true;
   }
   const auto grid = [&](int ncol) { return dim3((unsigned)(((int64_t)ncol * max_tiles + 7) / 8 * 8)); };
   hipLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds,
                      s, g, u, ws, x, H, ws.act, I);
-  if (after_gate_up) hipEventRecord((hipEvent_t)after_gate_up, s);
+  if (after_gate_up) (void)hipEventRecord((hipEvent_t)after_gate_up, s);
   hipLaunchKernelGGL(moe_pf_down_kernel, grid(H / (32 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds, s,
                      d, ws, ws.act, I, ws.y, H);
   return Q6MOE_OK;
