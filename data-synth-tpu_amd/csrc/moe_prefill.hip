@@ -95,9 +95,12 @@ struct HalfRegs {
 __device__ __forceinline__ void load_half(const uint8_t* units, int kbs, int rg, int kb, int h, int lane,
                                           HalfRegs& r) {
   const uint8_t* u = units + ((int64_t)rg * kbs + kb) * kQ6Unit + 16 * lane + 8 * h;
-  r.c0 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(u));
-  r.c1 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(u + 1024));
-  r.c2 = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(u + 2048));
+  // Plain (cached) loads: a K half reads 8 of every 16 bytes of a code line
+  // and the next K half the other 8, so the line must stay in L2 between the
+  // two steps (a non-temporal hint here doubles the L2-to-fabric traffic).
+  r.c0 = *reinterpret_cast<const u32x2*>(u);
+  r.c1 = *reinterpret_cast<const u32x2*>(u + 1024);
+  r.c2 = *reinterpret_cast<const u32x2*>(u + 2048);
   const uint8_t* v = units + ((int64_t)rg * kbs + kb) * kQ6Unit;
   r.sc = *reinterpret_cast<const uint32_t*>(v + 3072 + 4 * lane);
   r.d = *reinterpret_cast<const uint16_t*>(v + 3328 + 2 * (lane & 15));
