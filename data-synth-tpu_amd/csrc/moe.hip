@@ -133,14 +133,15 @@ __global__ void __launch_bounds__(kRouteMaxExperts)
     if (act) {
       ws.active[slot] = e;
       ws.act_off[slot] = base;
-      ws.tile_off[slot] = t0;
-      for (int j = 0; j < nt; ++j) ws.tile_slot[t0 + j] = slot;
+      for (int j = 0; j < nt; ++j) {
+        const int r0 = base + j * mtile;
+        ws.tile[t0 + j] = PfTile{e, r0, total - j * mtile < mtile ? total - j * mtile : mtile, slot};
+      }
     }
   }
   if (e == kRouteMaxExperts - 1) {
     const int na = s_a[e];
     ws.act_off[na] = s_c[e];
-    ws.tile_off[na] = s_t[e];
     ws.hdr[0] = na;
     ws.hdr[1] = s_c[e];
     ws.hdr[2] = s_t[e];
@@ -428,7 +429,7 @@ __global__ void __launch_bounds__(256)
 // Host side
 // ---------------------------------------------------------------------------
 struct WsLayout {
-  size_t hdr, active, act_off, tile_off, tile_slot, ent_r, route_tok, route_w, tok_pos, act,
+  size_t hdr, active, act_off, tile, ent_r, route_tok, route_w, tok_pos, act,
       y, sh_act, sh_y, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, chunk_cnt, total;
 };
 
@@ -447,8 +448,7 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
   L.hdr = take(64);
   L.active = take(4 * E);
   L.act_off = take(4 * (E + 1));
-  L.tile_off = take(4 * (E + 1));
-  L.tile_slot = take(4 * (E + n / mtile + 1));
+  L.tile = take(sizeof(PfTile) * (E + n / mtile + 1));
   L.ent_r = take(4 * n);
   L.route_tok = take(4 * n);
   L.route_w = take(4 * n);
@@ -679,8 +679,7 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   ws.hdr = reinterpret_cast<int*>(w + L.hdr);
   ws.active = reinterpret_cast<int*>(w + L.active);
   ws.act_off = reinterpret_cast<int*>(w + L.act_off);
-  ws.tile_off = reinterpret_cast<int*>(w + L.tile_off);
-  ws.tile_slot = reinterpret_cast<int*>(w + L.tile_slot);
+  ws.tile = reinterpret_cast<PfTile*>(w + L.tile);
   ws.ent_r = reinterpret_cast<float*>(w + L.ent_r);
   ws.route_tok = reinterpret_cast<int*>(w + L.route_tok);
   ws.route_w = reinterpret_cast<float*>(w + L.route_w);

@@ -48,12 +48,16 @@ __device__ __forceinline__ const uint8_t* unit_ptr(const Proj& p, int64_t e, int
 }
 
 // Workspace views written by the routing kernel and read by the GEMM kernels.
+// A prefill tile: one 16-byte record, read by one scalar load.
+struct alignas(16) PfTile {
+  int expert, r0, nv, slot;  // expert id, first route position, routes (<= 128), active slot
+};
+
 struct MoeWs {
   int* hdr;          // [0] active experts, [1] routes, [2] prefill tiles
   int* active;       // [E] expert id per slot (ascending)
   int* act_off;      // [E+1] first route position of each slot
-  int* tile_off;     // [E+1] first prefill tile of each slot
-  int* tile_slot;    // [max tiles] slot of each prefill tile
+  PfTile* tile;      // [max tiles] prefill tiles (128 routes of one expert)
   float* ent_r;      // [B*k] merged BF16 route weight of an entry (0: no route)
   int* route_tok;    // [routes] token of each route, grouped by expert, tokens ascending
   float* route_w;    // [routes] its BF16 weight as FP32

@@ -146,14 +146,11 @@ __device__ __forceinline__ bool pf_item(const MoeWs& ws, int ncol, int& tile, in
   return true;
 }
 
-__device__ __forceinline__ bool tile_info(const MoeWs& ws, int tile, Tile& T) {
-  if (tile >= ws.hdr[2]) return false;
-  const int slot = ws.tile_slot[tile];
-  const int a0 = ws.act_off[slot], a1 = ws.act_off[slot + 1];
-  T.expert = ws.active[slot];
-  T.r0 = a0 + (tile - ws.tile_off[slot]) * kM;
-  T.nv = a1 - T.r0 < kM ? a1 - T.r0 : kM;
-  return true;
+__device__ __forceinline__ void tile_info(const MoeWs& ws, int tile, Tile& T) {
+  const PfTile d = ws.tile[tile];  // one scalar load
+  T.expert = d.expert;
+  T.r0 = d.r0;
+  T.nv = d.nv;
 }
 
 // The streaming core shared by both kernels. ``rg_of(u)`` gives unit u's row
@@ -270,7 +267,8 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   Tile T;
   int tile, col;
-  if (!pf_item(ws, inter / (16 * kWaves), tile, col) || !tile_info(ws, tile, T)) return;
+  if (!pf_item(ws, inter / (16 * kWaves), tile, col)) return;
+  tile_info(ws, tile, T);
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
   const int rgb = col * kWaves + wave;  // this wave's row group (gate and up)
@@ -311,7 +309,8 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   Tile T;
   int tile, col;
-  if (!pf_item(ws, hidden / (32 * kWaves), tile, col) || !tile_info(ws, tile, T)) return;
+  if (!pf_item(ws, hidden / (32 * kWaves), tile, col)) return;
+  tile_info(ws, tile, T);
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
   const int rgb = col * 2 * kWaves + 2 * wave;  // this wave's two row groups

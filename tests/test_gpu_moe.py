@@ -136,6 +136,26 @@ def test_q4_with_shared_expert(device, tokens):
     assert_moe_close(got, _oracle(L, shared=L["shared"]))
 
 
+@pytest.mark.parametrize("qtype,tokens,mode", [("Q4_K", 8, 1), ("Q4_K", 100, 2), ("Q6_K", 100, 2), ("Q6_K", 20, 1)])
+def test_shared_expert_repeated_calls(device, qtype, tokens, mode):
+    # Decode-shaped (mode 1) and prefill-shaped (mode 2) calls with a shared
+    # expert: three calls in a row on the same stream and workspace, with no
+    # synchronisation between them, each bitwise equal to the first.
+    L = moe_layer(seed=31, experts=8, top_k=3, hidden=512, intermediate=256, tokens=tokens, qtype=qtype,
+                  sigma=0.015, shared_intermediate=768, pack=False)
+    want = _oracle(L, shared=L["shared"])
+    got, ctx = _run(L, device, mode=mode, shared=L["shared"])
+    assert_moe_close(got, want)
+    fn, tabs, x, ids, w, sh = ctx
+    fn.mode = mode
+    try:
+        outs = [fn(*tabs, x, ids, w, shared=sh) for _ in range(3)]
+    finally:
+        fn.mode = 0
+    for o in outs:
+        np.testing.assert_array_equal(o.float().cpu().numpy(), got)
+
+
 def test_raw_gguf_tables_match_packed_tables(device):
     L = moe_layer(seed=13, experts=4, top_k=2, hidden=512, intermediate=256, tokens=5, pack=False)
     got, ctx = _run(L, device)
