@@ -263,32 +263,64 @@ __global__ void __launch_bounds__(512)
       const int tok = q < si.cnt ? (src.dense ? q : src.route_tok[si.t0 + q]) : -1;
       xr[t] = tok >= 0 ? x + (int64_t)tok * hidden : nullptr;
     }
-    for (int kb = wave; kb < gate.kb; kb += kw) {
-      u32x4 xf[NT][8];
+    if constexpr (NT == 1) {
+      // Two K blocks per pass: all four units' loads are in flight together
+      // (the second block is clamped to the first when it does not exist).
+      static_assert(RPW == 1, "one row group per workgroup");
+      const int rg = rg0;
+      for (int kb0 = wave; kb0 < gate.kb && rg * 16 < inter; kb0 += 2 * kw) {
+        const bool two = kb0 + kw < gate.kb;
+        const int kbs[2] = {kb0, two ? kb0 + kw : kb0};
+        Unit<FMT> ug[2], uu[2];
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+        for (int b = 0; b < 2; ++b) {
+          ug[b].load(gate, si.expert, rg, kbs[b], lane);
+          uu[b].load(up, si.expert, rg, kbs[b], lane);
+        }
 #pragma unroll
-        for (int f = 0; f < 8; ++f)
-          xf[t][f] = xr[t] ? load_row8(xr[t], kb * kQK + Unit<FMT>::xoff(f, jA), hidden)
-                           : u32x4{0u, 0u, 0u, 0u};
+        for (int b = 0; b < 2; ++b) {
+          if (b == 1 && !two) break;
+          u32x4 xf[8];
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        const int rg = rg0 + r;
-        if (rg * 16 >= inter) break;
-        Unit<FMT> ug, uu;
-        ug.load(gate, si.expert, rg, kb, lane);
-        uu.load(up, si.expert, rg, kb, lane);
-        u32x4 a[8];
-        ug.decode(a, lane);
+          for (int f = 0; f < 8; ++f)
+            xf[f] = xr[0] ? load_row8(xr[0], kbs[b] * kQK + Unit<FMT>::xoff(f, jA), hidden) : u32x4{0u, 0u, 0u, 0u};
+          u32x4 a[8];
+          ug[b].decode(a, lane);
 #pragma unroll
-        for (int f = 0; f < 8; ++f)
+          for (int f = 0; f < 8; ++f) ag[0][0] = mfma16(a[f], xf[f], ag[0][0]);
+          uu[b].decode(a, lane);
 #pragma unroll
-          for (int t = 0; t < NT; ++t) ag[r][t] = mfma16(a[f], xf[t][f], ag[r][t]);
-        uu.decode(a, lane);
+          for (int f = 0; f < 8; ++f) au[0][0] = mfma16(a[f], xf[f], au[0][0]);
+        }
+      }
+    } else {
+      for (int kb = wave; kb < gate.kb; kb += kw) {
+        u32x4 xf[NT][8];
 #pragma unroll
-        for (int f = 0; f < 8; ++f)
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-          for (int t = 0; t < NT; ++t) au[r][t] = mfma16(a[f], xf[t][f], au[r][t]);
+          for (int f = 0; f < 8; ++f)
+            xf[t][f] = xr[t] ? load_row8(xr[t], kb * kQK + Unit<FMT>::xoff(f, jA), hidden)
+                             : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          const int rg = rg0 + r;
+          if (rg * 16 >= inter) break;
+          Unit<FMT> ug, uu;
+          ug.load(gate, si.expert, rg, kb, lane);
+          uu.load(up, si.expert, rg, kb, lane);
+          u32x4 a[8];
+          ug.decode(a, lane);
+#pragma unroll
+          for (int f = 0; f < 8; ++f)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) ag[r][t] = mfma16(a[f], xf[t][f], ag[r][t]);
+          uu.decode(a, lane);
+#pragma unroll
+          for (int f = 0; f < 8; ++f)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) au[r][t] = mfma16(a[f], xf[t][f], au[r][t]);
+        }
       }
     }
 #pragma unroll
@@ -344,7 +376,15 @@ __global__ void __launch_bounds__(512)
       const int q = tc + t * 16 + j;
       ar[t] = q < si.cnt ? act + (int64_t)(si.t0 + q) * inter : nullptr;
     }
+    // All RPW units of a K block are loaded before the first is decoded (row
+    // groups past the matrix are clamped to its last one and not used).
     for (int kb = wave; kb < down.kb; kb += kw) {
+      Unit<FMT> ud[RPW];
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const int rg = rg0 + r < (hidden + 15) / 16 ? rg0 + r : (hidden + 15) / 16 - 1;
+        ud[r].load(down, si.expert, rg, kb, lane);
+      }
       u32x4 xf[NT][8];
 #pragma unroll
       for (int t = 0; t < NT; ++t)
@@ -354,12 +394,9 @@ __global__ void __launch_bounds__(512)
                            : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
-        const int rg = rg0 + r;
-        if (rg * 16 >= hidden) break;
-        Unit<FMT> ud;
-        ud.load(down, si.expert, rg, kb, lane);
+        if ((rg0 + r) * 16 >= hidden) break;
         u32x4 a[8];
-        ud.decode(a, lane);
+        ud[r].decode(a, lane);
 #pragma unroll
         for (int f = 0; f < 8; ++f)
 #pragma unroll
