@@ -377,11 +377,13 @@ __global__ void __launch_bounds__(512)
       ar[t] = q < si.cnt ? act + (int64_t)(si.t0 + q) * inter : nullptr;
     }
     // All RPW units of a K block are loaded before the first is decoded (row
-    // groups past the matrix are clamped to its last one and not used).
+    // groups past the matrix are clamped to its last one and not used); with
+    // four token groups, Q8_0 units are loaded one at a time (registers).
+    constexpr int kPre = FMT == FMT_Q8 && NT > 1 ? 1 : RPW;
     for (int kb = wave; kb < down.kb; kb += kw) {
-      Unit<FMT> ud[RPW];
+      Unit<FMT> ud[kPre];
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) {
+      for (int r = 0; r < kPre; ++r) {
         const int rg = rg0 + r < (hidden + 15) / 16 ? rg0 + r : (hidden + 15) / 16 - 1;
         ud[r].load(down, si.expert, rg, kb, lane);
       }
@@ -396,7 +398,12 @@ __global__ void __launch_bounds__(512)
       for (int r = 0; r < RPW; ++r) {
         if ((rg0 + r) * 16 >= hidden) break;
         u32x4 a[8];
-        ud[r].decode(a, lane);
+        if constexpr (kPre == RPW) {
+          ud[r].decode(a, lane);
+        } else {
+          if (r > 0) ud[0].load(down, si.expert, rg0 + r, kb, lane);
+          ud[0].decode(a, lane);
+        }
 #pragma unroll
         for (int f = 0; f < 8; ++f)
 #pragma unroll
@@ -519,8 +526,11 @@ static Proj make_proj(const q6moe_table& t, int rows, int k) {
 
 // Bytes of one expert's unit-major table.
 static int64_t unit_table_bytes(int qtype, int64_t rows, int64_t k) {
-  return cdiv(rows, 16) * cdiv(k, kQK) * (qtype == Q6MOE_Q6_K ? kQ6Unit : kQ4Unit);
+  return cdiv(rows, 16) * cdiv(k, kQK) * (qtype == Q6MOE_Q6_K ? kQ6Unit : qtype == Q6MOE_Q4_K ? kQ4Unit : kQ8Unit);
 }
+
+static bool expert_qtype(int q) { return q == Q6MOE_Q6_K || q == Q6MOE_Q4_K || q == Q6MOE_Q8_0; }
+static int fmt_of(int q) { return q == Q6MOE_Q6_K ? FMT_Q6 : q == Q6MOE_Q4_K ? FMT_Q4K : FMT_Q8; }
 
 static int validate_table(const q6moe_table& t, const char* name, int64_t rows, int64_t k, int64_t experts) {
   std::string n(name);
@@ -528,8 +538,8 @@ static int validate_table(const q6moe_table& t, const char* name, int64_t rows, 
     set_error(n + ": null data");
     return Q6MOE_ERR_INVALID;
   }
-  if (t.qtype != Q6MOE_Q6_K && t.qtype != Q6MOE_Q4_K) {
-    set_error(n + ": qtype must be Q6_K or Q4_K");
+  if (!expert_qtype(t.qtype)) {
+    set_error(n + ": qtype must be Q6_K, Q4_K or Q8_0");
     return Q6MOE_ERR_UNSUPPORTED;
   }
   const int64_t need = unit_table_bytes(t.qtype, rows, k);
@@ -541,7 +551,8 @@ static int validate_table(const q6moe_table& t, const char* name, int64_t rows, 
   return Q6MOE_OK;
 }
 
-template <int FMT, typename Mark>
+// FG: gate/up table format, FD: down table format.
+template <int FG, int FD, typename Mark>
 static void launch_phases(const Proj& g, const Proj& u, const Proj& d, const TokenSrc& src, int grid_x,
                           int max_tokens, const uint16_t* x, int H, int I, uint16_t* act, uint16_t* y,
                           hipStream_t s, Mark mark) {
@@ -549,16 +560,16 @@ static void launch_phases(const Proj& g, const Proj& u, const Proj& d, const Tok
   const int kw2 = d.kb < 8 ? d.kb : 8;
   const unsigned rb1 = (unsigned)cdiv(I, 16), rb2 = (unsigned)cdiv(H, 16 * 2);
   if (max_tokens <= 16) {
-    hipLaunchKernelGGL((moe_gate_up_kernel<FMT, 1, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
+    hipLaunchKernelGGL((moe_gate_up_kernel<FG, 1, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
                        H, act, I, kw1);
     mark(2);
-    hipLaunchKernelGGL((moe_down_kernel<FMT, 1, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
+    hipLaunchKernelGGL((moe_down_kernel<FD, 1, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
                        H, kw2);
   } else {
-    hipLaunchKernelGGL((moe_gate_up_kernel<FMT, 4, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
+    hipLaunchKernelGGL((moe_gate_up_kernel<FG, 4, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
                        H, act, I, kw1);
     mark(2);
-    hipLaunchKernelGGL((moe_down_kernel<FMT, 4, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
+    hipLaunchKernelGGL((moe_down_kernel<FD, 4, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
                        H, kw2);
   }
 }
@@ -579,22 +590,45 @@ __device__ __forceinline__ uint32_t q6_code_at(const uint8_t* blk, int p) {
 // bit-planar (see q6p_decode): code word g of chunk c of lane l (row l % 16,
 // sub-block 4g + l / 16) at 1024c + 16l + 4g, the lane's four sub-scales at
 // 3072 + 4l, the rows' FP16 scales at 3328. Q4_K units are the rows' 144-byte
-// blocks in 16-byte chunks (chunk c of row j at 16 * (16c + j)). Rows past the
-// projection's are zero.
+// blocks in 16-byte chunks (chunk c of row j at 16 * (16c + j)). Q8_0 units
+// hold lane l's 16 codes of chunk g at 1024g + 16l and the rows' 8 block
+// scales at 4096. Rows (and Q8_0 blocks) past the projection's are zero.
+// rblocks: GGUF blocks per row in raw (K/256 for Q6_K and Q4_K, K/32 for Q8_0).
 template <int FMT>
 __global__ void __launch_bounds__(256) moe_pack_kernel(const uint8_t* __restrict__ raw, int64_t raw_stride, int rows,
-                                                       int kbs, uint8_t* __restrict__ dst, int64_t dst_stride,
-                                                       int64_t words) {
-  constexpr int U = UnitBytes<FMT>::value, BS = FMT == FMT_Q6 ? 210 : 144;
+                                                       int kbs, int rblocks, uint8_t* __restrict__ dst,
+                                                       int64_t dst_stride, int64_t words) {
+  constexpr int U = UnitBytes<FMT>::value, BS = FMT == FMT_Q6 ? 210 : FMT == FMT_Q4K ? 144 : 34;
   const int64_t wi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (wi >= words) return;
   const int64_t e = blockIdx.y, o = wi * 4;
   const int64_t unit = o / U;
   const int ob = (int)(o - unit * U);
   const int rg = (int)(unit / kbs), kb = (int)(unit - (int64_t)rg * kbs);
-  auto block = [&](int row) { return raw + e * raw_stride + ((int64_t)(rg * 16 + row) * kbs + kb) * BS; };
+  auto block = [&](int row) { return raw + e * raw_stride + ((int64_t)(rg * 16 + row) * rblocks + kb) * BS; };
   uint32_t v = 0;
-  if (FMT == FMT_Q6 && ob < 3072) {
+  if (FMT == FMT_Q8) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int b = ob + t;
+      int j, blk, src;  // row in the group, Q8_0 block in the row, byte in the block
+      if (b < 4096) {
+        const int g = b >> 10, l = (b >> 4) & 63;
+        j = l & 15;
+        blk = 8 * kb + 2 * g + (l >> 5);
+        src = 2 + 16 * ((l >> 4) & 1) + (b & 15);
+      } else {
+        const int idx = (b - 4096) >> 1;
+        j = idx >> 3;
+        blk = 8 * kb + 2 * (idx & 3) + ((idx >> 2) & 1);
+        src = b & 1;
+      }
+      const int row = rg * 16 + j;
+      const uint32_t byte =
+          row < rows && blk < rblocks ? raw[e * raw_stride + ((int64_t)row * rblocks + blk) * BS + src] : 0u;
+      v |= byte << (8 * t);
+    }
+  } else if (FMT == FMT_Q6 && ob < 3072) {
     const int c = ob >> 10, l = (ob >> 4) & 63, g = (ob >> 2) & 3;
     const int j = l & 15, jA = l >> 4;
     if (rg * 16 + j < rows) {
@@ -643,8 +677,8 @@ __global__ void __launch_bounds__(256) moe_pack_kernel(const uint8_t* __restrict
 using namespace q6moe;
 
 extern "C" size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width) {
-  if ((qtype != Q6MOE_Q6_K && qtype != Q6MOE_Q4_K) || rows < 1 || width < 1 || rows > (1 << 24) ||
-      width > (1 << 24))
+  if (!expert_qtype(qtype) || rows < 1 || width < 1 || rows > (1 << 24) || width > (1 << 24) ||
+      (qtype == Q6MOE_Q8_0 && width % 32))
     return 0;
   return (size_t)unit_table_bytes(qtype, rows, width);
 }
@@ -652,7 +686,8 @@ extern "C" size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width) 
 extern "C" int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, int64_t rows, int64_t width,
                               uint8_t* dst, void* stream) {
   Q6MOE_REQUIRE(raw && dst, "moe_pack: null pointer");
-  Q6MOE_REQUIRE(qtype == Q6MOE_Q6_K || qtype == Q6MOE_Q4_K, "moe_pack: qtype must be Q6_K or Q4_K");
+  Q6MOE_REQUIRE(expert_qtype(qtype), "moe_pack: qtype must be Q6_K, Q4_K or Q8_0");
+  Q6MOE_REQUIRE(qtype != Q6MOE_Q8_0 || width % 32 == 0, "moe_pack: Q8_0 rows must hold whole 32-value blocks");
   Q6MOE_REQUIRE(experts >= 1 && experts <= 65535 && rows >= 1 && width >= 1 && rows <= (1 << 24) &&
                     width <= (1 << 24),
                 "moe_pack: bad shape");
@@ -663,10 +698,13 @@ extern "C" int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, in
   const dim3 grid((unsigned)cdiv(words, 256), (unsigned)experts);
   if (qtype == Q6MOE_Q6_K)
     hipLaunchKernelGGL(moe_pack_kernel<FMT_Q6>, grid, dim3(256), 0, (hipStream_t)stream, raw, rows * kbs * 210,
-                       (int)rows, kbs, dst, bytes, words);
-  else
+                       (int)rows, kbs, kbs, dst, bytes, words);
+  else if (qtype == Q6MOE_Q4_K)
     hipLaunchKernelGGL(moe_pack_kernel<FMT_Q4K>, grid, dim3(256), 0, (hipStream_t)stream, raw, rows * kbs * 144,
-                       (int)rows, kbs, dst, bytes, words);
+                       (int)rows, kbs, kbs, dst, bytes, words);
+  else
+    hipLaunchKernelGGL(moe_pack_kernel<FMT_Q8>, grid, dim3(256), 0, (hipStream_t)stream, raw,
+                       rows * (width / 32) * 34, (int)rows, kbs, (int)(width / 32), dst, bytes, words);
   return check_launch("moe_pack_kernel");
 }
 
@@ -688,8 +726,9 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   Q6MOE_REQUIRE(H % 8 == 0 && I % 8 == 0, "moe_forward: hidden and intermediate must be multiples of 8");
   Q6MOE_REQUIRE(aligned(a->x, 16) && aligned(a->out, 16) && aligned(a->workspace, 256),
                 "moe_forward: x/out need 16-byte and workspace 256-byte alignment");
-  Q6MOE_REQUIRE(a->gate.qtype == a->up.qtype && a->up.qtype == a->down.qtype,
-                "moe_forward: gate, up and down must share one qtype");
+  Q6MOE_REQUIRE(a->gate.qtype == a->up.qtype && (a->gate.qtype == Q6MOE_Q6_K || a->gate.qtype == Q6MOE_Q4_K) &&
+                    (a->down.qtype == a->gate.qtype || a->down.qtype == Q6MOE_Q8_0),
+                "moe_forward: gate and up must share Q6_K or Q4_K; down must be that type or Q8_0");
   Q6MOE_REQUIRE(a->mode >= 0 && a->mode <= 2, "moe_forward: mode must be 0, 1 or 2");
   int rc;
   if ((rc = validate_table(a->gate, "gate", I, H, E)) || (rc = validate_table(a->up, "up", I, H, E)) ||
@@ -699,7 +738,7 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   if (Is) {
     Q6MOE_REQUIRE(Is >= 1 && Is % 8 == 0 && Is <= (1 << 24), "moe_forward: shared_intermediate");
     Q6MOE_REQUIRE(a->shared_gate.qtype == a->gate.qtype && a->shared_up.qtype == a->gate.qtype &&
-                      a->shared_down.qtype == a->gate.qtype,
+                      a->shared_down.qtype == a->down.qtype,
                   "moe_forward: the shared expert must use the routed experts' qtype");
     if ((rc = validate_table(a->shared_gate, "shared_gate", Is, H, 1)) ||
         (rc = validate_table(a->shared_up, "shared_up", Is, H, 1)) ||
@@ -735,18 +774,26 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
     set_error("moe_forward: decode mode needs tokens*top_k <= 1024, top_k <= 32, experts <= 256");
     return Q6MOE_ERR_INVALID;
   }
-  const int fmt = a->gate.qtype == Q6MOE_Q6_K ? FMT_Q6 : FMT_Q4K;
+  const int fmt = fmt_of(a->gate.qtype), fmt_dn = fmt_of(a->down.qtype);
+  // Generic (non-tiled) expert phases for the call's formats.
+  auto phases = [&](const Proj& pg, const Proj& pu, const Proj& pd, const TokenSrc& src, int grid_x, int max_tok,
+                    int inter, uint16_t* act_out, uint16_t* y_out, auto mk) {
+    if (fmt == FMT_Q6 && fmt_dn == FMT_Q6)
+      launch_phases<FMT_Q6, FMT_Q6>(pg, pu, pd, src, grid_x, max_tok, a->x, (int)H, inter, act_out, y_out, s, mk);
+    else if (fmt == FMT_Q6)
+      launch_phases<FMT_Q6, FMT_Q8>(pg, pu, pd, src, grid_x, max_tok, a->x, (int)H, inter, act_out, y_out, s, mk);
+    else if (fmt_dn == FMT_Q4K)
+      launch_phases<FMT_Q4K, FMT_Q4K>(pg, pu, pd, src, grid_x, max_tok, a->x, (int)H, inter, act_out, y_out, s, mk);
+    else
+      launch_phases<FMT_Q4K, FMT_Q8>(pg, pu, pd, src, grid_x, max_tok, a->x, (int)H, inter, act_out, y_out, s, mk);
+  };
   if (decode) {
     mark(0);
     if (Is) {
       TokenSrc dense{1, (int)B, nullptr, nullptr, nullptr, nullptr};
       const Proj sg = make_proj(a->shared_gate, (int)Is, (int)H), su = make_proj(a->shared_up, (int)Is, (int)H),
                  sd = make_proj(a->shared_down, (int)H, (int)Is);
-      auto none = [](int) {};
-      if (fmt == FMT_Q6)
-        launch_phases<FMT_Q6>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s, none);
-      else
-        launch_phases<FMT_Q4K>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s, none);
+      phases(sg, su, sd, dense, 1, (int)B, (int)Is, ws.sh_act, ws.sh_y, [](int) {});
       if ((rc = check_launch("moe shared expert kernels"))) return rc;
     }
     mark(1);
@@ -773,7 +820,7 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
     D.out = a->out;
     D.after_gate_up = a->events ? a->events[2] : nullptr;
     D.after_down = a->events ? a->events[3] : nullptr;
-    if ((rc = launch_moe_decode(fmt, D, s))) return rc;
+    if ((rc = launch_moe_decode(fmt, fmt_dn, D, s))) return rc;
     rc = check_launch("moe decode kernels");
     mark(4);
     return rc;
@@ -813,22 +860,24 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
       return Q6MOE_ERR_HIP;
     }
     const int max_tiles = (int)(E + B * K / kPrefillTile + 1);
-    launch_moe_prefill(g, u, d, ws, max_tiles, a->x, (int)H, (int)I, s, a->events ? a->events[2] : nullptr);
-  } else if (a->gate.qtype == Q6MOE_Q6_K) {
-    launch_phases<FMT_Q6>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s, mark);
+    // Q8_0 down: the tiled gate/up, then the generic down over the same routes
+    const bool tiled_down = fmt_dn == FMT_Q6;
+    launch_moe_prefill(g, u, d, ws, max_tiles, a->x, (int)H, (int)I, s, a->events ? a->events[2] : nullptr,
+                       tiled_down);
+    if (!tiled_down) {
+      const int kw2 = d.kb < 8 ? d.kb : 8;
+      hipLaunchKernelGGL((moe_down_kernel<FMT_Q8, 4, 2>), dim3(slots, (unsigned)cdiv(H, 16 * 2)), dim3(64 * kw2), 0,
+                         s, d, routed, ws.act, (int)I, ws.y, (int)H, kw2);
+    }
   } else {
-    launch_phases<FMT_Q4K>(g, u, d, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, ws.y, s, mark);
+    phases(g, u, d, routed, slots, max_tokens, (int)I, ws.act, ws.y, mark);
   }
   if ((rc = check_launch("moe expert kernels"))) return rc;
   if (Is) {
     TokenSrc dense{1, (int)B, nullptr, nullptr, nullptr, nullptr};
     const Proj sg = make_proj(a->shared_gate, (int)Is, (int)H), su = make_proj(a->shared_up, (int)Is, (int)H),
                sd = make_proj(a->shared_down, (int)H, (int)Is);
-    auto none = [](int) {};
-    if (a->gate.qtype == Q6MOE_Q6_K)
-      launch_phases<FMT_Q6>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s, none);
-    else
-      launch_phases<FMT_Q4K>(sg, su, sd, dense, 1, (int)B, a->x, (int)H, (int)Is, ws.sh_act, ws.sh_y, s, none);
+    phases(sg, su, sd, dense, 1, (int)B, (int)Is, ws.sh_act, ws.sh_y, [](int) {});
     if ((rc = check_launch("moe shared expert kernels"))) return rc;
   }
   mark(3);

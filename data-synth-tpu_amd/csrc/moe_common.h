@@ -5,7 +5,7 @@
 
 namespace q6moe {
 
-enum { FMT_Q6 = 0, FMT_Q4K = 1 };
+enum { FMT_Q6 = 0, FMT_Q4K = 1, FMT_Q8 = 2 };
 
 // Expert tables of the routed-expert kernels are unit-major: a unit is 16
 // output rows x one 256-wide K block, stored exactly as a wave stages it in
@@ -19,10 +19,16 @@ enum { FMT_Q6 = 0, FMT_Q4K = 1 };
 //     sc    [3072, 3328) lane l's sub-scales of sub-blocks 4g + jA at 3072 + 4l + g
 //     d     [3328, 3360) row j's FP16 scale at 3328 + 2j
 //   Q4_K unit (2304 B): chunk c (0..8) of row j's 144-byte block at 16*(16c + j)
-// (GGUF block formats: kaggle/glm53_offload/gguf_quant.py:115-173). Rows past
+//   Q8_0 unit (4352 B: 16 rows x 8 blocks of 34 B, rearranged):
+//     codes [0, 4096)    chunk g of lane l at 1024g + 16l: row j's 16 int8 codes at
+//                        K positions 64g + 16jA + [0, 16), i.e. codes 16(jA%2) + [0, 16)
+//                        of its block 2g + jA/2
+//     d     [4096, 4352) FP16 scale of row j's block 2g + h at 4096 + 8(2j + h) + 2g
+// (GGUF block formats: kaggle/glm53_offload/gguf_quant.py:111-173). Rows past
 // the matrix are zero.
 constexpr int kQ6Unit = 3360;
 constexpr int kQ4Unit = 2304;
+constexpr int kQ8Unit = 4352;
 
 template <int FMT>
 struct UnitBytes;
@@ -33,6 +39,10 @@ struct UnitBytes<0> {
 template <>
 struct UnitBytes<1> {
   static constexpr int value = kQ4Unit;
+};
+template <>
+struct UnitBytes<2> {
+  static constexpr int value = kQ8Unit;
 };
 
 // One projection's expert table: [rows x k] per expert.
@@ -111,13 +121,13 @@ struct DecArgs {
 };
 
 bool dec_supported(int64_t B, int64_t K, int64_t E);
-int launch_moe_decode(int fmt, const DecArgs& A, hipStream_t s);
+int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s);  // fmt_dn: fmt_gu or FMT_Q8
 
 // Prefill grouped GEMM (Q6_K, hidden and intermediate multiples of 256).
 bool pf_supported(int fmt, int64_t H, int64_t I);
 int64_t pf_tile_routes();
 int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
-                       const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up);
+                       const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up, bool with_down);
 
 // ---------------------------------------------------------------------------
 // Unit decoders: 16 output rows x one 256-wide K block -> 8 MFMA A operands.
@@ -197,6 +207,24 @@ struct Unit<FMT_Q4K> {
   static __device__ __forceinline__ int xoff(int f, int jA) {
     return 64 * jA + 32 * (f >> 2) + 8 * (f & 3);
   }
+};
+
+// Q8_0 unit: lane (row l%16, k-group jA = l/16) holds codes chunk g (fragments
+// 2g, 2g+1) and the four FP16 scales of its blocks 2g + jA/2; w = d * q exact
+// in FP32, RNE to BF16 (gguf_quant.py:111-114). Fragment positions are the
+// Q6_K ones.
+template <>
+struct Unit<FMT_Q8> {
+  u32x4 c[4];
+  u32x2 d;
+  __device__ __forceinline__ void load(const Proj& p, int64_t e, int rgroup, int kb, int lane) {
+    const uint8_t* u = unit_ptr<FMT_Q8>(p, e, rgroup, kb);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) c[g] = ld16_stream(u + 1024 * g + 16 * lane);
+    d = *reinterpret_cast<const u32x2*>(u + 4096 + 8 * (2 * (lane & 15) + (lane >> 5)));
+  }
+  __device__ __forceinline__ void decode(u32x4 a[8], int) const { q8_decode(c, d, a); }
+  static __device__ __forceinline__ int xoff(int f, int jA) { return q6_xfrag_offset(f, jA); }
 };
 
 }  // namespace q6moe

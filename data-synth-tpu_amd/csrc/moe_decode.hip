@@ -42,11 +42,12 @@ constexpr int kDownRows = 4;  // 16-row groups of down per wave
 constexpr int kPassTokens = 16;  // routes per weight pass (MFMA columns)
 
 // One ring stage holds a unit as it lies in the table (Q6_K 3360 B, Q4_K
-// 2304 B), the Q6_K FP16 scales repeated up to the stage's end.
-constexpr int kUnitBytes = 3584;
+// 2304 B, Q8_0 4352 B), the Q6_K FP16 scales repeated up to the stage's end.
+template <int FMT>
+constexpr int stage_bytes() { return FMT == FMT_Q8 ? 4352 : 3584; }
 constexpr int kXLoads = 8;   // token-operand loads per K block (one per MFMA)
 
-static_assert(kStages * kUnitBytes >= 8 * kDecMaxEntries + 4 * kDecMaxExperts,
+static_assert(kStages * stage_bytes<FMT_Q6>() >= 8 * kDecMaxEntries + 4 * kDecMaxExperts,
               "routing scratch overlays the ring");
 
 template <int I, int N, typename F>
@@ -173,6 +174,36 @@ struct WStream<FMT_Q4K> {
   }
 };
 
+template <>
+struct WStream<FMT_Q8> {
+  static constexpr int kDma = 5;
+  const uint8_t* data;
+  int kbs;
+  uint32_t v16, v4;
+  __device__ __forceinline__ WStream(const Proj& p, int64_t e, int lane) {
+    data = p.data + e * p.dstride;
+    kbs = p.kb;
+    v16 = opaque(16 * lane);
+    v4 = opaque(4 * lane);
+  }
+  // unit: four 1 KB code chunks and the 256 B of scales, copied as they lie
+  __device__ __forceinline__ void issue(int rg, int kb, uint8_t* st) const {
+    const uint8_t* u = data + ((int64_t)rg * kbs + kb) * kQ8Unit;
+    dma16(u, v16, st);
+    dma16(u + 1024, v16, st + 1024);
+    dma16(u + 2048, v16, st + 2048);
+    dma16(u + 3072, v16, st + 3072);
+    dma4(u + 4096, v4, st + 4096);
+  }
+  static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {
+    u32x4 c[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) c[g] = *reinterpret_cast<const u32x4*>(st + 1024 * g + 16 * lane);
+    const u32x2 d = *reinterpret_cast<const u32x2*>(st + 4096 + 8 * (2 * (lane & 15) + (lane >> 5)));
+    q8_decode(c, d, a);
+  }
+};
+
 // Token operands: lane (token column j, K group jA) reads row ``row`` of the
 // BF16 matrix [rows, k] at columns kb*256 + xoff(f, jA); xoff splits into a
 // lane part xoff(0, jA) and a fragment part xoff(f, 0) in both formats.
@@ -220,7 +251,7 @@ __device__ __forceinline__ void stream_units(uint8_t* ring, int kb0, int kbs, co
   static_assert(kStages == 3 && P >= kStages - 1, "one K block of token operands in flight");
   const int lane = threadIdx.x & 63;
   u32x4 xA[8], xB[8];
-  auto stage = [&](int u) { return ring + (u % kStages) * kUnitBytes; };
+  auto stage = [&](int u) { return ring + (u % kStages) * stage_bytes<FMT>(); };
   auto compute = [&](auto pc, int u, u32x4(&xc)[8]) {
     constexpr int p = decltype(pc)::value;
     if constexpr (p == 0) xs.mask(xc, kb0 + u / P);
@@ -515,14 +546,15 @@ __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTa
 // w streams K blocks [w*kbs/NS, (w+1)*kbs/NS) through its own ring and the
 // partial sums meet in LDS, added in wave order by wave 0. NS > 1 when the
 // items alone would leave SIMDs idle (few tokens or experts).
-constexpr int kWaveLds = kStages * kUnitBytes + 4 * kDecMaxTokens;  // ring + token list per wave
+template <int FMT>
+constexpr int wave_lds() { return kStages * stage_bytes<FMT>() + 4 * kDecMaxTokens; }  // ring + token list
 
 __device__ __forceinline__ int split_waves() { return __builtin_amdgcn_readfirstlane(blockDim.x >> 6); }
 __device__ __forceinline__ int split_wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Sums the P accumulators of all waves into wave 0's (wave order); every wave
 // passes its barriers. The other waves' rings are free when this is called.
-template <int P>
+template <int P, int kWaveLds>
 __device__ __forceinline__ void split_reduce(uint8_t* smem, int ns, int wave, f32x4 (&acc)[P]) {
   if (ns == 1) return;
   const int lane = threadIdx.x & 63;
@@ -549,8 +581,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
                            int hidden, uint16_t* __restrict__ act, int inter) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int ns = split_waves(), wave = split_wave();
-  uint8_t* ring = smem + wave * kWaveLds;
-  int* tok = reinterpret_cast<int*>(ring + kStages * kUnitBytes);
+  uint8_t* ring = smem + wave * wave_lds<FMT>();
+  int* tok = reinterpret_cast<int*>(ring + kStages * stage_bytes<FMT>());
   const int rg = blockIdx.x, slot = blockIdx.y;
   const int lane = threadIdx.x & 63, jA = lane >> 4, j = lane & 15;
   SlotRoute sr;
@@ -565,7 +597,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     if (kb1 > kb0)
       stream_units<FMT, kFullK, 2>(
           ring, kb0, kb1 - kb0, xs, [&](int p, int kb, uint8_t* st) { (p ? wu : wg).issue(rg, kb, st); }, acc);
-    split_reduce<2>(smem, ns, wave, acc);
+    split_reduce<2, wave_lds<FMT>()>(smem, ns, wave, acc);
     // lane holds rows 4*(lane/16)+q, token column lane%16 of both accumulators
     if (wave == 0 && j < nt) {
 #pragma unroll
@@ -588,7 +620,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
                         float* __restrict__ contrib, int hidden) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int ns = split_waves(), wave = split_wave();
-  uint8_t* ring = smem + wave * kWaveLds;
+  uint8_t* ring = smem + wave * wave_lds<FMT>();
   const int slot = blockIdx.y;
   if (slot >= T.hdr[0]) return;
   const int t0 = T.slot_t0[slot], cnt = T.slot_cnt[slot];
@@ -615,7 +647,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
             wd.issue(rg, kb, st);
           },
           acc);
-    split_reduce<kDownRows>(smem, ns, wave, acc);
+    split_reduce<kDownRows, wave_lds<FMT>()>(smem, ns, wave, acc);
     if (wave == 0 && j < nt) {
 #pragma unroll
       for (int r = 0; r < kDownRows; ++r) {
@@ -693,25 +725,27 @@ static int split_for(int64_t items) {
   return ns;
 }
 
-template <int FMT, bool kFullK>
+// FG: gate/up table format, FD: down table format.
+template <int FG, int FD, bool kFullK>
 static int launch(const DecArgs& A, hipStream_t s) {
   const int groups_i = (int)cdiv(A.I, 16), groups_h = (int)cdiv(A.H, 16);
+  constexpr int lds_gu = wave_lds<FG>(), lds_dn = wave_lds<FD>();
   static bool attr_done = false;
   if (!attr_done) {
-    hipFuncSetAttribute((const void*)moe_dec_gate_up_kernel<FMT, kFullK>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        4 * kWaveLds);
-    hipFuncSetAttribute((const void*)moe_dec_down_kernel<FMT, kFullK>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        4 * kWaveLds);
+    (void)hipFuncSetAttribute((const void*)moe_dec_gate_up_kernel<FG, kFullK>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 4 * lds_gu);
+    (void)hipFuncSetAttribute((const void*)moe_dec_down_kernel<FD, kFullK>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 4 * lds_dn);
     attr_done = true;
   }
   const int dn_x = (int)cdiv(groups_h, kDownRows);
   const int ns_gu = split_for((int64_t)groups_i * A.max_slots), ns_dn = split_for((int64_t)dn_x * A.max_slots);
-  hipLaunchKernelGGL((moe_dec_gate_up_kernel<FMT, kFullK>), dim3((unsigned)groups_i, A.max_slots), dim3(64 * ns_gu),
-                     ns_gu * kWaveLds, s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I);
-  if (A.after_gate_up) hipEventRecord((hipEvent_t)A.after_gate_up, s);
-  hipLaunchKernelGGL((moe_dec_down_kernel<FMT, kFullK>), dim3((unsigned)dn_x, A.max_slots), dim3(64 * ns_dn),
-                     ns_dn * kWaveLds, s, A.down, A.T, A.act, A.I, A.contrib, A.H);
-  if (A.after_down) hipEventRecord((hipEvent_t)A.after_down, s);
+  hipLaunchKernelGGL((moe_dec_gate_up_kernel<FG, kFullK>), dim3((unsigned)groups_i, A.max_slots), dim3(64 * ns_gu),
+                     ns_gu * lds_gu, s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I);
+  if (A.after_gate_up) (void)hipEventRecord((hipEvent_t)A.after_gate_up, s);
+  hipLaunchKernelGGL((moe_dec_down_kernel<FD, kFullK>), dim3((unsigned)dn_x, A.max_slots), dim3(64 * ns_dn),
+                     ns_dn * lds_dn, s, A.down, A.T, A.act, A.I, A.contrib, A.H);
+  if (A.after_down) (void)hipEventRecord((hipEvent_t)A.after_down, s);
   hipLaunchKernelGGL(moe_dec_combine_kernel, dim3(A.R.B, (unsigned)cdiv(A.H, 256)), dim3(64), 0, s, A.T,
                      A.contrib, A.H, A.R.K, A.sh_y, A.sh_scale, A.out);
   return Q6MOE_OK;
@@ -721,10 +755,15 @@ bool dec_supported(int64_t B, int64_t K, int64_t E) {
   return B <= kDecMaxTokens && B * K <= kDecMaxEntries && E <= kDecMaxExperts;
 }
 
-int launch_moe_decode(int fmt, const DecArgs& A, hipStream_t s) {
+template <int FG, int FD>
+static int launch_k(const DecArgs& A, hipStream_t s) {
   const bool full = A.H % kQK == 0 && A.I % kQK == 0;
-  if (fmt == FMT_Q6) return full ? launch<FMT_Q6, true>(A, s) : launch<FMT_Q6, false>(A, s);
-  return full ? launch<FMT_Q4K, true>(A, s) : launch<FMT_Q4K, false>(A, s);
+  return full ? launch<FG, FD, true>(A, s) : launch<FG, FD, false>(A, s);
+}
+
+int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s) {
+  if (fmt_gu == FMT_Q6) return fmt_dn == FMT_Q8 ? launch_k<FMT_Q6, FMT_Q8>(A, s) : launch_k<FMT_Q6, FMT_Q6>(A, s);
+  return fmt_dn == FMT_Q8 ? launch_k<FMT_Q4K, FMT_Q8>(A, s) : launch_k<FMT_Q4K, FMT_Q4K>(A, s);
 }
 
 }  // namespace q6moe

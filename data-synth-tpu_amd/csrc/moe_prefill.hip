@@ -347,7 +347,7 @@ bool pf_supported(int fmt, int64_t H, int64_t I) {
 int64_t pf_tile_routes() { return pf::kM; }
 
 int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
-                       const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up) {
+                       const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up, bool with_down) {
   static bool attr_done = false;
   if (!attr_done) {
     (void)hipFuncSetAttribute((const void*)moe_pf_gate_up_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
@@ -358,8 +358,9 @@ int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs&
   hipLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds,
                      s, g, u, ws, x, H, ws.act, I);
   if (after_gate_up) (void)hipEventRecord((hipEvent_t)after_gate_up, s);
-  hipLaunchKernelGGL(moe_pf_down_kernel, grid(H / (32 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds, s,
-                     d, ws, ws.act, I, ws.y, H);
+  if (with_down)
+    hipLaunchKernelGGL(moe_pf_down_kernel, grid(H / (32 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds, s,
+                       d, ws, ws.act, I, ws.y, H);
   return Q6MOE_OK;
 }
 

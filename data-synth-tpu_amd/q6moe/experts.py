@@ -32,7 +32,8 @@ from . import _lib
 from .quant import BLOCK_LAYOUTS
 
 EXPERT_ROW_TILE = 128
-SUPPORTED = ("Q6_K", "Q4_K")
+SUPPORTED = ("Q6_K", "Q4_K", "Q8_0")  # tables pack_experts takes
+GATE_UP_TYPES = ("Q6_K", "Q4_K")       # gate/up types the kernels run; down is that type or Q8_0
 
 
 @dataclass(frozen=True)
@@ -142,8 +143,9 @@ def _as_table(t, qtype, rows, width, name):
 class ExpertFFN:
     """Callable returned by ``expert_parallel``."""
 
-    def __init__(self, qtype, hidden, intermediate, mode=0):
+    def __init__(self, qtype, hidden, intermediate, mode=0, down_qtype=None):
         self.qtype = qtype
+        self.down_qtype = down_qtype or qtype
         self.hidden = hidden
         self.intermediate = intermediate
         self.mode = mode
@@ -157,10 +159,10 @@ class ExpertFFN:
         """``events``: optional 5 timing events (torch.cuda.Event, already
         recorded once so they exist) stamped before routing, after routing,
         after gate/up, after down and after the combine."""
-        H, I, q = self.hidden, self.intermediate, self.qtype
+        H, I, q, qd = self.hidden, self.intermediate, self.qtype, self.down_qtype
         gate = _as_table(gate, q, I, H, "gate")
         up = _as_table(up, q, I, H, "up")
-        down = _as_table(down, q, H, I, "down")
+        down = _as_table(down, qd, H, I, "down")
         experts = gate.experts
         if up.experts != experts or down.experts != experts:
             raise ValueError("gate, up and down must hold the same number of experts")
@@ -188,7 +190,7 @@ class ExpertFFN:
             Is = sg.rows
             sg = _as_table(sg, q, Is, H, "shared gate")
             su = _as_table(su, q, Is, H, "shared up")
-            sd = _as_table(sd, q, H, Is, "shared down")
+            sd = _as_table(sd, qd, H, Is, "shared down")
             args.shared_gate, args.shared_up, args.shared_down = sg.c_table(), su.c_table(), sd.c_table()
             args.shared_intermediate = Is
             scale = shared.get("scale")
@@ -245,14 +247,14 @@ def expert_parallel(
         raise ValueError("Tensor parallel size must divide the device count")
     if intermediate % tensor_parallel or (intermediate // tensor_parallel) % BLOCK_LAYOUTS[down_type][0]:
         raise ValueError("Tensor slices must contain whole down quantization blocks")
-    if not (gate_type == up_type == down_type) or gate_type not in SUPPORTED:
+    if gate_type != up_type or gate_type not in GATE_UP_TYPES or down_type not in (gate_type, "Q8_0"):
         raise NotImplementedError(
-            f"this build runs Q6_K or Q4_K experts with one type for gate/up/down; got "
+            f"this build runs Q6_K or Q4_K gate/up with down of the same type or Q8_0; got "
             f"{gate_type}/{up_type}/{down_type}"
         )
     if compute == "int8_q8":
-        raise NotImplementedError("the int8_q8 policy applies to Q8_0 projections, which this build does not run")
-    return ExpertFFN(gate_type, hidden, intermediate)
+        raise NotImplementedError("the int8_q8 (W8A8) policy is not part of this build")
+    return ExpertFFN(gate_type, hidden, intermediate, down_qtype=down_type)
 
 
 def grouped_expert_parallel(mesh=None, *, gate_type, up_type, down_type, hidden, intermediate,

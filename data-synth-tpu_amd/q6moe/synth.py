@@ -75,12 +75,15 @@ def moe_layer(
     bias_sigma=None,
     shared_intermediate=0,
     pack=True,
+    down_qtype=None,
 ):
     """Draw order: x [B, H]; logits [B, E]; bias [E] (if bias_sigma); then per expert
     gate [I, H], up [I, H], down [H, I]; then the shared expert gate, up, down.
 
     Returns raw GGUF tables ``gate/up/down`` [E, rows, blocks, bytes] and, for
     Q6_K with ``pack``, the stacked SoA planes ``*_data`` / ``*_scales``.
+    ``down_qtype`` (default ``qtype``) quantizes the down projections (routed
+    and shared), e.g. Q6_K gate/up with Q8_0 down.
     """
     rng = np.random.default_rng(seed)
     x = _normal(rng, (tokens, hidden))
@@ -88,13 +91,15 @@ def moe_layer(
     if bias_sigma is not None:
         logits = (logits + _normal(rng, (experts,), bias_sigma)[None, :]).astype(np.float32)
     quant = QUANTIZERS[qtype]
+    down_qtype = down_qtype or qtype
+    quant_d = QUANTIZERS[down_qtype]
     tables = {"gate": [], "up": [], "down": []}
     for _ in range(experts):
         tables["gate"].append(quant(_normal(rng, (intermediate, hidden), sigma)))
         tables["up"].append(quant(_normal(rng, (intermediate, hidden), sigma)))
-        tables["down"].append(quant(_normal(rng, (hidden, intermediate), sigma)))
+        tables["down"].append(quant_d(_normal(rng, (hidden, intermediate), sigma)))
     out = dict(x=x, logits=logits, experts=experts, top_k=top_k, hidden=hidden,
-               intermediate=intermediate, qtype=qtype)
+               intermediate=intermediate, qtype=qtype, down_qtype=down_qtype)
     for name, parts in tables.items():
         out[name] = np.stack(parts)
     ids, weights = softmax_topk(logits, top_k)
@@ -103,12 +108,13 @@ def moe_layer(
         out["shared"] = dict(
             gate=quant(_normal(rng, (shared_intermediate, hidden), sigma)),
             up=quant(_normal(rng, (shared_intermediate, hidden), sigma)),
-            down=quant(_normal(rng, (hidden, shared_intermediate), sigma)),
+            down=quant_d(_normal(rng, (hidden, shared_intermediate), sigma)),
             intermediate=shared_intermediate,
         )
-    if pack and qtype == "Q6_K":
-        for name, width in (("gate", hidden), ("up", hidden), ("down", intermediate)):
-            out[name + "_data"], out[name + "_scales"] = pack_q6_experts(out[name], width)
+    if pack:
+        for name, width, q in (("gate", hidden, qtype), ("up", hidden, qtype), ("down", intermediate, down_qtype)):
+            if q == "Q6_K":
+                out[name + "_data"], out[name + "_scales"] = pack_q6_experts(out[name], width)
     return out
 
 

@@ -36,8 +36,9 @@ def assert_moe_close(got, want, exact_frac=0.9):
 
 def _run(L, device, mode=0, shared=None, weights=None, ids=None):
     q, H, I = L["qtype"], L["hidden"], L["intermediate"]
-    fn = expert_parallel(None, gate_type=q, up_type=q, down_type=q, hidden=H, intermediate=I)
-    tabs = [pack_experts(L[n], q, I if n != "down" else H, H if n != "down" else I, device)
+    qd = L.get("down_qtype", q)
+    fn = expert_parallel(None, gate_type=q, up_type=q, down_type=qd, hidden=H, intermediate=I)
+    tabs = [pack_experts(L[n], q if n != "down" else qd, I if n != "down" else H, H if n != "down" else I, device)
             for n in ("gate", "up", "down")]
     x = torch.from_numpy(L["x"]).to(device).to(torch.bfloat16)
     ids = torch.from_numpy(L["ids"] if ids is None else ids).to(device)
@@ -47,7 +48,7 @@ def _run(L, device, mode=0, shared=None, weights=None, ids=None):
         Is = shared["intermediate"]
         sh = dict(gate=pack_experts(shared["gate"][None], q, Is, H, device),
                   up=pack_experts(shared["up"][None], q, Is, H, device),
-                  down=pack_experts(shared["down"][None], q, H, Is, device))
+                  down=pack_experts(shared["down"][None], qd, H, Is, device))
     fn.mode = mode
     try:
         out = fn(*tabs, x, ids, w, shared=sh)
@@ -58,6 +59,7 @@ def _run(L, device, mode=0, shared=None, weights=None, ids=None):
 
 def _oracle(L, shared=None, weights=None, ids=None):
     q = L["qtype"]
+    qd = L.get("down_qtype", q)
     sh = None
     if shared is not None:
         from oracle.gguf import dequantize_rows
@@ -66,11 +68,11 @@ def _oracle(L, shared=None, weights=None, ids=None):
         H, Is = L["hidden"], shared["intermediate"]
         sh = dict(gate=bf16_round(dequantize_rows(shared["gate"], q, H)),
                   up=bf16_round(dequantize_rows(shared["up"], q, H)),
-                  down=bf16_round(dequantize_rows(shared["down"], q, Is)))
+                  down=bf16_round(dequantize_rows(shared["down"], qd, Is)))
     return oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"],
                                  L["ids"] if ids is None else ids,
                                  L["weights"] if weights is None else weights,
-                                 types=(q, q, q), hidden=L["hidden"], intermediate=L["intermediate"],
+                                 types=(q, q, qd), hidden=L["hidden"], intermediate=L["intermediate"],
                                  shared=sh)
 
 
@@ -235,3 +237,47 @@ def test_pack_is_the_unit_major_byte_permutation(device, qtype, rows, width):
     raw = np.random.default_rng(rows + width).integers(0, 256, size=(3, rows * (width // 256) * bs), dtype=np.uint8)
     table = pack_experts(raw, qtype, rows, width, device)
     np.testing.assert_array_equal(table.data.cpu().numpy(), _unit_major(raw, qtype, rows, width))
+
+
+
+def _q8_unit_major(raw, rows, width):
+    """Q8_0 unit-major table restated with NumPy: 16 rows x 8 blocks of 34 B
+    per unit; lane l (row j = l % 16, jA = l // 16) holds at 1024g + 16l the
+    16 codes of K positions 64g + 16jA + [0, 16), i.e. codes 16(jA % 2) + [0, 16)
+    of block 2g + jA // 2; the rows' FP16 block scales follow at
+    4096 + 8(2j + h) + 2g (block 2g + h). Missing rows and blocks are zero."""
+    E, nb, kbs, groups = raw.shape[0], width // 32, -(-width // 256), -(-rows // 16)
+    pad = np.zeros((E, groups * 16, kbs * 8, 34), np.uint8)
+    pad[:, :rows, :nb] = raw.reshape(E, rows, nb, 34)
+    blk = pad.reshape(E, groups, 16, kbs, 8, 34).transpose(0, 1, 3, 2, 4, 5)  # [E, g, kb, row, block, 34]
+    lane = np.arange(64)
+    j, jA = lane % 16, lane // 16
+    chunks = np.arange(4)
+    b = 2 * chunks[:, None] + (jA // 2)[None, :]                               # [chunk, lane]
+    off = 2 + 16 * (jA % 2)[None, :, None] + np.arange(16)[None, None, :]      # [1, lane, 16]
+    codes = blk[:, :, :, j[None, :, None], b[:, :, None], off]                 # [E, g, kb, chunk, lane, 16]
+    h, g = np.meshgrid(np.arange(2), chunks, indexing="ij")
+    d = blk[:, :, :, :, (2 * g + h).reshape(-1), 0:2]                          # [E, g, kb, row, 8 (h, g), 2]
+    unit = np.concatenate([codes.reshape(E, groups, kbs, 4096), d.reshape(E, groups, kbs, 256)], axis=-1)
+    return unit.reshape(E, -1)
+
+
+@pytest.mark.parametrize("rows,width", [(40, 512), (16, 256), (33, 288)])
+def test_pack_q8_0_is_the_unit_major_byte_permutation(device, rows, width):
+    raw = np.random.default_rng(rows * width).integers(0, 256, size=(3, rows * (width // 32) * 34), dtype=np.uint8)
+    table = pack_experts(raw, "Q8_0", rows, width, device)
+    np.testing.assert_array_equal(table.data.cpu().numpy(), _q8_unit_major(raw, rows, width))
+
+
+@pytest.mark.parametrize("qtype,tokens,mode,shared", [
+    ("Q6_K", 8, 1, 0), ("Q6_K", 20, 1, 512), ("Q4_K", 8, 1, 512),
+    ("Q6_K", 100, 2, 0), ("Q6_K", 300, 0, 512), ("Q4_K", 100, 2, 0)])
+def test_q8_0_down_matches_oracle(device, qtype, tokens, mode, shared):
+    # The real checkpoint's mix: Q6_K (or Q4_K) gate/up with Q8_0 down, through
+    # the decode kernels (mode 1) and the prefill path (mode 2, or 0 above 64
+    # tokens: tiled Q6_K gate/up, generic Q8_0 down).
+    L = moe_layer(seed=41 + tokens, experts=8, top_k=3, hidden=512, intermediate=256, tokens=tokens,
+                  qtype=qtype, down_qtype="Q8_0", sigma=0.02, shared_intermediate=shared, pack=False)
+    sh = L.get("shared")
+    got, _ = _run(L, device, mode=mode, shared=sh)
+    assert_moe_close(got, _oracle(L, shared=sh))
