@@ -97,18 +97,21 @@ int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, int64_t width
 
 /*
  * Expert tables of the routed FFN are unit-major, packed once from the GGUF
- * tables the reference keeps per expert ([E, bytes_per_expert], raw Q6_K or
- * Q4_K rows; kaggle/qwen38_tpu/parallel.py:40-87). A unit is 16 output rows x
- * one 256-wide K block (Q6_K 3360 bytes, Q4_K 2304 bytes; rows padded with
- * zeros to a multiple of 16); an expert's units run [row group][K block].
- * Q4_K units hold the rows' block bytes in 16-byte chunks. Q6_K units are
- * bit-planar: the same 6-bit codes, sub-scales and FP16 scales, rearranged per
- * decoding lane (map in csrc/moe_common.h and csrc/q6moe_device.h). Either
- * way the repack is lossless, so decoded values are those of the GGUF rows.
+ * tables the reference keeps per expert ([E, bytes_per_expert], raw Q6_K,
+ * Q4_K or Q8_0 rows; kaggle/qwen38_tpu/parallel.py:40-87). A unit is 16 output
+ * rows x one 256-wide K block (Q6_K 3360 bytes, Q4_K 2304, Q8_0 4352; rows and
+ * missing Q8_0 blocks padded with zeros); an expert's units run [row group][K
+ * block]. Q4_K units hold the rows' block bytes in 16-byte chunks. Q6_K units
+ * are bit-planar: the same 6-bit codes, sub-scales and FP16 scales, rearranged
+ * per decoding lane; Q8_0 units hold each lane's 16 codes per 64-column chunk
+ * and then the rows' FP16 block scales (maps in csrc/moe_common.h and
+ * csrc/q6moe_device.h). The repack is lossless, so decoded values are those of
+ * the GGUF rows.
  */
 size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width); /* per expert; 0 if invalid */
 
-/* raw [experts][rows][ceil(width/256)][210 or 144] -> dst [experts][table bytes]
+/* raw [experts][rows][ceil(width/256)][210 or 144] (Q6_K, Q4_K) or
+   [experts][rows][width/32][34] (Q8_0) -> dst [experts][table bytes]
    (dst 16-byte aligned). No counterpart call in the reference, whose matmul
    reads GGUF bytes directly; this is its one-time load-side preparation. */
 int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, int64_t rows, int64_t width,
@@ -116,7 +119,7 @@ int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, int64_t rows,
 
 /* Weight tables of one projection for all experts. */
 typedef struct q6moe_table {
-  int qtype;                /* Q6MOE_Q6_K or Q6MOE_Q4_K */
+  int qtype;                /* gate/up: Q6MOE_Q6_K or Q6MOE_Q4_K; down: the same or Q6MOE_Q8_0 */
   const uint8_t* data;      /* unit-major table of expert e at data + e * data_stride */
   int64_t data_stride;      /* bytes between experts (>= q6moe_moe_table_bytes, multiple of 16) */
   const uint8_t* scales;    /* unused (NULL): the scales live in the units */
