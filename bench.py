@@ -218,6 +218,40 @@ def measure_q4_shared(dev):
     return out
 
 
+def measure_q8_down(dev):
+    """The decode step of the headline layer (128 experts, top-8, H 2048, I 768, 8 tokens,
+    seed 1) with the checkpoint's mix: Q6_K gate/up and Q8_0 down. Layer copies rotate so
+    that one rotation's active bytes exceed 3x the Infinity Cache."""
+    import numpy as np
+    import torch
+
+    from q6moe.experts import expert_parallel, pack_experts
+    from q6moe.synth import moe_layer
+
+    L = moe_layer(seed=1, experts=EXPERTS, top_k=TOP_K, hidden=HIDDEN, intermediate=INTER, tokens=TOKENS,
+                  down_qtype="Q8_0", pack=False)
+    base = [pack_experts(L["gate"], "Q6_K", INTER, HIDDEN, dev), pack_experts(L["up"], "Q6_K", INTER, HIDDEN, dev),
+            pack_experts(L["down"], "Q8_0", HIDDEN, INTER, dev)]
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q8_0", hidden=HIDDEN,
+                         intermediate=INTER)
+    active = len(np.unique(L["ids"]))
+    down_bytes = HIDDEN * (INTER // 32) * 34
+    nbytes = active * (2 * Q6_PROJ_BYTES + down_bytes) + 2 * TOKENS * HIDDEN * 2 + TOKENS * TOP_K * 6
+    copies = max(2, -(-3 * 256 * 2**20 // nbytes))
+    layers = [base] + [[type(t)(t.qtype, t.data.clone(), None, t.rows, t.width) for t in base]
+                       for _ in range(copies - 1)]
+    x = torch.from_numpy(L["x"]).to(dev).to(torch.bfloat16)
+    ids = torch.from_numpy(L["ids"]).to(dev)
+    w = torch.from_numpy(L["weights"]).to(dev).to(torch.bfloat16)
+    ws = torch.empty(fn.workspace_bytes(TOKENS, TOP_K, EXPERTS), dtype=torch.uint8, device=dev)
+    o = torch.empty((TOKENS, HIDDEN), dtype=torch.bfloat16, device=dev)
+    us = _time_calls(lambda i: fn(*layers[i % copies], x, ids, w, workspace=ws, out=o), 200)
+    return {"workload": "moe_decode_q6k_gateup_q8_0_down_e128_top8_h2048_i768_b8", "us_per_step": round(us, 2),
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "active_experts": active,
+            "bytes_per_step": nbytes, "layer_copies": copies}
+
+
 def measure_kv_gather(dev):
     """Paged INT8 KV gather + dequant of every cached token: batch 8, 4 KV heads x 128,
     32768 tokens per sequence in pages of 256, FP32 per-token-per-head scales, seed 4.
@@ -393,9 +427,9 @@ def main():
         log("timing the prefill step (4096 tokens, seed 2) ...")
         result["prefill"] = measure_prefill(dev, steps=10, warmup=2)
     if not args.no_extras:
-        log("timing the single projection, the Q4_K + shared layer and the KV gather ...")
+        log("timing the single projection, the Q4_K + shared layer, the Q8_0-down layer and the KV gather ...")
         result["extras"] = {"projection": measure_projection(dev), "q4k_shared": measure_q4_shared(dev),
-                            "kv_gather": measure_kv_gather(dev)}
+                            "q8_0_down": measure_q8_down(dev), "kv_gather": measure_kv_gather(dev)}
     if not args.no_cpu_baseline:
         log("timing the CPU oracle on one step (one thread) ...")
         secs = cpu_baseline(L)
