@@ -83,6 +83,28 @@ class KvArgs(ctypes.Structure):
     ]
 
 
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp),
+        ("k_codes", _vp),
+        ("v_codes", _vp),
+        ("k_scales", _vp),
+        ("v_scales", _vp),
+        ("page_table", _vp),
+        ("lengths", _vp),
+        ("batch", _i64),
+        ("query_heads", _i64),
+        ("kv_heads", _i64),
+        ("head_dim", _i64),
+        ("pool_pages", _i64),
+        ("pages_per_seq", _i64),
+        ("page_size", _i64),
+        ("out", _vp),
+        ("workspace", _vp),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class KvWriteArgs(ctypes.Structure):
     _fields_ = [
         ("x", _vp),
@@ -120,6 +142,8 @@ SIGNATURES = {
     "q6moe_kv_read": (_int, [ctypes.POINTER(KvArgs), _vp]),
     "q6moe_kv_quantize": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _vp]),
     "q6moe_kv_write": (_int, [ctypes.POINTER(KvWriteArgs), _vp]),
+    "q6moe_attn_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
+    "q6moe_kv_decode_attention": (_int, [ctypes.POINTER(AttnArgs), _vp]),
 }
 
 _lib = None

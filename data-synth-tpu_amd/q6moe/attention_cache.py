@@ -197,6 +197,54 @@ def read_paged(pool, scales, page_table, *, page_size, kv_heads, head_dim, group
     return out
 
 
+def paged_decode_attention(q, k_pool, k_scales, v_pool, v_scales, page_table, lengths, *, page_size, kv_heads,
+                           workspace=None, out=None):
+    """Decode attention over the paged INT8 cache with the dequant fused in
+    (attention_cache.py:159-169 after read_quantized :71-81): q BF16 [B, Hq, 128]
+    -> BF16 [B, Hq, 128], the attention output before the reference's gate and
+    out projection. Pools int8 [pages, page_size, kv_heads*128], scales FP32
+    [pages, page_size, kv_heads] (one per token and head), page_table int32
+    [B, pages_per_seq], lengths int32 [B] attended tokens (the reference's
+    position + 1). No BF16 copy of K or V is made.
+    """
+    head_dim = 128
+    if q.dtype != torch.bfloat16 or q.ndim != 3 or q.shape[2] != head_dim:
+        raise ValueError("q must be BF16 [batch, query_heads, 128]")
+    for pool in (k_pool, v_pool):
+        if pool.dtype != torch.int8 or pool.ndim < 3 or pool.shape[1] != page_size or \
+                pool[0, 0].numel() != kv_heads * head_dim:
+            raise ValueError("pools must be int8 [pages, page_size, kv_heads * 128]")
+    for sc in (k_scales, v_scales):
+        if sc.dtype != torch.float32 or sc.numel() != k_pool.shape[0] * page_size * kv_heads:
+            raise ValueError("scales must be FP32 [pages, page_size, kv_heads]")
+    batch, hq = q.shape[0], q.shape[1]
+    table = page_table.to(device=q.device, dtype=torch.int32).contiguous()
+    lens = lengths.to(device=q.device, dtype=torch.int32).contiguous()
+    if table.shape[0] != batch or lens.shape != (batch,):
+        raise ValueError("page_table must be [batch, pages_per_seq] and lengths [batch]")
+    pps = table.shape[1]
+    lib = _lib.load()
+    need = int(lib.q6moe_attn_workspace_size(batch, hq, kv_heads, pps, page_size))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    if out is None:
+        out = torch.empty_like(q)
+    q = q.contiguous()
+    k_pool, v_pool, k_scales, v_scales = (t.contiguous() for t in (k_pool, v_pool, k_scales, v_scales))
+    a = _lib.AttnArgs()
+    a.q, a.k_codes, a.v_codes = q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr()
+    a.k_scales, a.v_scales = k_scales.data_ptr(), v_scales.data_ptr()
+    a.page_table, a.lengths = table.data_ptr(), lens.data_ptr()
+    a.batch, a.query_heads, a.kv_heads, a.head_dim = batch, hq, kv_heads, head_dim
+    a.pool_pages, a.pages_per_seq, a.page_size = k_pool.shape[0], pps, page_size
+    a.out = out.data_ptr()
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    with torch.cuda.device(q.device):
+        rc = lib.q6moe_kv_decode_attention(ctypes.byref(a), _lib.stream_handle(q.device))
+    _lib.check(rc, "kv_decode_attention")
+    return out
+
+
 def gather_scale_plane(plane, indices, groups, *, method="indexed"):
     """[B*G, T] scale plane, [B, S] indices -> [B, S, G] (attention_cache.py:46-68)."""
     if indices.ndim != 2 or plane.ndim != 2 or plane.shape[0] != indices.shape[0] * groups:

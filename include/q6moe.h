@@ -224,6 +224,41 @@ typedef struct q6moe_kv_write_args {
 
 int q6moe_kv_write(const q6moe_kv_write_args* args, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Decode attention over the paged INT8 KV cache.                           */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * The core of the reference's decode attention step (kaggle/qwen38_tpu/
+ * attention_cache.py:159-169: scores of the query against read_quantized keys,
+ * RNE to BF16, divided by sqrt(D), RNE; numerics.softmax over the attended
+ * tokens; RNE_bf16(prob) times read_quantized values with FP32 accumulation;
+ * RNE to BF16), with the dequant fused in: no BF16 copy of K or V is written.
+ * Replaces read_quantized(k), read_quantized(v) and the two einsums around
+ * the softmax for one query token per sequence; the output gate and the out
+ * projection stay with the caller. Paged cache, FP32 scale per token and KV
+ * head (group = head_dim), head_dim 128, up to 8 query heads per KV head.
+ * The reference's mask ``indices <= lengths`` is lengths[b] = position + 1
+ * attended tokens here (tokens 0 .. lengths[b]-1; clamped into [1, capacity]).
+ */
+typedef struct q6moe_attn_args {
+  const uint16_t* q;          /* BF16 [B, Hq, 128] */
+  const int8_t* k_codes;      /* [pool_pages, page_size, KVH*128] */
+  const int8_t* v_codes;
+  const float* k_scales;      /* FP32 [pool_pages*page_size, KVH] */
+  const float* v_scales;
+  const int32_t* page_table;  /* [B, pages_per_seq]; entries outside [0, pool_pages) read as 0 */
+  const int32_t* lengths;     /* [B] attended tokens */
+  int64_t batch, query_heads, kv_heads, head_dim, pool_pages, pages_per_seq, page_size;
+  uint16_t* out;              /* BF16 [B, Hq, 128] */
+  void* workspace;            /* >= q6moe_attn_workspace_size(...) bytes, 256-byte aligned */
+  size_t workspace_bytes;
+} q6moe_attn_args;
+
+size_t q6moe_attn_workspace_size(int64_t batch, int64_t query_heads, int64_t kv_heads, int64_t pages_per_seq,
+                                 int64_t page_size);
+int q6moe_kv_decode_attention(const q6moe_attn_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -250,3 +250,40 @@ def test_kv_paged_read_equals_dense_read_of_the_same_tokens():
             page, slot = table[b, t // P], t % P
             want = packed_q6.bf16_round(pool[page, slot].astype(np.float32) * scales[page, slot][:, None])
             np.testing.assert_array_equal(got[b, t], want)
+
+
+def test_decode_attention_oracle_closed_forms():
+    rng = np.random.default_rng(5)
+    b, kvh, r, d, t = 2, 2, 4, 128, 48
+    q = packed_q6.bf16_round(rng.standard_normal((b, kvh * r, d)).astype(np.float32))
+    v = packed_q6.bf16_round(rng.standard_normal((b, t, kvh, d)).astype(np.float32))
+    lengths = np.array([48, 17])
+    # equal keys: every attended token has the same score, so prob = RNE(1/n) and
+    # out = RNE(RNE(1/n) * sum of the attended values)
+    k_eq = np.broadcast_to(v[:, :1], v.shape).copy()
+    got = kv.decode_attention(q, k_eq, v, lengths)
+    for i, n in enumerate(lengths):
+        p = packed_q6.bf16_round(np.float32(1) / np.float32(n))
+        want = packed_q6.bf16_round(p * v[i, :n].sum(axis=0, dtype=np.float32))  # [kvh, d]
+        np.testing.assert_allclose(got[i].reshape(kvh, r, d), np.repeat(want[:, None], r, axis=1),
+                                   rtol=2e-2, atol=2e-2)
+    # a dominant key: token 5 of each sequence equals 4x the query of head 0 of
+    # its group, so that head attends (almost) only to token 5 and outputs v[5]
+    k = packed_q6.bf16_round(0.01 * rng.standard_normal((b, t, kvh, d)).astype(np.float32))
+    for i in range(b):
+        for g in range(kvh):
+            k[i, 5, g] = 4 * q[i, g * r]
+    got = kv.decode_attention(q, k, v, lengths)
+    for i in range(b):
+        for g in range(kvh):
+            np.testing.assert_allclose(got[i, g * r], v[i, 5, g], rtol=1e-2, atol=1e-2)
+    # against an FP64 softmax attention without the BF16 roundings
+    k = packed_q6.bf16_round(rng.standard_normal((b, t, kvh, d)).astype(np.float32))
+    got = kv.decode_attention(q, k, v, lengths)
+    for i, n in enumerate(lengths):
+        for h in range(kvh * r):
+            s = (k[i, :n, h // r].astype(np.float64) @ q[i, h].astype(np.float64)) / np.sqrt(d)
+            p = np.exp(s - s.max())
+            p /= p.sum()
+            want = p @ v[i, :n, h // r].astype(np.float64)
+            assert np.max(np.abs(got[i, h] - want)) <= 2e-2 * np.abs(want).max() + 1e-3
