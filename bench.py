@@ -283,6 +283,38 @@ def measure_kv_gather(dev):
             "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}
 
 
+def measure_kv_attention(dev):
+    """Fused decode attention over the same paged INT8 cache as the gather (batch 8, 32
+    query heads over 4 KV heads, head_dim 128, 32768 attended tokens per sequence, pages of
+    256, FP32 per-token-per-head scales, seed 4): the work of the gather plus the two
+    attention einsums, without the BF16 copy. Three pool copies rotate."""
+    import torch
+
+    from q6moe.attention_cache import paged_decode_attention
+    from q6moe.synth import kv_pages
+
+    K = kv_pages(seed=4)
+    P, H = K["page_size"], K["kv_heads"]
+    table = torch.from_numpy(K["page_table"]).to(dev)
+    pools = [{n: torch.from_numpy(K[n]).to(dev) for n in ("k", "k_scale", "v", "v_scale")} for _ in range(3)]
+    q = torch.from_numpy(K["q"]).to(dev).to(torch.bfloat16)
+    lengths = torch.full((K["batch"],), K["context"], dtype=torch.int32, device=dev)
+    o = torch.empty_like(q)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+
+    def call(i):
+        p = pools[i % 3]
+        paged_decode_attention(q, p["k"], p["k_scale"], p["v"], p["v_scale"], table, lengths, page_size=P,
+                               kv_heads=H, workspace=ws, out=o)
+
+    us = _time_calls(call, 30)
+    nbytes = sum(pools[0][n].numel() * pools[0][n].element_size() for n in pools[0]) + table.numel() * 4 + \
+        2 * q.numel() * 2
+    return {"workload": "kv_paged_decode_attention_b8_hq32_kvh4_d128_ctx32768_p256_f32scale",
+            "us_per_call": round(us, 1), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}
+
+
 def cpu_baseline(L):
     """The NumPy oracle (one thread) on one full decode step of the same workload."""
     from threadpoolctl import threadpool_limits
@@ -427,9 +459,10 @@ def main():
         log("timing the prefill step (4096 tokens, seed 2) ...")
         result["prefill"] = measure_prefill(dev, steps=10, warmup=2)
     if not args.no_extras:
-        log("timing the single projection, the Q4_K + shared layer, the Q8_0-down layer and the KV gather ...")
+        log("timing the single projection, the Q4_K + shared layer, the Q8_0-down layer, the KV gather and attention ...")
         result["extras"] = {"projection": measure_projection(dev), "q4k_shared": measure_q4_shared(dev),
-                            "q8_0_down": measure_q8_down(dev), "kv_gather": measure_kv_gather(dev)}
+                            "q8_0_down": measure_q8_down(dev), "kv_gather": measure_kv_gather(dev),
+                            "kv_attention": measure_kv_attention(dev)}
     if not args.no_cpu_baseline:
         log("timing the CPU oracle on one step (one thread) ...")
         secs = cpu_baseline(L)

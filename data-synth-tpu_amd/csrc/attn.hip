@@ -19,10 +19,12 @@
 //   2. attn_stats_kernel: per (sequence, query head), the maximum and the sum
 //      of exp(score - max) over the attended tokens (fixed reduction order).
 //   3. attn_pv_kernel: per chunk, the workgroup forms RNE_bf16(prob) once per
-//      (token, head) in LDS, then each lane accumulates 8 heads x 8 channels
-//      over token pairs with v_dot2_f32_bf16 (two tokens per instruction);
-//      the chunk's partial sums go to the workspace.
-//   4. attn_combine_kernel: partial sums over chunks in chunk order, RNE.
+//      (head, token) in LDS; each wave then runs P.V for its 64 tokens on
+//      MFMA with the dequantised values as A operand (row = 8 channels apart,
+//      so a lane dequantises the 8x8 code block it loaded straight into eight
+//      tiles' operands) and the probabilities as B; the chunk's partial sums
+//      go to the workspace.
+//   4. attn_combine_kernel: partial sums over chunks in a fixed order, RNE.
 //
 // HBM-bound: the INT8 codes and scales of K and V are read once.
 #include "q6moe_api.h"
@@ -57,10 +59,12 @@ __device__ __forceinline__ int attn_len(const AttnParams& p, int b) {
   return n < 1 ? 1 : (n > p.cap ? p.cap : n);
 }
 
-// Pool row of token t of sequence b, or -1 for an unmapped page (read as 0).
-__device__ __forceinline__ int64_t attn_row(const AttnParams& p, int b, int t) {
-  const int64_t pg = p.table[(int64_t)b * p.pps + t / p.page];
-  return pg < 0 || pg >= p.pool_pages ? -1 : pg * p.page + t % p.page;
+// Pool row of token t0 of sequence b, or -1 for an unmapped page (read as 0).
+// A wave's 64 tokens t0 + [0, 64) (t0 a multiple of 64) lie in one page,
+// since page_size is a multiple of 64: one table lookup per wave.
+__device__ __forceinline__ int64_t attn_base_row(const AttnParams& p, int b, int t0) {
+  const int64_t pg = p.table[(int64_t)b * p.pps + t0 / p.page];
+  return pg < 0 || pg >= p.pool_pages ? -1 : pg * p.page + t0 % p.page;
 }
 
 __global__ void __launch_bounds__(256) attn_scores_kernel(AttnParams p) {
@@ -83,18 +87,24 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnParams p) {
   }
   const float kDiv = static_cast<float>(11.313708498984761);  // float32(128 ** 0.5) (attention_cache.py:163)
   const int64_t rowbytes = (int64_t)p.kvh * kAttnD;
+  const int64_t base = attn_base_row(p, b, t0);
+  // the wave's rows start at pool row base (wave-uniform); the lane adds its
+  // token row col and channel group 32-bit offsets, row block rb adds 16 rows
+  const int8_t* kw = p.kc + (base < 0 ? 0 : base) * rowbytes + kh * kAttnD;
+  const float* sw = p.ks + (base < 0 ? 0 : base) * p.kvh + kh;
+  const uint32_t lane_off = (uint32_t)col * (uint32_t)rowbytes + 32u * g;
+  const uint32_t rb_off = 16u * (uint32_t)rowbytes;
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
     // A operand: token t (row col of the block), channels 32g + [0, 32)
     const int t = t0 + 16 * rb + col;
-    const int64_t row = t < n ? attn_row(p, b, t) : -1;
     u32x4 c0 = {0u, 0u, 0u, 0u}, c1 = {0u, 0u, 0u, 0u};
     float sc = 0.f;
-    if (row >= 0) {
-      const int8_t* src = p.kc + row * rowbytes + kh * kAttnD + 32 * g;
+    if (t < n && base >= 0) {
+      const int8_t* src = kw + lane_off + rb * rb_off;
       c0 = *reinterpret_cast<const u32x4*>(src);
       c1 = *reinterpret_cast<const u32x4*>(src + 16);
-      sc = p.ks[row * p.kvh + kh];
+      sc = sw[(16 * rb + col) * p.kvh];
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -124,11 +134,13 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnParams p) {
   }
 }
 
-// Sum of a 256-thread block in a fixed order (warp-level tree in LDS).
+constexpr int kStatsThreads = 1024;
+
+// Max or sum over a kStatsThreads block in a fixed order (tree in LDS).
 __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
   red[threadIdx.x] = v;
   __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
+  for (int off = kStatsThreads / 2; off > 0; off >>= 1) {
     if ((int)threadIdx.x < off) {
       const float a = red[threadIdx.x], c = red[threadIdx.x + off];
       red[threadIdx.x] = is_max ? fmaxf(a, c) : a + c;
@@ -140,16 +152,29 @@ __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) 
   return r;
 }
 
-__global__ void __launch_bounds__(256) attn_stats_kernel(AttnParams p) {
-  __shared__ float red[256];
+__global__ void __launch_bounds__(kStatsThreads) attn_stats_kernel(AttnParams p) {
+  __shared__ float red[kStatsThreads];
   const int h = blockIdx.x, b = blockIdx.y;
   const int n = attn_len(p, b);
   const uint16_t* s = p.s + ((int64_t)b * p.hq + h) * p.cap;
+  // 8 scores (16 bytes) per thread and step; cap is a multiple of 64, so the
+  // loads stay inside the row, and tokens from n on are skipped
+  auto score = [&](const u32x4& v, int k) { return bf16_to_float((uint16_t)(v[k >> 1] >> (16 * (k & 1)))); };
   float m = -__builtin_inff();
-  for (int t = threadIdx.x; t < n; t += 256) m = fmaxf(m, bf16_to_float(s[t]));
+  for (int t0 = 8 * threadIdx.x; t0 < n; t0 += 8 * kStatsThreads) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(s + t0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (t0 + k < n) m = fmaxf(m, score(v, k));
+  }
   m = block_reduce(m, red, true);
   float l = 0.f;
-  for (int t = threadIdx.x; t < n; t += 256) l += expf(bf16_to_float(s[t]) - m);
+  for (int t0 = 8 * threadIdx.x; t0 < n; t0 += 8 * kStatsThreads) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(s + t0);
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (t0 + k < n) l += expf(score(v, k) - m);
+  }
   l = block_reduce(l, red, false);
   if (threadIdx.x == 0) {
     p.stats[((int64_t)b * p.hq + h) * 2] = m;
@@ -158,93 +183,81 @@ __global__ void __launch_bounds__(256) attn_stats_kernel(AttnParams p) {
 }
 
 __global__ void __launch_bounds__(256) attn_pv_kernel(AttnParams p) {
-  __shared__ uint32_t pp[kAttnChunk / 2][kAttnR];  // BF16 prob pairs (tokens 2m, 2m+1) per head
-  __shared__ float red[4][kAttnR][kAttnD];         // per-wave partial sums
+  __shared__ __attribute__((aligned(16))) uint16_t pr[kAttnR][kAttnChunk];  // RNE_bf16(prob) [head][token]
+  __shared__ float red[4][kAttnR][kAttnD];                              // per-wave partial sums
   const int chunk = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = attn_len(p, b);
   const int c0 = chunk * kAttnChunk;
   if (c0 >= n) return;  // uniform over the workgroup
   const int nv = n - c0 < kAttnChunk ? n - c0 : kAttnChunk;
-  // 1. RNE_bf16(prob) of every (token, head) of the chunk, once
+  const int r16 = lane & 15, kg = lane >> 4;
+  // V codes first (their loads overlap the probability pass): lane (r16, kg)
+  // reads channels 8*r16 + [0, 8) of the wave's tokens 32s + 8kg + j (s = 0, 1;
+  // j = 0..7); tokens from nv on and unmapped pages read as 0.
+  const int64_t rowbytes = (int64_t)p.kvh * kAttnD;
+  const int64_t base = 64 * wave < nv ? attn_base_row(p, b, c0 + 64 * wave) : -1;
+  const int8_t* vw = p.vc + (base < 0 ? 0 : base) * rowbytes + kh * kAttnD;
+  const float* sw = p.vs + ((base < 0 ? 0 : base) + 8 * kg) * p.kvh + kh;
+  const uint32_t lane_off = (uint32_t)(8 * kg) * (uint32_t)rowbytes + 8u * r16;
+  u32x2 wv[2][8];
+  float sv[2][8];
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      wv[st][j] = u32x2{0u, 0u};
+      sv[st][j] = 0.f;
+      if (base >= 0 && 64 * wave + 32 * st + 8 * kg + j < nv) {
+        wv[st][j] = *reinterpret_cast<const u32x2*>(vw + lane_off + (uint32_t)(32 * st + j) * (uint32_t)rowbytes);
+        sv[st][j] = sw[(32 * st + j) * p.kvh];
+      }
+    }
+  // 1. RNE_bf16(prob) of every (head, token) of the chunk, once; heads from r
+  //    on are 0 (MFMA columns 8-15 take zero operands below)
   {
     const int t = threadIdx.x;
-    uint16_t* ph = reinterpret_cast<uint16_t*>(&pp[t >> 1][0]) + (t & 1);
 #pragma unroll
     for (int h = 0; h < kAttnR; ++h) {
-      float pr = 0.f;
+      float q = 0.f;
       if (t < nv && h < p.r) {
         const int64_t hh = (int64_t)b * p.hq + kh * p.r + h;
         const float m = p.stats[hh * 2], l = p.stats[hh * 2 + 1];
-        pr = bf16_round(expf(bf16_to_float(p.s[hh * p.cap + c0 + t]) - m) / l);
+        q = bf16_round(expf(bf16_to_float(p.s[hh * p.cap + c0 + t]) - m) / l);
       }
-      ph[2 * h] = bf16_bits(pr);
+      pr[h][t] = bf16_bits(q);
     }
   }
   __syncthreads();
-  // 2. lane (channel group dg, token group tg): channels 8dg + [0, 8), token
-  //    pairs m = 32*wave + 4i + tg (tokens 2m, 2m+1), i = 0..7
-  const int dg = lane & 15, tg = lane >> 4;
-  float acc[kAttnR][8];
+  // 2. out[h][d] over the wave's 64 tokens as 8 tiles of v_mfma_f32_16x16x32_bf16:
+  //    tile T has A[row r][k] = v[token 32s + k][channel 8r + T] (lane (r16, kg)
+  //    dequantises byte T of its 8 tokens) and B[k][col h] = prob[h][token 32s + k]
+  f32x4 acc[8];
 #pragma unroll
-  for (int h = 0; h < kAttnR; ++h)
+  for (int T = 0; T < 8; ++T) acc[T] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < 8; ++k) acc[h][k] = 0.f;
-  const int64_t rowbytes = (int64_t)p.kvh * kAttnD;
-#pragma unroll 2
-  for (int i = 0; i < 8; ++i) {
-    const int m = 32 * wave + 4 * i + tg;
-    if (2 * m >= nv) break;
-    uint32_t w[2][2];
-    float sc[2];
+  for (int st = 0; st < 2; ++st) {
+    u32x4 bq = {0u, 0u, 0u, 0u};
+    if (r16 < kAttnR) bq = *reinterpret_cast<const u32x4*>(&pr[r16][64 * wave + 32 * st + 8 * kg]);
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int t = c0 + 2 * m + e;
-      const int64_t row = 2 * m + e < nv ? attn_row(p, b, t) : -1;
-      w[e][0] = w[e][1] = 0u;
-      sc[e] = 0.f;
-      if (row >= 0) {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(p.vc + row * rowbytes + kh * kAttnD + 8 * dg);
-        w[e][0] = v[0];
-        w[e][1] = v[1];
-        sc[e] = p.vs[row * p.kvh + kh];
-      }
-    }
-    // BF16 pairs (token 2m, token 2m+1) of channel k
-    uint32_t vp[8];
+    for (int T = 0; T < 8; ++T) {
+      auto val = [&](int j) {
+        const uint32_t w = T < 4 ? wv[st][j][0] : wv[st][j][1];
+        return (float)(int8_t)(w >> (8 * (T & 3))) * sv[st][j];
+      };
+      u32x4 a;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int sh = 8 * (k & 3);
-      const float a = (float)(int8_t)(w[0][k >> 2] >> sh) * sc[0];
-      const float c = (float)(int8_t)(w[1][k >> 2] >> sh) * sc[1];
-      vp[k] = pack_bf16x2(a, c);
-    }
-    const u32x4 pa = *reinterpret_cast<const u32x4*>(&pp[m][0]);
-    const u32x4 pb = *reinterpret_cast<const u32x4*>(&pp[m][4]);
-#pragma unroll
-    for (int h = 0; h < kAttnR; ++h) {
-      const uint32_t ph = h < 4 ? pa[h] : pb[h - 4];
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        acc[h][k] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, vp[k]),
-                                                     __builtin_bit_cast(bf16x2, ph), acc[h][k], false);
+      for (int q = 0; q < 4; ++q) a[q] = pack_bf16x2(val(2 * q), val(2 * q + 1));
+      acc[T] = mfma16(a, bq, acc[T]);
     }
   }
-  // 3. sum the four token groups of each wave, then the four waves, in order
+  // 3. lane (h = r16, kg) holds out[h][8*(4kg + v) + T] = acc[T][v]; the four
+  //    waves' sums are added in wave order
+  if (r16 < kAttnR) {
 #pragma unroll
-  for (int h = 0; h < kAttnR; ++h)
+    for (int v = 0; v < 4; ++v)
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      float v = acc[h][k];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      acc[h][k] = v;
-    }
-  if (tg == 0) {
-#pragma unroll
-    for (int h = 0; h < kAttnR; ++h)
-#pragma unroll
-      for (int k = 0; k < 8; ++k) red[wave][h][8 * dg + k] = acc[h][k];
+      for (int T = 0; T < 8; ++T) red[wave][r16][32 * kg + 8 * v + T] = acc[T][v];
   }
   __syncthreads();
   float* dst = p.part + (((int64_t)b * p.kvh + kh) * p.nchunks + chunk) * kAttnR * kAttnD;
@@ -254,14 +267,33 @@ __global__ void __launch_bounds__(256) attn_pv_kernel(AttnParams p) {
   }
 }
 
-__global__ void __launch_bounds__(kAttnD) attn_combine_kernel(AttnParams p) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+// Eight thread groups per output channel each add a contiguous eighth of the
+// chunks in chunk order; the eight group sums are then added in group order.
+__global__ void __launch_bounds__(8 * kAttnD) attn_combine_kernel(AttnParams p) {
+  __shared__ float red[8][kAttnD];
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x % kAttnD, grp = threadIdx.x / kAttnD;
   const int kh = h / p.r, hr = h % p.r;
   const int nc = (attn_len(p, b) + kAttnChunk - 1) / kAttnChunk;
+  const int per = (nc + 7) / 8, cb = grp * per, ce = cb + per < nc ? cb + per : nc;
   const float* src = p.part + (((int64_t)b * p.kvh + kh) * p.nchunks) * kAttnR * kAttnD + hr * kAttnD + d;
   float v = 0.f;
-  for (int c = 0; c < nc; ++c) v += src[(int64_t)c * kAttnR * kAttnD];
-  p.out[((int64_t)b * p.hq + h) * kAttnD + d] = bf16_bits(v);
+  for (int c0 = cb; c0 < ce; c0 += 8) {
+    float x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = c0 + u < ce ? src[(int64_t)(c0 + u) * kAttnR * kAttnD] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (c0 + u < ce) v += x[u];
+  }
+  red[grp][d] = v;
+  __syncthreads();
+  if (grp == 0) {
+    float t = red[0][d];
+#pragma unroll
+    for (int g = 1; g < 8; ++g)
+      if (g * per < nc) t += red[g][d];
+    p.out[((int64_t)b * p.hq + h) * kAttnD + d] = bf16_bits(t);
+  }
 }
 
 struct AttnLayout {
@@ -337,8 +369,8 @@ extern "C" int q6moe_kv_decode_attention(const q6moe_attn_args* a, void* stream)
   hipStream_t s = (hipStream_t)stream;
   const dim3 chunks((unsigned)p.nchunks, (unsigned)p.kvh, (unsigned)a->batch);
   hipLaunchKernelGGL(attn_scores_kernel, chunks, dim3(256), 0, s, p);
-  hipLaunchKernelGGL(attn_stats_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(attn_stats_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(kStatsThreads), 0, s, p);
   hipLaunchKernelGGL(attn_pv_kernel, chunks, dim3(256), 0, s, p);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(kAttnD), 0, s, p);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(8 * kAttnD), 0, s, p);
   return check_launch("decode_attention kernels");
 }
