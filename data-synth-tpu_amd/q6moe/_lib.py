@@ -143,6 +143,7 @@ SIGNATURES = {
     "q6moe_kv_quantize": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _vp]),
     "q6moe_kv_write": (_int, [ctypes.POINTER(KvWriteArgs), _vp]),
     "q6moe_attn_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
+    "q6moe_route_topk": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "q6moe_kv_decode_attention": (_int, [ctypes.POINTER(AttnArgs), _vp]),
 }
 

@@ -151,6 +151,17 @@ typedef struct q6moe_moe_args {
 
 #define Q6MOE_MOE_EVENTS 5
 
+/*
+ * Router (routes_and_shared's routing, kaggle/qwen38_tpu/math.py:277-281): FP32
+ * softmax of logits [B, E] (E <= 256), top_k (k <= 32; larger probability
+ * first, lower expert id on ties), weights divided by their FP32 sum in
+ * selection order, rows with active[b] == 0 zeroed (active NULL: all active),
+ * RNE to BF16. Writes ids int32 [B, k] and weights BF16 [B, k]: the ids and
+ * weights q6moe_moe_forward takes.
+ */
+int q6moe_route_topk(const float* logits, int64_t tokens, int64_t experts, int64_t top_k,
+                     const uint8_t* active, int32_t* ids, uint16_t* weights, void* stream);
+
 size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_t experts, int64_t hidden,
                                 int64_t intermediate, int64_t shared_intermediate);
 
