@@ -379,14 +379,26 @@ __global__ void __launch_bounds__(512)
     // All RPW units of a K block are loaded before the first is decoded (row
     // groups past the matrix are clamped to its last one and not used); with
     // four token groups, Q8_0 units are loaded one at a time (registers).
+    // With one token group, two K blocks per pass, all their units in flight
+    // together (the second block clamped to the first when it does not exist).
     constexpr int kPre = FMT == FMT_Q8 && NT > 1 ? 1 : RPW;
-    for (int kb = wave; kb < down.kb; kb += kw) {
-      Unit<FMT> ud[kPre];
+    constexpr int kBat = NT == 1 ? 2 : 1;
+    for (int kb0 = wave; kb0 < down.kb; kb0 += kBat * kw) {
+      Unit<FMT> udb[kBat][kPre];
 #pragma unroll
-      for (int r = 0; r < kPre; ++r) {
-        const int rg = rg0 + r < (hidden + 15) / 16 ? rg0 + r : (hidden + 15) / 16 - 1;
-        ud[r].load(down, si.expert, rg, kb, lane);
+      for (int bt = 0; bt < kBat; ++bt) {
+        const int kbb = kb0 + bt * kw < down.kb ? kb0 + bt * kw : kb0;
+#pragma unroll
+        for (int r = 0; r < kPre; ++r) {
+          const int rg = rg0 + r < (hidden + 15) / 16 ? rg0 + r : (hidden + 15) / 16 - 1;
+          udb[bt][r].load(down, si.expert, rg, kbb, lane);
+        }
       }
+#pragma unroll
+      for (int bt = 0; bt < kBat; ++bt) {
+      if (bt > 0 && kb0 + bt * kw >= down.kb) break;
+      const int kb = kb0 + bt * kw;
+      Unit<FMT>(&ud)[kPre] = udb[bt];
       u32x4 xf[NT][8];
 #pragma unroll
       for (int t = 0; t < NT; ++t)
@@ -408,6 +420,7 @@ __global__ void __launch_bounds__(512)
         for (int f = 0; f < 8; ++f)
 #pragma unroll
           for (int t = 0; t < NT; ++t) acc[r][t] = mfma16(a[f], xf[t][f], acc[r][t]);
+      }
       }
     }
 #pragma unroll
@@ -559,12 +572,12 @@ static void launch_phases(const Proj& g, const Proj& u, const Proj& d, const Tok
   const int kw1 = g.kb < 8 ? g.kb : 8;
   const int kw2 = d.kb < 8 ? d.kb : 8;
   const unsigned rb1 = (unsigned)cdiv(I, 16), rb2 = (unsigned)cdiv(H, 16 * 2);
-  if (max_tokens <= 16) {
+  if (max_tokens <= 16) {  // one token group: one row group per down workgroup (twice the workgroups)
     hipLaunchKernelGGL((moe_gate_up_kernel<FG, 1, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
                        H, act, I, kw1);
     mark(2);
-    hipLaunchKernelGGL((moe_down_kernel<FD, 1, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
-                       H, kw2);
+    hipLaunchKernelGGL((moe_down_kernel<FD, 1, 1>), dim3(grid_x, (unsigned)cdiv(H, 16)), dim3(64 * kw2), 0, s, d,
+                       src, act, I, y, H, kw2);
   } else {
     hipLaunchKernelGGL((moe_gate_up_kernel<FG, 4, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
                        H, act, I, kw1);
