@@ -94,18 +94,27 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnParams p) {
   const float* sw = p.ks + (base < 0 ? 0 : base) * p.kvh + kh;
   const uint32_t lane_off = (uint32_t)col * (uint32_t)rowbytes + 32u * g;
   const uint32_t rb_off = 16u * (uint32_t)rowbytes;
-#pragma unroll
-  for (int rb = 0; rb < 4; ++rb) {
-    // A operand: token t (row col of the block), channels 32g + [0, 32)
+  // A operand of row block rb: token t0 + 16rb + col, channels 32g + [0, 32);
+  // the next block's loads are issued before this block is multiplied
+  u32x4 cw[4][2];
+  float scw[4];
+  auto load_rb = [&](int rb) {
     const int t = t0 + 16 * rb + col;
-    u32x4 c0 = {0u, 0u, 0u, 0u}, c1 = {0u, 0u, 0u, 0u};
-    float sc = 0.f;
+    cw[rb][0] = cw[rb][1] = u32x4{0u, 0u, 0u, 0u};
+    scw[rb] = 0.f;
     if (t < n && base >= 0) {
       const int8_t* src = kw + lane_off + rb * rb_off;
-      c0 = *reinterpret_cast<const u32x4*>(src);
-      c1 = *reinterpret_cast<const u32x4*>(src + 16);
-      sc = sw[(16 * rb + col) * p.kvh];
+      cw[rb][0] = *reinterpret_cast<const u32x4*>(src);
+      cw[rb][1] = *reinterpret_cast<const u32x4*>(src + 16);
+      scw[rb] = sw[(16 * rb + col) * p.kvh];
     }
+  };
+  load_rb(0);
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    if (rb + 1 < 4) load_rb(rb + 1);
+    const u32x4 c0 = cw[rb][0], c1 = cw[rb][1];
+    const float sc = scw[rb];
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
