@@ -62,7 +62,34 @@ __global__ void __launch_bounds__(kChunk)
   stage_chunk(s_ids, ids + e0, nb * K, [](int v) { return v; });
   stage_chunk(s_w, wts + e0, nb * K, [](uint16_t v) { return bf16_to_float(v); });
   __syncthreads();
-  if (tid < nb) {
+  if (tid < nb && K <= 8) {
+    // top_k <= 8: the token's entries in registers, every loop unrolled (the
+    // same comparisons and the same summation order as below)
+    int id[8];
+    float w[8], mg[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      id[kk] = kk < K ? s_ids[tid * K + kk] : -1;
+      w[kk] = kk < K ? s_w[tid * K + kk] : 0.f;
+    }
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const int e = id[kk];
+      bool first = kk < K && e >= 0 && e < E;
+#pragma unroll
+      for (int k2 = 0; k2 < kk; ++k2) first = first && id[k2] != e;
+      float sum = 0.f;
+#pragma unroll
+      for (int k2 = kk; k2 < 8; ++k2)
+        if (k2 < K && id[k2] == e) sum += w[k2];
+      const float m = first ? bf16_round(sum) : 0.f;
+      if (first && is_route(m)) atomicAdd(&cnt[e], 1);
+      mg[kk] = is_route(m) ? m : 0.f;
+    }
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      if (kk < K) s_w[tid * K + kk] = mg[kk];
+  } else if (tid < nb) {
     const int* id = s_ids + tid * K;
     float* w = s_w + tid * K;
     // The sum for entry kk reads weights kk..K-1 only, so entry kk's merged
@@ -175,7 +202,40 @@ __global__ void __launch_bounds__(kChunk)
     for (int kk = 0; kk < K; ++kk)
       if (is_route(s_r[tid * K + kk])) atomicOr(&bits[s_ids[tid * K + kk]][tid >> 5], 1u << (tid & 31));
   __syncthreads();
-  if (tid < nb) {
+  if (tid < nb && K <= 8) {
+    // top_k <= 8: the token's entries and its position list in registers; the
+    // list is sorted by an odd-even transposition network (non-routes last)
+    int pos[8];
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      pos[kk] = 0x7fffffff;
+      const float r = kk < K ? s_r[tid * K + kk] : 0.f;
+      if (kk < K && is_route(r)) {
+        const int e = s_ids[tid * K + kk];
+        int rank = __popc(bits[e][tid >> 5] & ((1u << (tid & 31)) - 1u));
+#pragma unroll
+        for (int w = 0; w < kChunkWords - 1; ++w)
+          if (w < (tid >> 5)) rank += __popc(bits[e][w]);
+        const int p = s_pos[e] + rank;
+        ws.route_tok[p] = b0 + tid;
+        ws.route_w[p] = r;
+        pos[kk] = p;
+      }
+    }
+#pragma unroll
+    for (int pass = 0; pass < 8; ++pass)
+#pragma unroll
+      for (int i = pass & 1; i + 1 < 8; i += 2)
+        if (pos[i] > pos[i + 1]) {
+          const int t = pos[i];
+          pos[i] = pos[i + 1];
+          pos[i + 1] = t;
+        }
+    int* tp = s_tp + tid * K;
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (q < K) tp[q] = pos[q] == 0x7fffffff ? -1 : pos[q];
+  } else if (tid < nb) {
     int* tp = s_tp + tid * K;
     int m = 0;
     for (int kk = 0; kk < K; ++kk) {
