@@ -83,35 +83,31 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// The weights of one unit for one K half, in the registers of the lane that
-// decodes them (row j = lane % 16, k-group jA = lane / 16): code words 2h and
-// 2h+1 of each of the three code chunks (bit-planar layout), the lane's
-// sub-scale word and the row's FP16 scale.
-struct HalfRegs {
-  u32x2 c0, c1, c2;
+// The weights of one unit (a whole K block), in the registers of the lane
+// that decodes them (row j = lane % 16, k-group jA = lane / 16): its four code
+// words of each of the three code chunks (bit-planar layout), its sub-scale
+// word and the row's FP16 scale. Both K halves decode from one load.
+struct BlockRegs {
+  u32x4 c0, c1, c2;
   uint32_t sc, d;
 };
 
-__device__ __forceinline__ void load_half(const uint8_t* units, int kbs, int rg, int kb, int h, int lane,
-                                          HalfRegs& r) {
-  const uint8_t* u = units + ((int64_t)rg * kbs + kb) * kQ6Unit + 16 * lane + 8 * h;
-  // Plain (cached) loads: a K half reads 8 of every 16 bytes of a code line
-  // and the next K half the other 8, so the line must stay in L2 between the
-  // two steps (a non-temporal hint here doubles the L2-to-fabric traffic).
-  r.c0 = *reinterpret_cast<const u32x2*>(u);
-  r.c1 = *reinterpret_cast<const u32x2*>(u + 1024);
-  r.c2 = *reinterpret_cast<const u32x2*>(u + 2048);
+__device__ __forceinline__ void load_block(const uint8_t* units, int kbs, int rg, int kb, int lane, BlockRegs& r) {
   const uint8_t* v = units + ((int64_t)rg * kbs + kb) * kQ6Unit;
+  r.c0 = *reinterpret_cast<const u32x4*>(v + 16 * lane);
+  r.c1 = *reinterpret_cast<const u32x4*>(v + 1024 + 16 * lane);
+  r.c2 = *reinterpret_cast<const u32x4*>(v + 2048 + 16 * lane);
   r.sc = *reinterpret_cast<const uint32_t*>(v + 3072 + 4 * lane);
   r.d = *reinterpret_cast<const uint16_t*>(v + 3328 + 2 * (lane & 15));
 }
 
 // The 4 A fragments of K half h (f = 4h..4h+3) of a unit.
-__device__ __forceinline__ void decode_half(const HalfRegs& w, int h, int lane, u32x4 a[4]) {
+__device__ __forceinline__ void decode_half(const BlockRegs& w, int h, int lane, u32x4 a[4]) {
   const float d = half_bits_to_float(w.d);
 #pragma unroll
   for (int gg = 0; gg < 2; ++gg)
-    q6p_group(w.c0[gg], w.c1[gg], w.c2[gg], q6p_ds(d, w.sc, 2 * h + gg), a[2 * gg], a[2 * gg + 1]);
+    q6p_group(w.c0[2 * h + gg], w.c1[2 * h + gg], w.c2[2 * h + gg], q6p_ds(d, w.sc, 2 * h + gg), a[2 * gg],
+              a[2 * gg + 1]);
 }
 
 // LDS byte offset of token-tile granule (token t, 8-column granule c) of a K half.
@@ -180,14 +176,19 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     units[u] = p.data + expert * p.dstride;
     rgs[u] = rg_of(u);
   }
-  HalfRegs wr[kXStages][kUnits];
-  // part p < kUnits: unit p's weights; the remaining parts split the token DMA
+  // One register set per unit: a K block's weights arrive during the step
+  // before its first half (once the previous block's second half is decoded)
+  // and serve both of its halves.
+  static_assert(kXStages == 2, "a K block's weights serve the steps of slots 0 and 1");
+  BlockRegs wr[kUnits];
+  // part p < kUnits: unit p's weights (first-half steps only); the remaining
+  // parts split the token DMA
   auto issue_part = [&](int s, auto slot_c, auto part_c) {
     constexpr int slot = decltype(slot_c)::value;
     constexpr int part = decltype(part_c)::value;
     const int kb = s >> 1, h = s & 1;
     if constexpr (part < kUnits) {
-      load_half(units[part], kbs, rgs[part], kb, h, lane, wr[slot][part]);
+      if constexpr (slot == 0) load_block(units[part], kbs, rgs[part], kb, lane, wr[part]);  // s even: h == 0
     } else {
       constexpr int np = 4 - kUnits, per = kXDma / np, i0 = (part - kUnits) * per;
       uint8_t* xs = smem + slot * kHalfBytes + wave * kXDma * 1024;
@@ -212,7 +213,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     // issued, for everything in flight before decoding them.
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
-      HalfRegs& w = wr[slot][u];
+      BlockRegs& w = wr[u];
       asm volatile("" : "+v"(w.c0), "+v"(w.c1), "+v"(w.c2), "+v"(w.sc), "+v"(w.d));
     }
     const bool more = s + kAhead < S;
@@ -220,7 +221,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     const uint8_t* xs = smem + slot * kHalfBytes;
     u32x4 a[kUnits][4];
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) decode_half(wr[slot][u], h, lane, a[u]);
+    for (int u = 0; u < kUnits; ++u) decode_half(wr[u], slot, lane, a[u]);  // slot == s % 2 == h
     static_for<0, 4>([&](auto fc) {
       constexpr int f = decltype(fc)::value;
       const int c = xfrag_gran(f, jA);
