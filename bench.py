@@ -45,7 +45,7 @@ Q6_PROJ_BYTES = 768 * 8 * 210  # one 768x2048 (or 2048x768) Q6_K projection: 210
 # WRITE_SIZE over this script, scaled by a 512 MiB device copy in the same run
 # (profiles/moe_q6k_e128_top8_h2048_i768__hbm_bytes.txt); they change only
 # when the kernels do and are re-measured with them.
-TRAFFIC_BYTES = {"moe_dec_gate_up_kernel": 129_900_000, "moe_pf_gate_up_kernel": 639_130_000}
+TRAFFIC_BYTES = {"moe_dec_gate_up_kernel": 129_900_000, "moe_pf_gate_up_kernel": 644_420_000}
 
 
 def log(*a):
