@@ -12,8 +12,8 @@
 //        (experts.py:108). The combine kernel in moe.hip sums f32(y)*f32(r).
 //
 // Each wave owns 2 units (16 weight rows x one 256-wide K block) per K block,
-// loads their bytes into registers one K half ahead and decodes them straight
-// into MFMA A operands; decoded weights never leave registers. The 128 token
+// loads a unit's bytes into registers in the step before the block's first K
+// half, and decodes each half straight into MFMA A operands; decoded weights never leave registers. The 128 token
 // rows of the current K half sit in LDS (double-buffered, XOR-swizzled so the
 // 16 token columns of an MFMA read hit distinct banks), filled by direct
 // global->LDS DMA, and every wave multiplies them against its own rows. The
@@ -38,8 +38,12 @@ constexpr int kHalfBytes = kM * 128 * 2;  // one K half of the token tile (32 KB
 constexpr int kXDma = kHalfBytes / 1024 / kWaves;  // token DMA instructions per wave per half
 constexpr int kAhead = 1;          // K halves in flight beyond the one being multiplied
 constexpr int kXStages = kAhead + 1;
-constexpr int kWLoads = 5;         // weight loads per unit per K half (3 code chunks, sub-scales, d)
-constexpr int kStepOps = kUnits * kWLoads + kXDma;  // vector-memory instructions per K half per wave
+constexpr int kWLoads = 5;         // weight loads per unit per K block (3 code chunks, sub-scales, d)
+// Vector-memory instructions per wave of the step before a first half (the
+// most of any step). The waits below need exact counts only for steps still in
+// flight behind the one awaited, and with one step ahead there are none.
+constexpr int kStepOps = kUnits * kWLoads + kXDma;
+static_assert(kAhead == 1, "per-step wait counts assume one step in flight");
 constexpr int kLds = kXStages * kHalfBytes;
 
 static_assert(kLds <= 160 * 1024, "LDS budget");
