@@ -191,10 +191,11 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     constexpr int slot = decltype(slot_c)::value;
     constexpr int part = decltype(part_c)::value;
     const int kb = s >> 1, h = s & 1;
-    if constexpr (part < kUnits) {
-      if constexpr (slot == 0) load_block(units[part], kbs, rgs[part], kb, lane, wr[part]);  // s even: h == 0
-    } else {
-      constexpr int np = 4 - kUnits, per = kXDma / np, i0 = (part - kUnits) * per;
+    if constexpr (slot == 0 && part < kUnits) {
+      load_block(units[part], kbs, rgs[part], kb, lane, wr[part]);  // s even: h == 0
+    } else if constexpr (slot == 0 || part < 4 - kUnits) {
+      // second-half steps load no weights: their token DMA goes out in the first parts
+      constexpr int np = 4 - kUnits, per = kXDma / np, i0 = (slot == 0 ? part - kUnits : part) * per;
       uint8_t* xs = smem + slot * kHalfBytes + wave * kXDma * 1024;
 #pragma unroll
       for (int i = i0; i < i0 + per; ++i) dma16(xb + (int64_t)(kb * kQK + h * 128) * 2, xoff[i], xs + i * 1024);
