@@ -160,7 +160,8 @@ __device__ __forceinline__ void tile_info(const MoeWs& ws, int tile, Tile& T) {
 // s % kXStages, kAhead steps before it is multiplied; one workgroup barrier
 // per step makes every wave's share visible and frees the stage read in the
 // step before. The next step's loads go out in four parts, one after each
-// fragment's MFMAs (unit 0, unit 1, then the two halves of the token DMA), so
+// fragment's MFMAs (unit 0, unit 1, then the two halves of the token DMA; for
+// a second-half step, which needs no weights, the DMA halves come first), so
 // that the four waves of a workgroup do not all queue their vector-memory
 // instructions at once right after the barrier.
 template <typename RowFn>
@@ -185,8 +186,9 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
   // and serve both of its halves.
   static_assert(kXStages == 2, "a K block's weights serve the steps of slots 0 and 1");
   BlockRegs wr[kUnits];
-  // part p < kUnits: unit p's weights (first-half steps only); the remaining
-  // parts split the token DMA
+  // For a first-half step, part p < kUnits loads unit p's weights and the
+  // remaining parts split the token DMA; a second-half step only DMAs, in the
+  // first parts
   auto issue_part = [&](int s, auto slot_c, auto part_c) {
     constexpr int slot = decltype(slot_c)::value;
     constexpr int part = decltype(part_c)::value;
