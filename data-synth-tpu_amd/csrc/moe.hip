@@ -542,12 +542,39 @@ __global__ void __launch_bounds__(256)
   *reinterpret_cast<u32x4*>(out + (int64_t)b * hidden + h) = o;
 }
 
+// Shared-expert gate (kaggle/qwen38_tpu/math.py:283 with linear and sigmoid of
+// math.py:10-24): gate[b] = RNE(sigmoid(RNE(x[b] . w))), x BF16 [B, H], w BF16
+// [H], FP32 accumulation. One wave per token; lane l sums the products of
+// columns 8(l + 64i) .. +7 in column order, then the 64 lane sums meet in a
+// fixed butterfly, so the result does not depend on scheduling.
+__global__ void __launch_bounds__(64)
+    moe_shared_gate_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int hidden,
+                           uint16_t* __restrict__ gate) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  const uint16_t* xr = x + (int64_t)b * hidden;
+  float acc = 0.f;
+  for (int h = 8 * lane; h < hidden; h += 512) {
+    const u32x4 xv = *reinterpret_cast<const u32x4*>(xr + h);
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(w + h);
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      acc += bf16_to_float((uint16_t)(xv[q >> 1] >> (16 * (q & 1)))) *
+             bf16_to_float((uint16_t)(wv[q >> 1] >> (16 * (q & 1))));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+  if (lane == 0) {
+    const float g = bf16_round(acc);
+    gate[b] = bf16_bits(sigmoid_acc(g));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 struct WsLayout {
   size_t hdr, active, act_off, tile, ent_r, route_tok, route_w, tok_pos, act,
-      y, sh_act, sh_y, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, chunk_cnt, total;
+      y, sh_act, sh_y, sh_gate, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, chunk_cnt, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -574,6 +601,7 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
   L.y = take(2 * n * H);
   L.sh_act = take(Is > 0 ? 2 * B * Is : 0);
   L.sh_y = take(Is > 0 ? 2 * B * H : 0);
+  L.sh_gate = take(Is > 0 ? 2 * B : 0);
   L.slot_e = take(4 * E);
   L.slot_t0 = take(4 * E);
   L.slot_cnt = take(4 * E);
@@ -745,6 +773,20 @@ __global__ void __launch_bounds__(256) moe_pack_kernel(const uint8_t* __restrict
   *reinterpret_cast<uint32_t*>(dst + e * dst_stride + o) = v;
 }
 
+// Unit-decode probe of the generic kernels' register path (Unit::load +
+// Unit::decode). grid (units per expert, experts).
+template <int FMT>
+__global__ void __launch_bounds__(64) moe_unit_unpack_kernel(Proj p, uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x;
+  const int e = blockIdx.y, rg = blockIdx.x / p.kb, kb = blockIdx.x - rg * p.kb;
+  Unit<FMT> u;
+  u.load(p, e, rg, kb, lane);
+  u32x4 a[8];
+  u.decode(a, lane);
+  store_unit_frags(a, out + (int64_t)e * p.rows * p.k, p, rg, kb, lane,
+                   [](int f, int jA) { return Unit<FMT>::xoff(f, jA); });
+}
+
 }  // namespace q6moe
 
 using namespace q6moe;
@@ -781,6 +823,39 @@ extern "C" int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, in
   return check_launch("moe_pack_kernel");
 }
 
+extern "C" int q6moe_moe_unpack(const uint8_t* table, int qtype, int64_t experts, int64_t rows, int64_t width,
+                                int64_t stride, int path, uint16_t* out, void* stream) {
+  Q6MOE_REQUIRE(table && out, "moe_unpack: null pointer");
+  Q6MOE_REQUIRE(expert_qtype(qtype), "moe_unpack: qtype must be Q6_K, Q4_K or Q8_0");
+  Q6MOE_REQUIRE(experts >= 1 && experts <= 65535 && rows >= 1 && width >= 1 && rows <= (1 << 24) &&
+                    width <= (1 << 24) && (qtype != Q6MOE_Q8_0 || width % 32 == 0),
+                "moe_unpack: bad shape");
+  Q6MOE_REQUIRE(path >= 0 && path <= 2, "moe_unpack: path must be 0 (generic), 1 (decode) or 2 (prefill)");
+  Q6MOE_REQUIRE(path != 2 || qtype == Q6MOE_Q6_K, "moe_unpack: the prefill path decodes Q6_K only");
+  const int64_t need = unit_table_bytes(qtype, rows, width);
+  Q6MOE_REQUIRE(aligned(table, 16) && (experts == 1 || (stride >= need && stride % 16 == 0)),
+                "moe_unpack: table must be 16-byte aligned with a stride covering one expert");
+  const int64_t units = cdiv(rows, 16) * cdiv(width, kQK);
+  Q6MOE_REQUIRE(units <= 0x7fffffff, "moe_unpack: too many units");
+  q6moe_table t{qtype, table, experts == 1 ? need : stride, nullptr, 0};
+  const Proj p = make_proj(t, (int)rows, (int)width);
+  hipStream_t s = (hipStream_t)stream;
+  const int fmt = fmt_of(qtype);
+  const dim3 grid((unsigned)units, (unsigned)experts);
+  if (path == 1) {
+    launch_dec_unpack(fmt, p, (int)experts, out, s);
+  } else if (path == 2) {
+    launch_pf_unpack(p, (int)experts, out, s);
+  } else if (fmt == FMT_Q6) {
+    hipLaunchKernelGGL(moe_unit_unpack_kernel<FMT_Q6>, grid, dim3(64), 0, s, p, out);
+  } else if (fmt == FMT_Q4K) {
+    hipLaunchKernelGGL(moe_unit_unpack_kernel<FMT_Q4K>, grid, dim3(64), 0, s, p, out);
+  } else {
+    hipLaunchKernelGGL(moe_unit_unpack_kernel<FMT_Q8>, grid, dim3(64), 0, s, p, out);
+  }
+  return check_launch("moe_unpack");
+}
+
 extern "C" size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_t experts, int64_t hidden,
                                            int64_t intermediate, int64_t shared_intermediate) {
   if (tokens < 1 || top_k < 1 || experts < 1 || hidden < 1 || intermediate < 1 || shared_intermediate < 0)
@@ -813,6 +888,8 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
     Q6MOE_REQUIRE(a->shared_gate.qtype == a->gate.qtype && a->shared_up.qtype == a->gate.qtype &&
                       a->shared_down.qtype == a->down.qtype,
                   "moe_forward: the shared expert must use the routed experts' qtype");
+    Q6MOE_REQUIRE(!(a->shared_router && a->shared_scale), "moe_forward: shared_router and shared_scale exclude each other");
+    Q6MOE_REQUIRE(!a->shared_router || aligned(a->shared_router, 16), "moe_forward: shared_router needs 16-byte alignment");
     if ((rc = validate_table(a->shared_gate, "shared_gate", Is, H, 1)) ||
         (rc = validate_table(a->shared_up, "shared_up", Is, H, 1)) ||
         (rc = validate_table(a->shared_down, "shared_down", H, Is, 1)))
@@ -839,6 +916,14 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   ws.sh_y = Is ? reinterpret_cast<uint16_t*>(w + L.sh_y) : nullptr;
 
   hipStream_t s = (hipStream_t)stream;
+  // Per-token shared-expert gate: the caller's, or computed here from the router.
+  const uint16_t* sh_scale = a->shared_scale;
+  if (Is && a->shared_router) {
+    uint16_t* g = reinterpret_cast<uint16_t*>(w + L.sh_gate);
+    hipLaunchKernelGGL(moe_shared_gate_kernel, dim3((unsigned)B), dim3(64), 0, s, a->x, a->shared_router, (int)H, g);
+    if ((rc = check_launch("moe_shared_gate_kernel"))) return rc;
+    sh_scale = g;
+  }
   auto mark = [&](int i) {
     if (a->events && a->events[i]) hipEventRecord((hipEvent_t)a->events[i], s);
   };
@@ -889,7 +974,7 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
     D.act = ws.act;
     D.contrib = reinterpret_cast<float*>(w + L.contrib);
     D.sh_y = ws.sh_y;
-    D.sh_scale = a->shared_scale;
+    D.sh_scale = sh_scale;
     D.out = a->out;
     D.after_gate_up = a->events ? a->events[2] : nullptr;
     D.after_down = a->events ? a->events[3] : nullptr;
@@ -955,7 +1040,7 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   }
   mark(3);
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)B, (unsigned)cdiv(H, 256 * 8)), dim3(256), 0, s,
-                     ws.tok_pos, ws.route_w, ws.y, (int)K, (int)H, ws.sh_y, a->shared_scale, a->out);
+                     ws.tok_pos, ws.route_w, ws.y, (int)K, (int)H, ws.sh_y, sh_scale, a->out);
   rc = check_launch("moe_combine_kernel");
   mark(4);
   return rc;

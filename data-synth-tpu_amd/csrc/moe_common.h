@@ -123,6 +123,11 @@ struct DecArgs {
 bool dec_supported(int64_t B, int64_t K, int64_t E);
 int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s);  // fmt_dn: fmt_gu or FMT_Q8
 
+// Unit-decode probes (q6moe_moe_unpack): the decode kernels' LDS-staged path
+// and the prefill kernels' whole-block register path, for the bit-exact tests.
+int launch_dec_unpack(int fmt, const Proj& p, int experts, uint16_t* out, hipStream_t s);
+int launch_pf_unpack(const Proj& p, int experts, uint16_t* out, hipStream_t s);
+
 // Prefill grouped GEMM (Q6_K, hidden and intermediate multiples of 256).
 bool pf_supported(int fmt, int64_t H, int64_t I);
 int64_t pf_tile_routes();
@@ -226,5 +231,22 @@ struct Unit<FMT_Q8> {
   __device__ __forceinline__ void decode(u32x4 a[8], int) const { q8_decode(c, d, a); }
   static __device__ __forceinline__ int xoff(int f, int jA) { return q6_xfrag_offset(f, jA); }
 };
+
+// Stores a lane's 8 decoded A fragments of unit (rg, kb) -- row rg*16 + lane%16,
+// K positions kb*256 + xoff(f) + [0, 8) -- into out [p.rows, p.k] (BF16 bits),
+// skipping positions past the matrix. Used by the unit-decode probes.
+template <typename XOff>
+__device__ __forceinline__ void store_unit_frags(const u32x4 (&a)[8], uint16_t* out, const Proj& p, int rg,
+                                                 int kb, int lane, XOff xoff) {
+  const int row = rg * 16 + (lane & 15);
+  if (row >= p.rows) return;
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    const int c0 = kb * kQK + xoff(f, lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (c0 + i < p.k) out[(int64_t)row * p.k + c0 + i] = (uint16_t)(a[f][i >> 1] >> (16 * (i & 1)));
+  }
+}
 
 }  // namespace q6moe

@@ -766,4 +766,34 @@ int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s) {
   return fmt_dn == FMT_Q8 ? launch_k<FMT_Q4K, FMT_Q8>(A, s) : launch_k<FMT_Q4K, FMT_Q4K>(A, s);
 }
 
+// Unit-decode probe of this path: one wave per unit copies the unit into an
+// LDS ring stage with the kernels' own DMA (WStream::issue) and decodes it with
+// WStream::decode, exactly as the streaming loop does, then stores the BF16
+// weights. grid (units per expert, experts).
+template <int FMT>
+__global__ void __launch_bounds__(64) moe_dec_unpack_kernel(Proj p, uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint8_t st[stage_bytes<FMT>()];
+  const int lane = threadIdx.x;
+  const int e = blockIdx.y, rg = blockIdx.x / p.kb, kb = blockIdx.x - rg * p.kb;
+  const WStream<FMT> ws(p, e, lane);
+  ws.issue(rg, kb, st);
+  wait_vm<0>();
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  u32x4 a[8];
+  WStream<FMT>::decode(st, lane, a);
+  store_unit_frags(a, out + (int64_t)e * p.rows * p.k, p, rg, kb, lane,
+                   [](int f, int jA) { return Unit<FMT>::xoff(f, jA); });
+}
+
+int launch_dec_unpack(int fmt, const Proj& p, int experts, uint16_t* out, hipStream_t s) {
+  const dim3 grid((unsigned)(cdiv(p.rows, 16) * p.kb), (unsigned)experts);
+  if (fmt == FMT_Q6)
+    hipLaunchKernelGGL(moe_dec_unpack_kernel<FMT_Q6>, grid, dim3(64), 0, s, p, out);
+  else if (fmt == FMT_Q4K)
+    hipLaunchKernelGGL(moe_dec_unpack_kernel<FMT_Q4K>, grid, dim3(64), 0, s, p, out);
+  else
+    hipLaunchKernelGGL(moe_dec_unpack_kernel<FMT_Q8>, grid, dim3(64), 0, s, p, out);
+  return Q6MOE_OK;
+}
+
 }  // namespace q6moe

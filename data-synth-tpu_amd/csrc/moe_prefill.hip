@@ -372,4 +372,24 @@ int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs&
   return Q6MOE_OK;
 }
 
+// Unit-decode probe of this path (Q6_K): load_block + decode_half of both K
+// halves, the prefill kernels' register path. grid (units per expert, experts).
+__global__ void __launch_bounds__(64) moe_pf_unpack_kernel(Proj p, uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x;
+  const int e = blockIdx.y, rg = blockIdx.x / p.kb, kb = blockIdx.x - rg * p.kb;
+  pf::BlockRegs w;
+  pf::load_block(p.data + (int64_t)e * p.dstride, p.kb, rg, kb, lane, w);
+  u32x4 a[8];
+  pf::decode_half(w, 0, lane, a);
+  pf::decode_half(w, 1, lane, a + 4);
+  store_unit_frags(a, out + (int64_t)e * p.rows * p.k, p, rg, kb, lane,
+                   [](int f, int jA) { return q6_xfrag_offset(f, jA); });
+}
+
+int launch_pf_unpack(const Proj& p, int experts, uint16_t* out, hipStream_t s) {
+  hipLaunchKernelGGL(moe_pf_unpack_kernel, dim3((unsigned)(cdiv(p.rows, 16) * p.kb), (unsigned)experts), dim3(64), 0,
+                     s, p, out);
+  return Q6MOE_OK;
+}
+
 }  // namespace q6moe

@@ -58,6 +58,7 @@ class MoeArgs(ctypes.Structure):
         ("workspace_bytes", _size),
         ("mode", _int),
         ("events", ctypes.POINTER(_vp)),
+        ("shared_router", _vp),
     ]
 
 
@@ -137,6 +138,7 @@ SIGNATURES = {
     "q6moe_gguf_decode": (_int, [_vp, _int, _i64, _i64, _vp, _int, _vp]),
     "q6moe_moe_table_bytes": (_size, [_int, _i64, _i64]),
     "q6moe_moe_pack": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp]),
+    "q6moe_moe_unpack": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _int, _vp, _vp]),
     "q6moe_moe_workspace_size": (_size, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "q6moe_moe_forward": (_int, [ctypes.POINTER(MoeArgs), _vp]),
     "q6moe_kv_read": (_int, [ctypes.POINTER(KvArgs), _vp]),

@@ -18,10 +18,12 @@ Expert tables are either ``ExpertTable`` objects from ``pack_experts`` or, as
 in the reference, raw GGUF byte tables ``uint8 [E, bytes_per_expert]`` on the
 GPU; raw tables are repacked on the device to the unit-major layout of the
 kernels (16 rows x one 256-wide K block per contiguous unit, bytes permuted
-only) once and cached per tensor version.
+only) once per live tensor object and version, and the packed copy is freed
+with the raw tensor.
 """
 
 import ctypes
+import weakref
 from dataclasses import dataclass
 from functools import lru_cache
 
@@ -102,25 +104,67 @@ def pack_experts(raw, qtype, rows, width, device=None):
     return ExpertTable(qtype, data, None, rows, width)
 
 
+UNPACK_PATHS = {"generic": 0, "decode": 1, "prefill": 2}
+
+
+def unpack_experts(table, path="generic"):
+    """Decode a unit-major ExpertTable back to BF16 [E, rows, width] with the
+    decoder one family of MoE kernels uses (``path``: "generic", "decode" or
+    "prefill"), through ``q6moe_moe_unpack``: each weight is RNE_bf16 of its
+    GGUF value, as ``dequantize_rows(..., dtype=bfloat16)`` gives it
+    (gguf_quant.py:111-173); Q6_K weights with code 32 come out as +0."""
+    if not isinstance(table, ExpertTable):
+        raise TypeError("unpack_experts takes an ExpertTable")
+    data = table.data
+    out = torch.empty((table.experts, table.rows, table.width), dtype=torch.bfloat16, device=data.device)
+    lib = _lib.load()
+    with torch.cuda.device(data.device):
+        rc = lib.q6moe_moe_unpack(_lib.ptr(data), _lib.QTYPE_CODES[table.qtype], table.experts, table.rows,
+                                  table.width, data.stride(0), UNPACK_PATHS[path], _lib.ptr(out),
+                                  _lib.stream_handle(data.device))
+    _lib.check(rc, "moe_unpack")
+    return out
+
+
 def stacked_table(data, qtype, rows, width):
     """Wrap an already-packed device table [E, q6moe_moe_table_bytes] (from ``q6moe_moe_pack``)."""
     return ExpertTable(qtype, data, None, rows, width)
 
 
 class _PackCache:
-    """Device repack of raw GGUF expert tables, keyed by (pointer, version, shape)."""
+    """Device repack of raw GGUF expert tables, one entry per live tensor.
+
+    An entry belongs to the tensor object it was made from: it is found by
+    that object's identity and removed by a finaliser when the object is
+    freed, so a later table that the caching allocator places at the same
+    address never sees another table's packed bytes. The entry also records
+    the tensor's version counter, pointer, shape and strides, and is rebuilt
+    when any of them changes (an in-place update). Entries live exactly as
+    long as their raw tables, whatever their number: a 48-layer model that
+    passes the same 144 table objects on every call packs each one once.
+    A view made afresh on every call (``table[layer]`` inside the layer loop)
+    is a new object each time and is repacked each time; pass the same
+    object, or pack once at load time with ``pack_experts`` /
+    ``ExpertFFN.prepare``.
+    """
 
     def __init__(self):
         self.entries = {}
 
     def get(self, raw, qtype, rows, width):
-        key = (raw.data_ptr(), raw._version, tuple(raw.shape), qtype, rows, width)
+        key = id(raw)
+        sig = (raw._version, raw.data_ptr(), tuple(raw.shape), tuple(raw.stride()), qtype, rows, width)
         hit = self.entries.get(key)
+        if hit is not None and hit[0] == sig:
+            return hit[1]
+        table = pack_experts(raw, qtype, rows, width, raw.device)
         if hit is None:
-            if len(self.entries) > 16:
-                self.entries.clear()
-            hit = self.entries[key] = pack_experts(raw, qtype, rows, width, raw.device)
-        return hit
+            weakref.finalize(raw, self.entries.pop, key, None)
+        self.entries[key] = (sig, table)
+        return table
+
+    def __len__(self):
+        return len(self.entries)
 
 
 _CACHE = _PackCache()
@@ -140,6 +184,39 @@ def _as_table(t, qtype, rows, width, name):
     return _CACHE.get(t, qtype, rows, width)
 
 
+def _rows_of(t, qtype, width):
+    """Output rows of one expert's projection: an ExpertTable's, or those a raw
+    GGUF table [1, bytes] (or [rows, blocks, bytes]) of row width ``width`` holds."""
+    if isinstance(t, ExpertTable):
+        return t.rows
+    values, size = BLOCK_LAYOUTS[qtype]
+    per_row = -(-width // values) * size
+    n = t.numel() // (t.shape[0] if t.ndim in (2, 4) else 1)
+    if n % per_row:
+        raise ValueError(f"shared expert table does not hold whole {qtype} rows of width {width}")
+    return n // per_row
+
+
+def _check_bf16_out(out, shape, device, name="out"):
+    if out is None:
+        return torch.empty(shape, dtype=torch.bfloat16, device=device)
+    if (not isinstance(out, torch.Tensor) or out.dtype != torch.bfloat16 or tuple(out.shape) != tuple(shape)
+            or out.device != device or not out.is_contiguous()):
+        raise ValueError(f"{name} must be a contiguous BF16 {list(shape)} tensor on {device}")
+    return out
+
+
+def _check_workspace(workspace, need, device):
+    if workspace is None:
+        return torch.empty(need, dtype=torch.uint8, device=device)
+    if (not isinstance(workspace, torch.Tensor) or workspace.dtype != torch.uint8 or workspace.device != device
+            or not workspace.is_contiguous()):
+        raise ValueError(f"workspace must be a contiguous uint8 tensor on {device}")
+    if workspace.numel() < need:
+        raise ValueError(f"workspace holds {workspace.numel()} bytes; this call needs {need}")
+    return workspace
+
+
 class ExpertFFN:
     """Callable returned by ``expert_parallel``."""
 
@@ -154,11 +231,29 @@ class ExpertFFN:
         return int(_lib.load().q6moe_moe_workspace_size(
             tokens, top_k, experts, self.hidden, self.intermediate, shared_intermediate))
 
+    def prepare(self, gate, up, down, device=None):
+        """Pack a layer's raw GGUF tables ([E, bytes_per_expert] uint8, host or
+        GPU) once, at load time: returns the (gate, up, down) ExpertTables that
+        calls take in place of the raw tables, so no call ever repacks."""
+        H, I = self.hidden, self.intermediate
+        return (pack_experts(gate, self.qtype, I, H, device), pack_experts(up, self.qtype, I, H, device),
+                pack_experts(down, self.down_qtype, H, I, device))
+
     def __call__(self, gate, up, down, x, ids, weights, *, shared=None, workspace=None, out=None,
                  events=None):
-        """``events``: optional 5 timing events (torch.cuda.Event, already
-        recorded once so they exist) stamped before routing, after routing,
-        after gate/up, after down and after the combine."""
+        """Routed FFN of x [B, hidden] BF16 with ids/weights [B, top_k].
+
+        ``shared`` adds the always-on shared expert (engine.py:199-203,
+        math.py:282-283): a dict with ``gate``, ``up`` (rows = shared
+        intermediate) and ``down`` tables, and optionally either ``router``
+        (BF16 [hidden]: the output is scaled per token by
+        RNE(sigmoid(RNE(x . router))), computed on the GPU) or ``scale``
+        (BF16 [B], that per-token factor precomputed by the caller).
+        ``out`` (BF16 [B, hidden]) and ``workspace`` (uint8, at least
+        ``workspace_bytes(...)``) are optional preallocated buffers on x's
+        device. ``events``: optional 5 timing events (torch.cuda.Event,
+        already recorded once so they exist) stamped before routing, after
+        routing, after gate/up, after down and after the combine."""
         H, I, q, qd = self.hidden, self.intermediate, self.qtype, self.down_qtype
         gate = _as_table(gate, q, I, H, "gate")
         up = _as_table(up, q, I, H, "up")
@@ -186,24 +281,30 @@ class ExpertFFN:
         Is = 0
         keep = []
         if shared is not None:
-            sg, su, sd = shared["gate"], shared["up"], shared["down"]
-            Is = sg.rows
-            sg = _as_table(sg, q, Is, H, "shared gate")
-            su = _as_table(su, q, Is, H, "shared up")
-            sd = _as_table(sd, qd, H, Is, "shared down")
+            Is = int(shared.get("intermediate") or _rows_of(shared["gate"], q, H))
+            sg = _as_table(shared["gate"], q, Is, H, "shared gate")
+            su = _as_table(shared["up"], q, Is, H, "shared up")
+            sd = _as_table(shared["down"], qd, H, Is, "shared down")
             args.shared_gate, args.shared_up, args.shared_down = sg.c_table(), su.c_table(), sd.c_table()
             args.shared_intermediate = Is
-            scale = shared.get("scale")
+            scale, router = shared.get("scale"), shared.get("router")
+            if scale is not None and router is not None:
+                raise ValueError("give the shared expert either a router or a precomputed scale, not both")
             if scale is not None:
                 scale = scale.to(device=x.device, dtype=torch.bfloat16).contiguous()
                 if scale.numel() != B:
                     raise ValueError("shared scale must hold one BF16 value per token")
                 keep.append(scale)
                 args.shared_scale = scale.data_ptr()
+            if router is not None:
+                if not isinstance(router, torch.Tensor) or router.dtype != torch.bfloat16 or router.numel() != H:
+                    raise ValueError(f"shared router must be a BF16 [{H}] tensor")
+                router = router.to(x.device).contiguous()
+                keep.append(router)
+                args.shared_router = router.data_ptr()
         need = self.workspace_bytes(B, K, experts, Is)
-        if workspace is None or workspace.numel() < need:
-            workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
-        out = torch.empty((B, H), dtype=torch.bfloat16, device=x.device) if out is None else out
+        workspace = _check_workspace(workspace, need, x.device)
+        out = _check_bf16_out(out, (B, H), x.device)
         args.out = out.data_ptr()
         args.workspace = workspace.data_ptr()
         args.workspace_bytes = workspace.numel()

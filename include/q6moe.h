@@ -117,6 +117,20 @@ size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width); /* per exp
 int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, int64_t rows, int64_t width,
                    uint8_t* dst, void* stream);
 
+/*
+ * Bit-exact decode probe of unit-major expert tables: table (expert e at
+ * table + e * stride) -> out BF16 [experts, rows, width], each weight
+ * RNE_bf16 of its GGUF value (kaggle/glm53_offload/gguf_quant.py:111-173,
+ * the values dequantize_rows(..., dtype=bfloat16) gives; a Q6_K weight whose
+ * code is 32 decodes to +0 whatever the sign of d*sc). ``path`` picks the
+ * decoder the MoE kernels use: 0 the generic kernels' register decode, 1 the
+ * decode-step kernels' LDS-staged decode, 2 the prefill kernels' whole-block
+ * decode (Q6_K only). No counterpart call in the reference: it is the
+ * unit-major analogue of q6moe_q6_decode, for tests of the decoders.
+ */
+int q6moe_moe_unpack(const uint8_t* table, int qtype, int64_t experts, int64_t rows, int64_t width,
+                     int64_t stride, int path, uint16_t* out, void* stream);
+
 /* Weight tables of one projection for all experts. */
 typedef struct q6moe_table {
   int qtype;                /* gate/up: Q6MOE_Q6_K or Q6MOE_Q4_K; down: the same or Q6MOE_Q8_0 */
@@ -147,6 +161,10 @@ typedef struct q6moe_moe_args {
   /* optional profiling: NULL, or Q6MOE_MOE_EVENTS hipEvent_t handles recorded on ``stream``
      before routing, after routing, after gate/up, after down, after the combine */
   void* const* events;
+  /* optional BF16 [H] shared-expert router (kaggle/qwen38_tpu/math.py:283): the shared
+     output is scaled per token by RNE(sigmoid(RNE(x . shared_router))), computed on the
+     device; NULL: shared_scale (or 1) is used. Not both. */
+  const uint16_t* shared_router;
 } q6moe_moe_args;
 
 #define Q6MOE_MOE_EVENTS 5

@@ -21,7 +21,7 @@ tokens and their routes instead of experts (routing_validation.py:52-71).
 import numpy as np
 
 from .gguf import dequantize_rows
-from .numerics import silu_bf16
+from .numerics import sigmoid, silu_bf16
 from .packed_q6 import bf16_round
 from .routing import route_weights
 
@@ -78,6 +78,17 @@ def expert_ffn(gate, up, down, x, ids, weights, *, types, hidden, intermediate, 
     if shared.get("gate_scale") is not None:
         y = bf16_round(y * bf16_round(np.asarray(shared["gate_scale"], np.float32))[:, None])
     return bf16_round(routed + y)
+
+
+def shared_gate(x, router):
+    """Per-token shared-expert gate of math.py:283 with linear / sigmoid of
+    math.py:10-24: RNE_bf16(sigmoid(RNE_bf16(x . router))), x BF16 values
+    [B, H], router BF16 values [H] (the checkpoint keeps it BF16,
+    checkpoint.py:316-321); the dot in FP64 here, FP32 in the reference."""
+    x = bf16_round(np.asarray(x, np.float32))
+    w = bf16_round(np.asarray(router, np.float32))
+    logit = bf16_round((x.astype(np.float64) @ w.astype(np.float64)).astype(np.float32))
+    return bf16_round(sigmoid(logit))
 
 
 def expert_ffn_per_token(gate, up, down, x, ids, weights, *, types, hidden, intermediate):

@@ -172,3 +172,28 @@ def test_dequantize_rows_hip_matches_oracle_and_frozen_vectors(device, qtype):
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
     gotb = dequantize_rows(torch.from_numpy(raw).to(device), qtype, width, dtype=torch.bfloat16)
     np.testing.assert_array_equal(_bf16_bits(gotb), packed_q6.bf16_bits(want))
+
+
+@pytest.mark.parametrize("case", ["r65_k300", "r130_k520", "r64_k256_all_scales"])
+def test_reference_packer_planes_decode_and_repack_on_device(device, case):
+    # Planes from the reference's own pack_q6 (tests/golden/packed_q6_soa_reference.npz):
+    # the device repack reproduces them byte for byte, and the kernels read them
+    # as the reference's layout (decode bit-exact, projection within rtol 2e-5).
+    from .conftest import GOLDEN
+
+    ref = np.load(GOLDEN / "packed_q6_soa_reference.npz")
+    raw, inputs = ref[f"{case}_raw"], int(ref[f"{case}_inputs"])
+    data, scales = ref[f"{case}_data"], ref[f"{case}_scales"]
+    outputs = raw.shape[0]
+    d_data, d_scales = q6_pack(torch.from_numpy(raw).to(device), inputs)
+    np.testing.assert_array_equal(d_data.cpu().numpy(), data)
+    np.testing.assert_array_equal(d_scales.cpu().numpy(), scales)
+    tdata, tscales = torch.from_numpy(data).to(device), torch.from_numpy(scales).to(device)
+    got = q6_decode(tdata, tscales, output_features=outputs, input_features=inputs)
+    want = packed_q6.bf16_round(packed_q6.decode_reference(raw, inputs))
+    np.testing.assert_array_equal(got.float().cpu().numpy(), want)
+    x = np.random.default_rng(3).normal(size=(9, inputs)).astype(np.float32)
+    xb = torch.from_numpy(x).to(device).to(torch.bfloat16)
+    y = q6_matmul(xb, tdata, tscales, output_features=outputs).cpu().numpy()
+    ref_y = packed_q6.projection_reference(xb.float().cpu().numpy(), raw)
+    np.testing.assert_allclose(y, ref_y, rtol=2e-5, atol=2e-4)

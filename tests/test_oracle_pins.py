@@ -287,3 +287,53 @@ def test_decode_attention_oracle_closed_forms():
             p /= p.sum()
             want = p @ v[i, :n, h // r].astype(np.float64)
             assert np.max(np.abs(got[i, h] - want)) <= 2e-2 * np.abs(want).max() + 1e-3
+
+
+SOA_GOLDEN = GOLDEN / "packed_q6_soa_reference.npz"
+SOA_CASES = ("r65_k300", "r130_k520", "r64_k256_all_scales")
+
+
+@pytest.mark.parametrize("case", SOA_CASES)
+def test_soa_byte_map_matches_reference_packer_output(case):
+    # Planes written by the reference's own pack_q6 (kaggle/packed_q6/layout.py:49-90,
+    # tests/golden/make_soa_golden.py): the oracle's byte map and the product
+    # packer must both reproduce them byte for byte.
+    from q6moe import pack_q6
+
+    ref = np.load(SOA_GOLDEN)
+    raw, inputs = ref[f"{case}_raw"], int(ref[f"{case}_inputs"])
+    data, scales = ref[f"{case}_data"], ref[f"{case}_scales"]
+    outputs = raw.shape[0]
+    assert int(ref[f"{case}_outputs"]) == outputs
+    plane, off = packed_q6.soa_offsets(outputs, inputs)
+    assert (data.size, scales.size) == packed_q6.soa_sizes(outputs, inputs)
+    np.testing.assert_array_equal(data[off[plane == 0]], raw[plane == 0])
+    np.testing.assert_array_equal(scales[off[plane == 1]], raw[plane == 1])
+    packed = pack_q6(raw, inputs)
+    np.testing.assert_array_equal(packed.data, data)
+    np.testing.assert_array_equal(packed.scales, scales)
+    np.testing.assert_array_equal(
+        packed_q6.decode_soa(data, scales, outputs, inputs).view(np.uint32),
+        packed_q6.decode_reference(raw, inputs).view(np.uint32),
+    )
+
+
+def test_shared_gate_oracle_closed_forms():
+    # math.py:283: RNE(sigmoid(RNE(x . router))). One-hot routers pick a column
+    # of x; sigmoid(0) = 0.5 exactly; large logits saturate. A dot of
+    # 1 + 17 * 2^-12 is not a BF16 value: it must round to 1 + 2^-7 before
+    # the sigmoid, which changes the gate by one BF16 step.
+    x = np.zeros((4, 8), np.float32)
+    x[1, 3] = 64.0
+    x[2, 3] = -64.0
+    x[3, :2] = (1.0, 17 * 2.0**-12)
+    router = np.zeros(8, np.float32)
+    router[3] = 1.0
+    g = moe.shared_gate(x, router)
+    assert g[0] == 0.5 and g[1] == 1.0 and g[2] == packed_q6.bf16_round(np.float32(np.exp(-64.0)))
+    r2 = np.zeros(8, np.float32)
+    r2[:2] = 1.0
+    want = packed_q6.bf16_round(np.float32(1.0 / (1.0 + np.exp(-(1.0 + 2.0**-7)))))
+    assert moe.shared_gate(x[3:], r2)[0] == want
+    unrounded = packed_q6.bf16_round(np.float32(1.0 / (1.0 + np.exp(-(1.0 + 17 * 2.0**-12)))))
+    assert want != unrounded
