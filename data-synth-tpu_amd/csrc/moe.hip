@@ -579,9 +579,14 @@ struct WsLayout {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I, int64_t Is,
-                          int64_t mtile) {
-  WsLayout L;
+// Workspace regions of one call. The routing result, the activations and the
+// shared expert's buffers are common; the decode kernels' per-slot tables and
+// token-major FP32 contributions, and the grouped kernels' route lists, tiles
+// and BF16 expert outputs, are each needed by one path only, so a call reserves
+// the regions of the path it takes (``decode``).
+static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I, int64_t Is, int64_t mtile,
+                          bool decode) {
+  WsLayout L{};
   const int64_t n = B * K;
   size_t o = 0;
   auto take = [&](size_t bytes) {
@@ -590,25 +595,28 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
     return at;
   };
   L.hdr = take(64);
-  L.active = take(4 * E);
-  L.act_off = take(4 * (E + 1));
-  L.tile = take(sizeof(PfTile) * (E + n / mtile + 1));
-  L.ent_r = take(4 * n);
-  L.route_tok = take(4 * n);
   L.route_w = take(4 * n);
-  L.tok_pos = take(4 * n);
   L.act = take(2 * n * I);
-  L.y = take(2 * n * H);
   L.sh_act = take(Is > 0 ? 2 * B * Is : 0);
   L.sh_y = take(Is > 0 ? 2 * B * H : 0);
   L.sh_gate = take(Is > 0 ? 2 * B : 0);
-  L.slot_e = take(4 * E);
-  L.slot_t0 = take(4 * E);
-  L.slot_cnt = take(4 * E);
-  L.tok_n = take(4 * B);
-  L.route_dst = take(4 * n);
-  L.contrib = take(4 * n * H);
-  L.chunk_cnt = take(4 * (cdiv(B, kChunk) + 1) * E);
+  if (decode) {
+    L.slot_e = take(4 * E);
+    L.slot_t0 = take(4 * E);
+    L.slot_cnt = take(4 * E);
+    L.tok_n = take(4 * B);
+    L.route_dst = take(4 * n);
+    L.contrib = take(4 * n * H);
+  } else {
+    L.active = take(4 * E);
+    L.act_off = take(4 * (E + 1));
+    L.tile = take(sizeof(PfTile) * (E + n / mtile + 1));
+    L.ent_r = take(4 * n);
+    L.route_tok = take(4 * n);
+    L.tok_pos = take(4 * n);
+    L.y = take(2 * n * H);
+    L.chunk_cnt = take(4 * (cdiv(B, kChunk) + 1) * E);
+  }
   L.total = o;
   return L;
 }
@@ -860,19 +868,24 @@ extern "C" size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_
                                            int64_t intermediate, int64_t shared_intermediate) {
   if (tokens < 1 || top_k < 1 || experts < 1 || hidden < 1 || intermediate < 1 || shared_intermediate < 0)
     return 0;
-  return ws_layout(tokens, top_k, experts, hidden, intermediate, shared_intermediate, kPrefillTile).total;
+  const size_t pf = ws_layout(tokens, top_k, experts, hidden, intermediate, shared_intermediate, kPrefillTile,
+                              false).total;
+  if (!dec_supported(tokens, top_k, experts)) return pf;
+  const size_t dec = ws_layout(tokens, top_k, experts, hidden, intermediate, shared_intermediate, kPrefillTile,
+                               true).total;
+  return pf > dec ? pf : dec;
 }
 
-extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
-  Q6MOE_REQUIRE(a, "moe_forward: null args");
-  Q6MOE_REQUIRE(a->x && a->ids && a->weights && a->out && a->workspace, "moe_forward: null pointer");
+// The routed FFN on a given workspace (the caller's, or the static scratch).
+static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  Q6MOE_REQUIRE(a->x && a->ids && a->weights && a->out && workspace, "moe_forward: null pointer");
   const int64_t B = a->tokens, K = a->top_k, E = a->experts, H = a->hidden, I = a->intermediate;
   Q6MOE_REQUIRE(B >= 1 && K >= 1 && E >= 1 && H >= 1 && I >= 1, "moe_forward: sizes must be positive");
   Q6MOE_REQUIRE(E <= kRouteMaxExperts, "moe_forward: at most 256 experts per call");
   Q6MOE_REQUIRE(K <= 32, "moe_forward: top_k must be at most 32");
   Q6MOE_REQUIRE(B * K <= (1 << 28) && H <= (1 << 24) && I <= (1 << 24), "moe_forward: problem too large");
   Q6MOE_REQUIRE(H % 8 == 0 && I % 8 == 0, "moe_forward: hidden and intermediate must be multiples of 8");
-  Q6MOE_REQUIRE(aligned(a->x, 16) && aligned(a->out, 16) && aligned(a->workspace, 256),
+  Q6MOE_REQUIRE(aligned(a->x, 16) && aligned(a->out, 16) && aligned(workspace, 256),
                 "moe_forward: x/out need 16-byte and workspace 256-byte alignment");
   Q6MOE_REQUIRE(a->gate.qtype == a->up.qtype && (a->gate.qtype == Q6MOE_Q6_K || a->gate.qtype == Q6MOE_Q4_K) &&
                     (a->down.qtype == a->gate.qtype || a->down.qtype == Q6MOE_Q8_0),
@@ -895,23 +908,34 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
         (rc = validate_table(a->shared_down, "shared_down", H, Is, 1)))
       return rc;
   }
-  const WsLayout L = ws_layout(B, K, E, H, I, Is, kPrefillTile);
-  if (a->workspace_bytes < L.total) {
+  if (a->mode == 1 && !dec_supported(B, K, E)) {
+    set_error("moe_forward: decode mode needs tokens*top_k <= 1024, top_k <= 32, experts <= 256");
+    return Q6MOE_ERR_INVALID;
+  }
+  const bool decode = dec_supported(B, K, E) && (a->mode == 1 || (a->mode == 0 && B <= 64));
+  const WsLayout L = ws_layout(B, K, E, H, I, Is, kPrefillTile, decode);
+  if (workspace_bytes < L.total) {
     set_error("moe_forward: workspace too small (need " + std::to_string(L.total) + " bytes)");
     return Q6MOE_ERR_INVALID;
   }
-  uint8_t* w = reinterpret_cast<uint8_t*>(a->workspace);
+  uint8_t* w = reinterpret_cast<uint8_t*>(workspace);
   MoeWs ws;
   ws.hdr = reinterpret_cast<int*>(w + L.hdr);
-  ws.active = reinterpret_cast<int*>(w + L.active);
-  ws.act_off = reinterpret_cast<int*>(w + L.act_off);
-  ws.tile = reinterpret_cast<PfTile*>(w + L.tile);
-  ws.ent_r = reinterpret_cast<float*>(w + L.ent_r);
-  ws.route_tok = reinterpret_cast<int*>(w + L.route_tok);
   ws.route_w = reinterpret_cast<float*>(w + L.route_w);
-  ws.tok_pos = reinterpret_cast<int*>(w + L.tok_pos);
   ws.act = reinterpret_cast<uint16_t*>(w + L.act);
-  ws.y = reinterpret_cast<uint16_t*>(w + L.y);
+  ws.active = ws.act_off = ws.route_tok = ws.tok_pos = nullptr;
+  ws.tile = nullptr;
+  ws.ent_r = nullptr;
+  ws.y = nullptr;
+  if (!decode) {  // regions of the grouped path only
+    ws.active = reinterpret_cast<int*>(w + L.active);
+    ws.act_off = reinterpret_cast<int*>(w + L.act_off);
+    ws.tile = reinterpret_cast<PfTile*>(w + L.tile);
+    ws.ent_r = reinterpret_cast<float*>(w + L.ent_r);
+    ws.route_tok = reinterpret_cast<int*>(w + L.route_tok);
+    ws.tok_pos = reinterpret_cast<int*>(w + L.tok_pos);
+    ws.y = reinterpret_cast<uint16_t*>(w + L.y);
+  }
   ws.sh_act = Is ? reinterpret_cast<uint16_t*>(w + L.sh_act) : nullptr;
   ws.sh_y = Is ? reinterpret_cast<uint16_t*>(w + L.sh_y) : nullptr;
 
@@ -927,11 +951,6 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   auto mark = [&](int i) {
     if (a->events && a->events[i]) hipEventRecord((hipEvent_t)a->events[i], s);
   };
-  const bool decode = dec_supported(B, K, E) && (a->mode == 1 || (a->mode == 0 && B <= 64));
-  if (a->mode == 1 && !dec_supported(B, K, E)) {
-    set_error("moe_forward: decode mode needs tokens*top_k <= 1024, top_k <= 32, experts <= 256");
-    return Q6MOE_ERR_INVALID;
-  }
   const int fmt = fmt_of(a->gate.qtype), fmt_dn = fmt_of(a->down.qtype);
   // Generic (non-tiled) expert phases for the call's formats.
   auto phases = [&](const Proj& pg, const Proj& pu, const Proj& pd, const TokenSrc& src, int grid_x, int max_tok,
@@ -1044,4 +1063,9 @@ extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   rc = check_launch("moe_combine_kernel");
   mark(4);
   return rc;
+}
+
+extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
+  Q6MOE_REQUIRE(a, "moe_forward: null args");
+  return moe_forward_impl(a, a->workspace, a->workspace_bytes, stream);
 }

@@ -241,7 +241,22 @@ class ExpertFFN:
 
     def __call__(self, gate, up, down, x, ids, weights, *, shared=None, workspace=None, out=None,
                  events=None):
-        """Routed FFN of x [B, hidden] BF16 with ids/weights [B, top_k].
+        """Routed FFN of x [B, hidden] BF16 through ``q6moe_moe_forward``; see ``args``."""
+        args, out, keep = self.args(gate, up, down, x, ids, weights, shared=shared, workspace=workspace, out=out,
+                                    events=events)
+        lib = _lib.load()
+        with torch.cuda.device(x.device):
+            rc = lib.q6moe_moe_forward(ctypes.byref(args), _lib.stream_handle(x.device))
+        _lib.check(rc, "moe_forward")
+        del keep
+        return out
+
+    def args(self, gate, up, down, x, ids, weights, *, shared=None, workspace=None, out=None, events=None,
+             with_workspace=True):
+        """The ``q6moe_moe_args`` of one call, its output tensor and the tensors
+        the arguments point into (keep them alive until the call is issued).
+
+        Routed FFN of x [B, hidden] BF16 with ids/weights [B, top_k].
 
         ``shared`` adds the always-on shared expert (engine.py:199-203,
         math.py:282-283): a dict with ``gate``, ``up`` (rows = shared
@@ -302,12 +317,14 @@ class ExpertFFN:
                 router = router.to(x.device).contiguous()
                 keep.append(router)
                 args.shared_router = router.data_ptr()
-        need = self.workspace_bytes(B, K, experts, Is)
-        workspace = _check_workspace(workspace, need, x.device)
+        if with_workspace:
+            need = self.workspace_bytes(B, K, experts, Is)
+            workspace = _check_workspace(workspace, need, x.device)
+            keep.append(workspace)
+            args.workspace = workspace.data_ptr()
+            args.workspace_bytes = workspace.numel()
         out = _check_bf16_out(out, (B, H), x.device)
         args.out = out.data_ptr()
-        args.workspace = workspace.data_ptr()
-        args.workspace_bytes = workspace.numel()
         args.mode = self.mode
         if events is not None:
             if len(events) != 5:
@@ -315,11 +332,8 @@ class ExpertFFN:
             handles = (ctypes.c_void_p * 5)(*[ctypes.c_void_p(ev.cuda_event) for ev in events])
             keep.append(handles)
             args.events = ctypes.cast(handles, ctypes.POINTER(ctypes.c_void_p))
-        lib = _lib.load()
-        with torch.cuda.device(x.device):
-            rc = lib.q6moe_moe_forward(ctypes.byref(args), _lib.stream_handle(x.device))
-        _lib.check(rc, "moe_forward")
-        return out
+        keep += [x, ids, weights, gate, up, down]
+        return args, out, keep
 
 
 @lru_cache(maxsize=32)
