@@ -15,6 +15,8 @@
 //                        optional always-on shared expert RNE(routed + shared).
 //
 // No atomics touch floating-point data, so results are bitwise reproducible.
+#include <mutex>
+
 #include "moe_common.h"
 #include "q6moe_api.h"
 
@@ -876,8 +878,52 @@ extern "C" size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_
   return pf > dec ? pf : dec;
 }
 
+// Scratch of q6moe_moe_forward_noalloc: the workspace regions of one call
+// (routing tables, activations, expert outputs or contributions, shared-expert
+// buffers) for callers that cannot allocate device memory. Each GPU holds its
+// own copy for the life of the process. Host code uses the per-device address
+// from hipGetSymbolAddress, never the array's name. Every call on a GPU shares
+// that GPU's copy: calls that overlap on one GPU (other streams, other host
+// threads) race. No region needs to start zeroed (each is written before it
+// is read in a call), so nothing is cleared between calls.
+constexpr size_t kStaticScratchBytes = Q6MOE_NOALLOC_SCRATCH_BYTES;
+static_assert(kStaticScratchBytes == size_t(32) << 20, "32 MiB of static scratch per device");
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch[kMaxScratchDevices];
+
+// The current device's address of ``scratch``, looked up once per device with
+// that device current.
+static int static_scratch(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    set_error(std::string("moe_forward_noalloc: hipGetDevice: ") + hipGetErrorString(err));
+    return Q6MOE_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    set_error("moe_forward_noalloc: device index out of range");
+    return Q6MOE_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p) {
+      set_error(std::string("moe_forward_noalloc: hipGetSymbolAddress(scratch): ") + hipGetErrorString(err));
+      return Q6MOE_ERR_HIP;
+    }
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return Q6MOE_OK;
+}
+
 // The routed FFN on a given workspace (the caller's, or the static scratch).
-static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t workspace_bytes, void* stream,
+                            bool static_ws = false) {
   Q6MOE_REQUIRE(a->x && a->ids && a->weights && a->out && workspace, "moe_forward: null pointer");
   const int64_t B = a->tokens, K = a->top_k, E = a->experts, H = a->hidden, I = a->intermediate;
   Q6MOE_REQUIRE(B >= 1 && K >= 1 && E >= 1 && H >= 1 && I >= 1, "moe_forward: sizes must be positive");
@@ -915,7 +961,12 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   const bool decode = dec_supported(B, K, E) && (a->mode == 1 || (a->mode == 0 && B <= 64));
   const WsLayout L = ws_layout(B, K, E, H, I, Is, kPrefillTile, decode);
   if (workspace_bytes < L.total) {
-    set_error("moe_forward: workspace too small (need " + std::to_string(L.total) + " bytes)");
+    if (static_ws)
+      set_error("moe_forward_noalloc: this call needs " + std::to_string(L.total) +
+                " bytes of scratch; the static scratch holds " + std::to_string(kStaticScratchBytes) +
+                " (use q6moe_moe_forward with a workspace)");
+    else
+      set_error("moe_forward: workspace too small (need " + std::to_string(L.total) + " bytes)");
     return Q6MOE_ERR_INVALID;
   }
   uint8_t* w = reinterpret_cast<uint8_t*>(workspace);
@@ -1068,4 +1119,14 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
 extern "C" int q6moe_moe_forward(const q6moe_moe_args* a, void* stream) {
   Q6MOE_REQUIRE(a, "moe_forward: null args");
   return moe_forward_impl(a, a->workspace, a->workspace_bytes, stream);
+}
+
+extern "C" int q6moe_moe_forward_noalloc(const q6moe_moe_args* a, void* stream) {
+  Q6MOE_REQUIRE(a, "moe_forward_noalloc: null args");
+  Q6MOE_REQUIRE(!a->workspace && a->workspace_bytes == 0,
+                "moe_forward_noalloc: takes no workspace (workspace must be NULL and workspace_bytes 0)");
+  void* ptr = nullptr;
+  const int rc = static_scratch(&ptr);
+  if (rc) return rc;
+  return moe_forward_impl(a, ptr, kStaticScratchBytes, stream, true);
 }

@@ -141,6 +141,7 @@ SIGNATURES = {
     "q6moe_moe_unpack": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _int, _vp, _vp]),
     "q6moe_moe_workspace_size": (_size, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "q6moe_moe_forward": (_int, [ctypes.POINTER(MoeArgs), _vp]),
+    "q6moe_moe_forward_noalloc": (_int, [ctypes.POINTER(MoeArgs), _vp]),
     "q6moe_kv_read": (_int, [ctypes.POINTER(KvArgs), _vp]),
     "q6moe_kv_quantize": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _vp]),
     "q6moe_kv_write": (_int, [ctypes.POINTER(KvWriteArgs), _vp]),

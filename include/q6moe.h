@@ -185,6 +185,21 @@ size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_t experts, 
 
 int q6moe_moe_forward(const q6moe_moe_args* args, void* stream);
 
+/*
+ * q6moe_moe_forward without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. args->workspace must
+ * be NULL and args->workspace_bytes 0: the call uses the library's static
+ * per-device scratch of Q6MOE_NOALLOC_SCRATCH_BYTES (32 MiB, held by each GPU
+ * the library runs on until the process ends) and allocates nothing. Calls
+ * whose regions (q6moe_moe_workspace_size of their shape) exceed it are
+ * rejected with Q6MOE_ERR_INVALID. Every call on a GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (several streams or host threads)
+ * race; serialise them.
+ */
+#define Q6MOE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int q6moe_moe_forward_noalloc(const q6moe_moe_args* args, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* INT8 KV cache gather + dequant (read_quantized).                         */
 /* ------------------------------------------------------------------------ */
