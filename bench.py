@@ -1,25 +1,47 @@
 #!/usr/bin/env python3
-"""Benchmark of the packed-Q6 routed-expert decode step on one MI355X.
+"""Benchmark of the packed-Q6/Q4 expert matmul and the Q8 KV gather on one MI355X.
 
-Workload (default): one MoE expert-FFN decode step with Q6_K experts --
-128 experts, top-8 routing, hidden 2048, expert intermediate 768, SwiGLU,
-8 tokens, weights N(0, 0.02) quantized to Q6_K, x N(0, 1) BF16, router
-logits N(0, 1) -> softmax -> top-8 -> renormalised BF16 weights, seed 1.
+Headline workload: one MoE expert-FFN decode step with Q6_K experts -- 128
+experts, top-8 routing, hidden 2048, expert intermediate 768, SwiGLU, 8 tokens,
+weights N(0, 0.02) quantized to Q6_K, x N(0, 1) BF16, router logits N(0, 1) ->
+softmax -> top-8 -> renormalised BF16 weights, seed 1. A step is one call of
+the routed FFN (route sort, fused gate/up + SwiGLU, down projection, combine).
+Steps rotate over ``--layers`` copies of the layer's expert tables at distinct
+HBM addresses (default 4: about 0.8 GB of active expert bytes per rotation,
+over 3x the 256 MB Infinity Cache), so the weights stream from HBM. ``value``
+is algorithmic bytes per step (active experts' packed weights + activations +
+routing inputs + output, each byte once) over the mean time of ``--steps``
+back-to-back steps.
 
-A step is one call of the routed FFN (route sort, fused gate/up + SwiGLU,
-down projection, combine). Steps rotate over ``--layers`` copies of the
-layer's expert tables at distinct HBM addresses (default 4: about 0.8 GB of
-active expert bytes per rotation, over 3x the 256 MB Infinity Cache), so the
-weights stream from HBM. The metric is algorithmic bytes per step (active
-experts' packed weights + activations + routing inputs + output) / time.
+Every workload is checked before it is timed (finite outputs, and, in the CPU
+baseline leg, the CPU oracle's values within tolerance: max relative error
+1e-2 for the MoE, rtol 2e-5 / atol 2e-4 for the projection, bit-exact for the
+KV gather); a failure prints an error line and exits with status 1.
 
-Output: one JSON line (rank 0) with the ``roofline`` of the dominant kernel
-(moe_dec_gate_up_kernel, timed with HIP events on the stream it runs on), the
-``cpu_baseline`` (the NumPy oracle on this host, one step, one thread) and a
-``prefill`` block: the same layer shapes with 4096 tokens, skewed routing
-(per-expert logit bias N(0, 0.5)), seed 2, whose FLOPs (2 * 4096 * 8 * 3 *
-2048 * 768) over the step time give TFLOP/s against the 2.5 PFLOP/s dense
-BF16 MFMA peak.
+Besides the headline line's ``roofline`` (moe_dec_gate_up_kernel, HIP events
+recorded between the launches on their stream) and ``cpu_baseline``, the
+``configs`` block carries, per workload: throughput with tokens/s, the median,
+min and max over seeded interleaved repetitions of every method
+(kaggle/packed_q6/benchmark.py:127-154), the dominant kernel's roofline, the
+HBM traffic per launch from the committed rocprofv3 counter summaries
+(profiles/*__hbm_bytes.txt; null where none exists) and a CPU baseline:
+
+* projection  x BF16 [8, 2048] x Q6_K W [2048 -> 768], seed 0 (hot, and over 640
+  distinct weight copies, timed as replays of a captured HIP graph); beside
+  it the decode-then-BF16-GEMM and predecoded-BF16 GEMM baselines
+  (kaggle/packed_q6/baselines.py:14-46).
+* decode      the headline step; beside it the decode-then-BF16-GEMM and
+  predecoded-BF16 baselines on the library GEMM (torch.bmm).
+* prefill     the same layer with 4096 tokens, skewed routing (per-expert logit
+  bias N(0, 0.5)), seed 2; TFLOP/s against the 2.5 PFLOP/s dense BF16 peak.
+* q4k_shared  Q4_K, 64 experts, top-6, hidden 4096, intermediate 1024, plus an
+  always-on shared expert of 4096, N(0, 0.015), seed 3, at 1, 8 and 64 tokens.
+* kv_gather   paged INT8 KV gather + dequant of 8 x 32768 tokens, 4 KV heads of
+  128, pages of 256, FP32 per-token-per-head scales, seed 4.
+
+The CPU baseline is the NumPy oracle (``kind: port``) on this host with the
+stated number of threads (the host's CPU affinity, at most 16), on a bounded
+sample of each workload; it is reported beside the GPU numbers, not targeted.
 """
 
 import argparse
@@ -41,33 +63,325 @@ EXPERTS, TOP_K, HIDDEN, INTER, TOKENS, SEED = 128, 8, 2048, 768, 8, 1
 PREFILL_TOKENS, PREFILL_SEED, PREFILL_BIAS = 4096, 2, 0.5
 PREFILL_FLOPS = 2 * PREFILL_TOKENS * TOP_K * 3 * HIDDEN * INTER
 Q6_PROJ_BYTES = 768 * 8 * 210  # one 768x2048 (or 2048x768) Q6_K projection: 210 bytes per 256 weights
-# L2-to-fabric bytes per launch measured with rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE over this script, scaled by a 512 MiB device copy in the same run
-# (profiles/moe_q6k_e128_top8_h2048_i768__hbm_bytes.txt); they change only
-# when the kernels do and are re-measured with them.
-TRAFFIC_BYTES = {"moe_dec_gate_up_kernel": 129_900_000, "moe_pf_gate_up_kernel": 644_420_000}
+PROFILES = ROOT / "profiles"
+REPS = 7  # interleaved repetitions per method (>= 7, as the reference harness)
+
+
+class CheckFailed(RuntimeError):
+    pass
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def step_bytes(active, routes):
-    """Algorithmic HBM bytes of one decode step (each needed byte once)."""
-    weights = active * 3 * Q6_PROJ_BYTES
-    x = TOKENS * HIDDEN * 2
-    out = TOKENS * HIDDEN * 2
-    routing = TOKENS * TOP_K * (4 + 2)
-    return weights + x + out + routing
+def cpu_threads():
+    return max(1, min(len(os.sched_getaffinity(0)), 16))
 
 
-def gate_up_bytes(active, routes):
-    """Algorithmic bytes of one moe_dec_gate_up_kernel launch: gate+up of the active
-    experts, the token activations it reads and the SwiGLU rows it writes."""
-    return active * 2 * Q6_PROJ_BYTES + TOKENS * HIDDEN * 2 + routes * INTER * 2
+def stats(samples):
+    import numpy as np
+
+    v = np.asarray(samples, np.float64)
+    return {"median": round(float(np.median(v)), 3), "min": round(float(v.min()), 3),
+            "max": round(float(v.max()), 3), "mean": round(float(v.mean()), 3), "n": int(v.size)}
 
 
-def measure_prefill(dev, steps, warmup):
+def traffic_of(kernel):
+    """HBM-side bytes per dispatch of ``kernel`` and the summary they come from:
+    the last column of its row in a committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (profiles/*__hbm_bytes.txt, MB per dispatch after scaling by a
+    device copy of known size). (None, None) when no summary lists it."""
+    for f in sorted(PROFILES.glob("*__hbm_bytes.txt")):
+        for line in f.read_text().splitlines():
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if line.startswith("|") and len(cells) >= 3 and cells[0].split(" (")[0] == kernel:
+                try:
+                    return int(round(float(cells[-1]) * 1e6)), f"profiles/{f.name}"
+                except ValueError:
+                    return None, None
+    return None, None
+
+
+def roofline(kernel, bound, work, avg_us, *, work_unit):
+    """Roofline block of one kernel: ``work`` algorithmic bytes (or FLOPs) per
+    launch over its average launch duration."""
+    if bound == "hbm":
+        achieved, peak, unit = work / (avg_us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        achieved, peak, unit = work / (avg_us * 1e-6) / 1e12, MFMA_PEAK_TFLOPS, "TFLOP/s"
+    traffic, source = traffic_of(kernel)
+    return {"kernel": kernel, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_source": source,
+            work_unit: int(work), "avg_launch_us": round(float(avg_us), 3)}
+
+
+def check_close(name, got, want, *, rel=1e-2, exact_frac=0.9):
+    """The MoE gate: finite, max relative error <= rel, and at least exact_frac
+    of the outputs bit-identical to the oracle's BF16 values."""
+    import numpy as np
+
+    got = np.asarray(got, np.float32)
+    if not np.isfinite(got).all():
+        raise CheckFailed(f"{name}: nonfinite output rejected before timing")
+    err = float(np.max(np.abs(got - want)) / max(float(np.abs(want).max()), 1e-30))
+    same = float(np.mean(got == want))
+    if err > rel or same < exact_frac:
+        raise CheckFailed(f"{name}: max relative error {err:.3g} (limit {rel}), {same:.3f} bit-identical")
+    return {"passed": True, "max_rel_error": round(err, 6), "bit_identical_frac": round(same, 4)}
+
+
+def check_finite(name, t):
+    import torch
+
+    if not bool(torch.isfinite(t.float()).all()):
+        raise CheckFailed(f"{name}: nonfinite output rejected before timing")
+
+
+def timed_reps(methods, reps=REPS, inner=10, warmup=2, seed=42):
+    """Per-call device time (us) of each method: ``reps`` repetitions of
+    ``inner`` back-to-back calls bracketed by HIP events on the current stream,
+    the methods interleaved in a seeded random order per repetition
+    (kaggle/packed_q6/benchmark.py:127-149). Returns median/min/max per method."""
+    import numpy as np
+    import torch
+
+    names = list(methods)
+    for name in names:
+        for i in range(warmup):
+            methods[name](i)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(seed)
+    samples = {n: [] for n in names}
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    i = 0
+    for _ in range(reps):
+        for name in rng.permutation(names):
+            fn = methods[name]
+            torch.cuda.synchronize()
+            a.record()
+            for k in range(inner):
+                fn(i + k)
+            b.record()
+            torch.cuda.synchronize()
+            samples[name].append(a.elapsed_time(b) * 1e3 / inner)
+            i += inner
+    return {n: stats(v) for n, v in samples.items()}
+
+
+def phase_means(fn, steps, n_events=5):
+    """Mean per-phase durations (us) of ``steps`` calls of fn(i, events), with
+    ``n_events`` HIP events stamped by the library between its launches."""
+    import numpy as np
+    import torch
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n_events)] for _ in range(steps)]
+    for row in evs:
+        for ev in row:
+            ev.record()
+    torch.cuda.synchronize()
+    for i in range(steps):
+        fn(i, evs[i])
+    torch.cuda.synchronize()
+    return np.array([[row[j].elapsed_time(row[j + 1]) for j in range(n_events - 1)] for row in evs]).mean(0) * 1e3
+
+
+def copies_for(nbytes, lo=2, hi=16):
+    """Weight copies whose rotation exceeds 3x the 256 MB Infinity Cache."""
+    return min(hi, max(lo, -(-3 * 256 * 2**20 // nbytes)))
+
+
+def clone_tables(tabs):
+    return [type(t)(t.qtype, t.data.clone(), None, t.rows, t.width) for t in tabs]
+
+
+def cpu_oracle_moe(L, rows, types, hidden, inter, shared=None, reps=1):
+    """CPU baseline leg: the NumPy oracle on ``rows`` tokens of L with
+    cpu_threads() threads (BLAS threads and a pool over experts); returns
+    (output, seconds per run, threads)."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import moe as oracle_moe
+
+    n = cpu_threads()
+    times, out = [], None
+    with threadpool_limits(n):
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            out = oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"][rows], L["ids"][rows],
+                                        L["weights"][rows], types=types, hidden=hidden, intermediate=inter,
+                                        shared=shared, workers=n)
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    return out, times[len(times) // 2], n
+
+
+class MoeGemmBaselines:
+    """Decode-then-BF16-GEMM baselines of one routed-FFN step on the library's
+    BLAS (the structure of the reference's XLA path, experts.py:82-110 with
+    baselines.py:14-46): the active experts' GGUF rows are decoded to BF16 in
+    HBM with ``dequantize_rows(backend="hip")`` (one launch per projection),
+    then every token runs through every active expert with torch.bmm (BF16
+    operands, FP32 accumulation, BF16 output), SiLU and the product in BF16,
+    and the FP32 route-weighted sum over experts. The active-expert list and
+    the contiguous copy of their GGUF rows are prepared once, outside the
+    timing; ``predecoded`` skips the decode (weights kept as BF16)."""
+
+    def __init__(self, L, dev, qtype, hidden, inter, tokens):
+        import numpy as np
+        import torch
+
+        self.qtype, self.H, self.I, self.E = qtype, hidden, inter, L["experts"]
+        ids = L["ids"][:tokens]
+        self.active = np.unique(ids[L["weights"][:tokens] != 0])
+        self.raw = {n: torch.from_numpy(np.ascontiguousarray(L[n][self.active])).to(dev)
+                    for n in ("gate", "up", "down")}
+        self.ids = torch.from_numpy(ids).to(dev).long()
+        self.w = torch.from_numpy(L["weights"][:tokens]).to(dev).to(torch.bfloat16)
+        self.x = torch.from_numpy(L["x"][:tokens]).to(dev).to(torch.bfloat16)
+        self.act = torch.from_numpy(self.active).to(dev).long()
+        self.pre = self.decode()
+
+    def decode(self):
+        import torch
+
+        from q6moe.quant import dequantize_rows
+
+        return [dequantize_rows(self.raw[n], self.qtype, w, dtype=torch.bfloat16)
+                for n, w in (("gate", self.H), ("up", self.H), ("down", self.I))]
+
+    def gemms(self, wg, wu, wd):
+        import torch
+
+        U, B = wg.shape[0], self.x.shape[0]
+        # route weights r[b, e]: BF16 sums of the token's weights for e (experts.py:66-73)
+        r = torch.zeros((B, self.E), dtype=torch.float32, device=self.x.device)
+        r.scatter_add_(1, self.ids, self.w.float())
+        r = r.to(torch.bfloat16).float()[:, self.act].t()  # [U, B]
+        xt = self.x.t().contiguous().unsqueeze(0).expand(U, -1, -1).contiguous()  # [U, H, B]
+        gt = torch.bmm(wg, xt)  # [U, I, B], both operands contiguous
+        ut = torch.bmm(wu, xt)
+        at = torch.nn.functional.silu(gt) * ut
+        yt = torch.bmm(wd, at)  # [U, H, B]
+        return (yt.float() * r[:, None, :]).sum(0).t().to(torch.bfloat16)
+
+    def decode_then_gemm(self, i=0):
+        return self.gemms(*self.decode())
+
+    def predecoded(self, i=0):
+        return self.gemms(*self.pre)
+
+
+# ---------------------------------------------------------------------------
+# Workloads
+# ---------------------------------------------------------------------------
+
+
+def measure_projection(dev, with_cpu):
+    """Single packed-Q6 projection, x BF16 [8, 2048] x W [2048 -> 768], seed 0."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from q6moe import _lib, pack_q6
+    from q6moe.kernel import q6_decode, q6_matmul
+    from q6moe.synth import projection
+
+    w = projection(seed=0)
+    packed = pack_q6(w["raw"], 2048)
+    data = torch.from_numpy(packed.data).to(dev)
+    scales = torch.from_numpy(packed.scales).to(dev)
+    x = torch.from_numpy(w["x"]).to(dev).to(torch.bfloat16)
+    res = {"workload": "q6_projection_x8x2048_w2048to768_seed0"}
+    y32 = q6_matmul(x, data, scales, output_features=768).cpu().numpy()
+    if not np.isfinite(y32).all():
+        raise CheckFailed("projection: nonfinite output rejected before timing")
+    if with_cpu:
+        from threadpoolctl import threadpool_limits
+
+        from oracle import packed_q6
+
+        n = cpu_threads()
+        times = []
+        with threadpool_limits(n):
+            for _ in range(20):
+                t0 = time.perf_counter()
+                want = packed_q6.projection_reference(x.float().cpu().numpy(), w["raw"])
+                times.append(time.perf_counter() - t0)
+        np.testing.assert_allclose(y32, want, rtol=2e-5, atol=2e-4)
+        err = y32.astype(np.float64) - want
+        res["check"] = {"passed": True, "rtol": 2e-5, "atol": 2e-4, "max_abs_error": float(np.abs(err).max())}
+        secs = float(np.median(times))
+        res["cpu_baseline"] = {"value": round(8 / secs, 1), "unit": "tokens/s", "cores": n, "kind": "port",
+                               "sample": f"the whole projection (decode of W, FP64 product) by the NumPy oracle, "
+                                         f"median of 20 runs: {secs * 1e3:.2f} ms"}
+    lib = _lib.load()
+    yb = torch.empty((8, 768), dtype=torch.bfloat16, device=dev)
+    stream = lambda: _lib.stream_handle(dev)  # noqa: E731
+
+    def fused_call(d, s):
+        rc = lib.q6moe_q6_matmul(ctypes.c_void_p(x.data_ptr()), 8, 2048, 2048, ctypes.c_void_p(d.data_ptr()),
+                                 ctypes.c_void_p(s.data_ptr()), 768, ctypes.c_void_p(yb.data_ptr()), _lib.BF16,
+                                 768, stream())
+        _lib.check(rc, "q6_matmul")
+
+    xt = x.t().contiguous()
+
+    def decode_gemm():
+        wdec = q6_decode(data, scales, output_features=768, input_features=2048)
+        return torch.mm(wdec, xt)  # [768, 8]: both operands contiguous
+
+    wpre = q6_decode(data, scales, output_features=768, input_features=2048)
+    base = {"decode_then_bf16_gemm": decode_gemm, "predecoded_bf16_gemm": lambda: torch.mm(wpre, xt)}
+    for name, f in base.items():
+        check_finite(name, f())
+    # Launch-bound (a ~5 us kernel): time replays of captured HIP graphs of
+    # ``per`` calls, so host dispatch is not in the per-call time.
+    per, copies = 20, 640
+    datas, scaless = data.repeat(copies, 1), scales.repeat(copies, 1)
+    graphs = {}
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for name, body in (("fused_hot", lambda k: fused_call(data, scales)),
+                           ("fused_cold", lambda k: fused_call(datas[k], scaless[k])),
+                           ("decode_then_bf16_gemm", lambda k: decode_gemm()),
+                           ("predecoded_bf16_gemm", lambda k: torch.mm(wpre, xt))):
+            for k in range(2):
+                body(k)
+            g = torch.cuda.CUDAGraph()
+            n_calls = copies if name == "fused_cold" else per
+            with torch.cuda.graph(g, stream=s):
+                for k in range(n_calls):
+                    body(k)
+            graphs[name] = (g, n_calls)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    fused_call(data, scales)
+    eager = yb.clone()
+    graphs["fused_hot"][0].replay()
+    torch.cuda.synchronize()
+    if not torch.equal(eager.view(torch.int16), yb.view(torch.int16)):
+        raise CheckFailed("projection: graph replay differs from the eager call")
+    t = timed_reps({n: (lambda i, g=g: g.replay()) for n, (g, _) in graphs.items()}, inner=3)
+    per_call = {n: {k: (round(v / graphs[n][1], 3) if k != "n" else v) for k, v in st.items()}
+                for n, st in t.items()}
+    nbytes = 1_290_240 + 32_768 + 12_288
+    hot, cold = per_call["fused_hot"]["median"], per_call["fused_cold"]["median"]
+    res.update({
+        "value": round(8 / (hot * 1e-6), 1), "unit": "tokens/s", "us_per_call": hot,
+        "tokens_per_s": round(8 / (hot * 1e-6), 1), "cold_us_per_call": cold,
+        "cold_GBps": round(nbytes / (cold * 1e-6) / 1e9, 1), "bytes_per_call": nbytes, "cold_copies": copies,
+        "timing": "device time per call from replays of captured HIP graphs",
+        "methods_us_per_call": per_call,
+        "roofline": roofline("q6moe::q6_skinny_kernel<1>", "hbm", nbytes, cold, work_unit="bytes_per_launch"),
+    })
+    res["roofline"]["note"] = "cold calls: 640 distinct weight copies (826 MB) in rotation"
+    return res
+
+
+def measure_prefill(dev, steps, warmup, with_cpu):
     """Prefill step (routing, gate/up, down, combine) on the seed-2 4096-token layer."""
     import numpy as np
     import torch
@@ -86,98 +400,44 @@ def measure_prefill(dev, steps, warmup):
                          intermediate=INTER)
     ws = torch.empty(fn.workspace_bytes(PREFILL_TOKENS, TOP_K, EXPERTS), dtype=torch.uint8, device=dev)
     out = torch.empty((PREFILL_TOKENS, HIDDEN), dtype=torch.bfloat16, device=dev)
+    res = {"workload": "moe_prefill_q6k_e128_top8_h2048_i768_t4096_skew0.5_seed2"}
+    fn(*tabs, x, ids, w, workspace=ws, out=out)
+    got = out.float().cpu().numpy()
+    if not np.isfinite(got).all():
+        raise CheckFailed("prefill: nonfinite output rejected before timing")
+    if with_cpu:
+        rows = np.random.default_rng(7).choice(PREFILL_TOKENS, 128, replace=False)
+        rows.sort()
+        want, secs, n = cpu_oracle_moe(L, rows, ("Q6_K",) * 3, HIDDEN, INTER)
+        res["check"] = dict(check_close("prefill", got[rows], want), sample_tokens=int(rows.size))
+        flops = 2 * rows.size * TOP_K * 3 * HIDDEN * INTER
+        res["cpu_baseline"] = {"value": round(flops / secs / 1e12, 6), "unit": "TFLOP/s", "cores": n,
+                               "kind": "port", "tokens_per_s": round(rows.size / secs, 1),
+                               "sample": f"128 of the 4096 tokens (all their routes) by the NumPy oracle: "
+                                         f"{secs:.2f} s"}
     for _ in range(warmup):
         fn(*tabs, x, ids, w, workspace=ws, out=out)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(steps):
-        fn(*tabs, x, ids, w, workspace=ws, out=out)
-    b.record()
-    torch.cuda.synchronize()
-    step_us = a.elapsed_time(b) / steps * 1e3
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
-    for row in evs:
-        for ev in row:
-            ev.record()
-    torch.cuda.synchronize()
-    for i in range(steps):
-        fn(*tabs, x, ids, w, workspace=ws, out=out, events=evs[i])
-    torch.cuda.synchronize()
-    ph = np.array([[row[j].elapsed_time(row[j + 1]) for j in range(4)] for row in evs]).mean(0) * 1e3
-    gu_flops = PREFILL_FLOPS * 2 / 3
-    gu_tflops = gu_flops / (ph[1] * 1e-6) / 1e12
+    t = timed_reps({"fused": lambda i: fn(*tabs, x, ids, w, workspace=ws, out=out)}, inner=max(1, steps // 5))
+    step_us = t["fused"]["median"]
+    ph = phase_means(lambda i, ev: fn(*tabs, x, ids, w, workspace=ws, out=out, events=ev), steps)
     tflops = PREFILL_FLOPS / (step_us * 1e-6) / 1e12
-    return {
-        "workload": "moe_prefill_q6k_e128_top8_h2048_i768_t4096_skew0.5",
-        "value": round(tflops, 1),
-        "unit": "TFLOP/s",
-        "us_per_step": round(step_us, 1),
-        "mfma_fraction": round(tflops / MFMA_PEAK_TFLOPS, 4),
-        "flops_per_step": PREFILL_FLOPS,
+    res.update({
+        "value": round(tflops, 1), "unit": "TFLOP/s", "us_per_step": round(step_us, 1),
+        "tokens_per_s": round(PREFILL_TOKENS / (step_us * 1e-6), 1),
+        "mfma_fraction": round(tflops / MFMA_PEAK_TFLOPS, 4), "flops_per_step": PREFILL_FLOPS,
+        "step_us": t["fused"],
         "phases_us": {k: round(float(v), 1) for k, v in zip(("route", "gate_up", "down", "combine"), ph)},
-        "roofline": {
-            "kernel": "moe_pf_gate_up_kernel",
-            "bound": "mfma",
-            "achieved": round(gu_tflops, 1),
-            "peak": MFMA_PEAK_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(gu_tflops / MFMA_PEAK_TFLOPS, 4),
-            "traffic": TRAFFIC_BYTES["moe_pf_gate_up_kernel"],
-            "flops_per_launch": int(gu_flops),
-            "avg_launch_us": round(float(ph[1]), 1),
-        },
-    }
+        "roofline": roofline("q6moe::moe_pf_gate_up_kernel", "mfma", PREFILL_FLOPS * 2 / 3, ph[1],
+                             work_unit="flops_per_launch"),
+    })
+    return res
 
 
-def _time_calls(fn, calls, warmup=3):
-    """Mean device time (us) of ``calls`` back-to-back invocations of fn(i)."""
-    import torch
-
-    for i in range(warmup):
-        fn(i)
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for i in range(calls):
-        fn(i)
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) / calls * 1e3
-
-
-def measure_projection(dev):
-    """Single packed-Q6 projection, x bf16 [8, 2048] x W [2048 -> 768], seed 0, BF16 output.
-    Hot: the same 1.3 MB weights every call (us per call, cache-resident). Cold:
-    640 distinct weight copies (826 MB, over 3x the Infinity Cache) in rotation."""
-    import torch
-
-    from q6moe import pack_q6
-    from q6moe.kernel import q6_matmul
-    from q6moe.synth import projection
-
-    w = projection(seed=0)
-    packed = pack_q6(w["raw"], 2048)
-    data = torch.from_numpy(packed.data).to(dev)
-    scales = torch.from_numpy(packed.scales).to(dev)
-    x = torch.from_numpy(w["x"]).to(dev).to(torch.bfloat16)
-    hot = _time_calls(lambda i: q6_matmul(x, data, scales, output_features=768, out_dtype=torch.bfloat16), 200)
-    copies = 640
-    datas = data.repeat(copies, 1)
-    scaless = scales.repeat(copies, 1)
-    cold = _time_calls(lambda i: q6_matmul(x, datas[i % copies], scaless[i % copies], output_features=768,
-                                           out_dtype=torch.bfloat16), copies)
-    nbytes = 1_290_240 + 32_768 + 12_288
-    return {"workload": "q6_projection_x8x2048_w2048to768", "hot_us_per_call": round(hot, 2),
-            "cold_us_per_call": round(cold, 2), "cold_GBps": round(nbytes / (cold * 1e-6) / 1e9, 1),
-            "bytes_per_call": nbytes, "cold_copies": copies}
-
-
-def measure_q4_shared(dev):
+def measure_q4_shared(dev, with_cpu):
     """Q4_K decode with an always-on shared expert: 64 experts, top-6, H 4096, I 1024,
-    shared I 4096, N(0, 0.015), seed 3; tokens 1, 8, 64. The routed and shared weight tables
-    rotate over enough copies that the active bytes of one rotation exceed 3x the Infinity
-    Cache."""
+    shared I 4096, N(0, 0.015), seed 3; tokens 1, 8, 64 (the first rows of the
+    64-token layer). The routed and shared tables rotate over enough copies that
+    the active bytes of one rotation exceed 3x the Infinity Cache."""
     import numpy as np
     import torch
 
@@ -193,28 +453,58 @@ def measure_q4_shared(dev):
     base += [pack_experts(sh["gate"][None], "Q4_K", IS, H4, dev), pack_experts(sh["up"][None], "Q4_K", IS, H4, dev),
              pack_experts(sh["down"][None], "Q4_K", H4, IS, dev)]
     fn = expert_parallel(None, gate_type="Q4_K", up_type="Q4_K", down_type="Q4_K", hidden=H4, intermediate=I4)
-    per_expert, shared_bytes = 7_077_888, 28_311_552
-    out = {"workload": "moe_decode_q4k_e64_top6_h4096_i1024_shared4096", "batches": {}}
+    per_expert, shared_bytes, proj_bytes = 7_077_888, 28_311_552, 1024 * 16 * 144  # Q4_K [1024, 4096]
+    out = {"workload": "moe_decode_q4k_e64_top6_h4096_i1024_shared4096_seed3", "batches": {}}
+    shared_dec = None
+    if with_cpu:
+        from oracle.gguf import dequantize_rows
+        from oracle.packed_q6 import bf16_round
+
+        shared_dec = dict(gate=bf16_round(dequantize_rows(sh["gate"], "Q4_K", H4)),
+                          up=bf16_round(dequantize_rows(sh["up"], "Q4_K", H4)),
+                          down=bf16_round(dequantize_rows(sh["down"], "Q4_K", IS)))
     layers = [base]
     for b in (1, 8, 64):
         active = len(np.unique(L["ids"][:b]))
+        routes = int(np.count_nonzero(L["weights"][:b]))
         nbytes = active * per_expert + shared_bytes + 2 * b * H4 * 2
-        want = min(12, max(2, -(-3 * 256 * 2**20 // nbytes)))
-        while len(layers) < want:
-            layers.append([type(t)(t.qtype, t.data.clone(), None, t.rows, t.width) for t in base])
+        want_copies = copies_for(nbytes, hi=12)
+        while len(layers) < want_copies:
+            layers.append(clone_tables(base))
         x = torch.from_numpy(L["x"][:b]).to(dev).to(torch.bfloat16)
         ids = torch.from_numpy(L["ids"][:b]).to(dev)
         w = torch.from_numpy(L["weights"][:b]).to(dev).to(torch.bfloat16)
         ws = torch.empty(fn.workspace_bytes(b, K4, E4, IS), dtype=torch.uint8, device=dev)
         o = torch.empty((b, H4), dtype=torch.bfloat16, device=dev)
-        def call(i):
-            g, u, d, sg, su, sd = layers[i % want]
-            fn(g, u, d, x, ids, w, shared=dict(gate=sg, up=su, down=sd), workspace=ws, out=o)
 
-        us = _time_calls(call, 100)
-        out["batches"][str(b)] = {"us_per_step": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
-                                  "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                                  "active_experts": active, "bytes_per_step": nbytes, "layer_copies": want}
+        def call(i, events=None):
+            g, u, d, sg, su, sd = layers[i % want_copies]
+            fn(g, u, d, x, ids, w, shared=dict(gate=sg, up=su, down=sd), workspace=ws, out=o, events=events)
+
+        call(0)
+        row = {}
+        got = o.float().cpu().numpy()
+        if not np.isfinite(got).all():
+            raise CheckFailed(f"q4k_shared B={b}: nonfinite output rejected before timing")
+        if with_cpu:
+            want, secs, n = cpu_oracle_moe(L, slice(0, b), ("Q4_K",) * 3, H4, I4, shared=shared_dec)
+            row["check"] = check_close(f"q4k_shared B={b}", got, want)
+            row["cpu_baseline"] = {"value": round(nbytes / secs / 1e9, 4), "unit": "GB/s", "cores": n,
+                                   "kind": "port", "tokens_per_s": round(b / secs, 2),
+                                   "sample": f"the whole {b}-token step by the NumPy oracle: {secs:.2f} s"}
+        t = timed_reps({"fused": call}, inner=20)
+        us = t["fused"]["median"]
+        ph = phase_means(call, 50)
+        gu_bytes = active * 2 * proj_bytes + b * H4 * 2 + routes * I4 * 2  # gate+up, x, SwiGLU rows
+        row.update({"us_per_step": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                    "tokens_per_s": round(b / (us * 1e-6), 1),
+                    "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "step_us": t["fused"],
+                    "phases_us": {k: round(float(v), 2) for k, v in
+                                  zip(("shared", "routed_gate_up", "routed_down", "combine"), ph)},
+                    "active_experts": active, "bytes_per_step": nbytes, "layer_copies": want_copies,
+                    "roofline": roofline("q6moe::moe_dec_gate_up_kernel<1, true>", "hbm", gu_bytes, ph[1],
+                                         work_unit="bytes_per_launch")})
+        out["batches"][str(b)] = row
     return out
 
 
@@ -237,95 +527,121 @@ def measure_q8_down(dev):
     active = len(np.unique(L["ids"]))
     down_bytes = HIDDEN * (INTER // 32) * 34
     nbytes = active * (2 * Q6_PROJ_BYTES + down_bytes) + 2 * TOKENS * HIDDEN * 2 + TOKENS * TOP_K * 6
-    copies = max(2, -(-3 * 256 * 2**20 // nbytes))
-    layers = [base] + [[type(t)(t.qtype, t.data.clone(), None, t.rows, t.width) for t in base]
-                       for _ in range(copies - 1)]
+    copies = copies_for(nbytes)
+    layers = [base] + [clone_tables(base) for _ in range(copies - 1)]
     x = torch.from_numpy(L["x"]).to(dev).to(torch.bfloat16)
     ids = torch.from_numpy(L["ids"]).to(dev)
     w = torch.from_numpy(L["weights"]).to(dev).to(torch.bfloat16)
     ws = torch.empty(fn.workspace_bytes(TOKENS, TOP_K, EXPERTS), dtype=torch.uint8, device=dev)
     o = torch.empty((TOKENS, HIDDEN), dtype=torch.bfloat16, device=dev)
-    us = _time_calls(lambda i: fn(*layers[i % copies], x, ids, w, workspace=ws, out=o), 200)
+    fn(*base, x, ids, w, workspace=ws, out=o)
+    check_finite("q8_0_down", o)
+    t = timed_reps({"fused": lambda i: fn(*layers[i % copies], x, ids, w, workspace=ws, out=o)}, inner=20)
+    us = t["fused"]["median"]
     return {"workload": "moe_decode_q6k_gateup_q8_0_down_e128_top8_h2048_i768_b8", "us_per_step": round(us, 2),
-            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "active_experts": active,
-            "bytes_per_step": nbytes, "layer_copies": copies}
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "tokens_per_s": round(TOKENS / (us * 1e-6), 1),
+            "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "step_us": t["fused"],
+            "active_experts": active, "bytes_per_step": nbytes, "layer_copies": copies}
 
 
-def measure_kv_gather(dev):
-    """Paged INT8 KV gather + dequant of every cached token: batch 8, 4 KV heads x 128,
-    32768 tokens per sequence in pages of 256, FP32 per-token-per-head scales, seed 4.
-    One call reads K and V (codes, scales, page tables) and writes BF16 [8, 32768, 4, 128]
-    for each; three pool copies rotate so the 276 MB of codes are not cache-resident."""
+def measure_kv(dev, with_cpu):
+    """Paged INT8 KV gather + dequant of every cached token (batch 8, 4 KV heads x 128,
+    32768 tokens per sequence in pages of 256, FP32 per-token-per-head scales, seed 4):
+    one call reads K and V (codes, scales, page tables) and writes BF16
+    [8, 32768, 4, 128] for each; three pool copies rotate so the 276 MB of codes
+    are not cache-resident. Then the fused decode attention over the same cache
+    (32 query heads, all 32768 tokens attended)."""
+    import numpy as np
     import torch
 
-    from q6moe.attention_cache import read_paged
+    from q6moe.attention_cache import paged_decode_attention, read_paged
     from q6moe.synth import kv_pages
 
     K = kv_pages(seed=4)
-    P, H, D = K["page_size"], K["kv_heads"], K["head_dim"]
+    B, T, P, H, D = K["batch"], K["context"], K["page_size"], K["kv_heads"], K["head_dim"]
     table = torch.from_numpy(K["page_table"]).to(dev)
-    pools = []
-    for _ in range(3):
-        pools.append({n: torch.from_numpy(K[n]).to(dev) for n in ("k", "k_scale", "v", "v_scale")})
-    ok = torch.empty((8, K["context"], H, D), dtype=torch.bfloat16, device=dev)
+    pools = [{n: torch.from_numpy(K[n]).to(dev) for n in ("k", "k_scale", "v", "v_scale")} for _ in range(3)]
+    ok = torch.empty((B, T, H, D), dtype=torch.bfloat16, device=dev)
     ov = torch.empty_like(ok)
+    res = {"workload": "kv_paged_gather_b8_kvh4_d128_ctx32768_p256_f32scale_seed4"}
+    read_paged(pools[0]["k"], pools[0]["k_scale"], table, page_size=P, kv_heads=H, head_dim=D, out=ok)
+    check_finite("kv_gather", ok)
+    if with_cpu:
+        from concurrent.futures import ThreadPoolExecutor
+
+        from oracle import kv as oracle_kv
+        from oracle.packed_q6 import bf16_bits
+
+        n = cpu_threads()
+        chunks = np.array_split(np.arange(T), n)
+
+        def part(c):
+            idx = c[None, :].astype(np.int32)
+            return oracle_kv.read_paged(K["k"], K["k_scale"], K["page_table"][:1], P, H, D, D, idx)
+
+        t0 = time.perf_counter()
+        with ThreadPoolExecutor(n) as pool:
+            want = np.concatenate(list(pool.map(part, chunks)), axis=1)
+        secs = time.perf_counter() - t0
+        got = ok[:1].view(torch.int16).cpu().numpy().view(np.uint16)
+        if not np.array_equal(got, bf16_bits(want)):
+            raise CheckFailed("kv_gather: sequence 0 of K differs from the oracle")
+        res["check"] = {"passed": True, "bit_exact": "sequence 0 of K, all 32768 tokens"}
+        per_seq = 813_699_072 / B / 2
+        res["cpu_baseline"] = {"value": round(per_seq / secs / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
+                               "context_tokens_per_s": round(T / secs, 1),
+                               "sample": f"one sequence of K (32768 tokens) by the NumPy oracle, tokens split "
+                                         f"over {n} threads: {secs:.2f} s"}
 
     def call(i):
         p = pools[i % 3]
         read_paged(p["k"], p["k_scale"], table, page_size=P, kv_heads=H, head_dim=D, out=ok)
         read_paged(p["v"], p["v_scale"], table, page_size=P, kv_heads=H, head_dim=D, out=ov)
 
-    us = _time_calls(call, 30)
+    t = timed_reps({"fused": call}, inner=5)
+    us = t["fused"]["median"]
+    # one launch per read_paged: events around each K and V launch
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(61)]
+    torch.cuda.synchronize()
+    for i in range(30):
+        p = pools[i % 3]
+        evs[2 * i].record()
+        read_paged(p["k"], p["k_scale"], table, page_size=P, kv_heads=H, head_dim=D, out=ok)
+        evs[2 * i + 1].record()
+        read_paged(p["v"], p["v_scale"], table, page_size=P, kv_heads=H, head_dim=D, out=ov)
+    evs[60].record()
+    torch.cuda.synchronize()
+    launch_us = float(np.mean([evs[j].elapsed_time(evs[j + 1]) for j in range(60)]) * 1e3)
     nbytes = 813_699_072
-    return {"workload": "kv_paged_gather_b8_kvh4_d128_ctx32768_p256_f32scale", "us_per_call": round(us, 1),
-            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}
-
-
-def measure_kv_attention(dev):
-    """Fused decode attention over the same paged INT8 cache as the gather (batch 8, 32
-    query heads over 4 KV heads, head_dim 128, 32768 attended tokens per sequence, pages of
-    256, FP32 per-token-per-head scales, seed 4): the work of the gather plus the two
-    attention einsums, without the BF16 copy. Three pool copies rotate."""
-    import torch
-
-    from q6moe.attention_cache import paged_decode_attention
-    from q6moe.synth import kv_pages
-
-    K = kv_pages(seed=4)
-    P, H = K["page_size"], K["kv_heads"]
-    table = torch.from_numpy(K["page_table"]).to(dev)
-    pools = [{n: torch.from_numpy(K[n]).to(dev) for n in ("k", "k_scale", "v", "v_scale")} for _ in range(3)]
+    per_launch = B * T * H * D + B * T * H * 4 + B * (T // P) * 4 + B * T * H * D * 2
+    res.update({"us_per_call": round(us, 1), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                "context_tokens_per_s": round(B * T / (us * 1e-6), 1),
+                "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes,
+                "call_us": t["fused"],
+                "roofline": roofline("q6moe::kv_read_vec_kernel<unsigned int>", "hbm", per_launch, launch_us,
+                                     work_unit="bytes_per_launch")})
+    # fused decode attention over the same cache
     q = torch.from_numpy(K["q"]).to(dev).to(torch.bfloat16)
-    lengths = torch.full((K["batch"],), K["context"], dtype=torch.int32, device=dev)
-    o = torch.empty_like(q)
-    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    lengths = torch.full((B,), T, dtype=torch.int32, device=dev)
+    oq = torch.empty_like(q)
+    aws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
 
-    def call(i):
+    def attn(i):
         p = pools[i % 3]
         paged_decode_attention(q, p["k"], p["k_scale"], p["v"], p["v_scale"], table, lengths, page_size=P,
-                               kv_heads=H, workspace=ws, out=o)
+                               kv_heads=H, workspace=aws, out=oq)
 
-    us = _time_calls(call, 30)
-    nbytes = sum(pools[0][n].numel() * pools[0][n].element_size() for n in pools[0]) + table.numel() * 4 + \
+    attn(0)
+    check_finite("kv_attention", oq)
+    ta = timed_reps({"fused": attn}, inner=5)
+    aus = ta["fused"]["median"]
+    abytes = sum(pools[0][n].numel() * pools[0][n].element_size() for n in pools[0]) + table.numel() * 4 + \
         2 * q.numel() * 2
-    return {"workload": "kv_paged_decode_attention_b8_hq32_kvh4_d128_ctx32768_p256_f32scale",
-            "us_per_call": round(us, 1), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
-            "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}
-
-
-def cpu_baseline(L):
-    """The NumPy oracle (one thread) on one full decode step of the same workload."""
-    from threadpoolctl import threadpool_limits
-
-    from oracle import moe as oracle_moe
-
-    with threadpool_limits(1):
-        t0 = time.perf_counter()
-        oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"], L["ids"], L["weights"],
-                              types=("Q6_K",) * 3, hidden=HIDDEN, intermediate=INTER)
-        return time.perf_counter() - t0
+    attention = {"workload": "kv_paged_decode_attention_b8_hq32_kvh4_d128_ctx32768_p256_f32scale",
+                 "us_per_call": round(aus, 1), "GBps": round(abytes / (aus * 1e-6) / 1e9, 1),
+                 "hbm_fraction": round(abytes / (aus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": abytes,
+                 "call_us": ta["fused"]}
+    return res, attention
 
 
 def main():
@@ -334,10 +650,11 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=4)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the CPU oracle leg (and with it the oracle value checks; finiteness is still checked)")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
-                    help="skip the single-projection, Q4_K+shared and KV-gather measurements")
+                    help="skip the projection, Q4_K+shared, Q8_0-down and KV measurements")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="first copy a buffer of this many MiB device-to-device 5 times (a known-size "
                          "kernel for scaling hardware byte counters)")
@@ -350,13 +667,22 @@ def main():
     if not (1 <= args.steps <= 100000 and 0 <= args.warmup <= 10000 and 1 <= args.layers <= 16):
         log("steps must be 1..100000, warmup 0..10000, layers 1..16")
         return 2
+    try:
+        return run(args)
+    except CheckFailed as exc:
+        log(f"check failed: {exc}")
+        print(json.dumps({"metric": METRIC, "error": str(exc)}), flush=True)
+        return 1
 
+
+def run(args):
     import numpy as np
     import torch
 
     from q6moe.experts import expert_parallel, pack_experts
     from q6moe.synth import moe_layer
 
+    with_cpu = not args.no_cpu_baseline
     dev = torch.device("cuda", 0)
     if args.calib_copy_mb > 0:
         src = torch.ones(args.calib_copy_mb << 18, dtype=torch.float32, device=dev)
@@ -372,9 +698,7 @@ def main():
     log(f"  quantized {EXPERTS} experts in {time.perf_counter() - t0:.1f}s")
     base = [pack_experts(L[n], "Q6_K", INTER if n != "down" else HIDDEN, HIDDEN if n != "down" else INTER, dev)
             for n in ("gate", "up", "down")]
-    layers = [base]
-    for _ in range(args.layers - 1):
-        layers.append([type(t)(t.qtype, t.data.clone(), None, t.rows, t.width) for t in base])
+    layers = [base] + [clone_tables(base) for _ in range(args.layers - 1)]
     x = torch.from_numpy(L["x"]).to(dev).to(torch.bfloat16)
     ids = torch.from_numpy(L["ids"]).to(dev)
     w = torch.from_numpy(L["weights"]).to(dev).to(torch.bfloat16)
@@ -389,10 +713,28 @@ def main():
         g, u, d = layers[i % len(layers)]
         fn(g, u, d, x, ids, w, workspace=ws, out=out, events=events)
 
+    # correctness gate before any timing
+    step(0)
+    got = out.float().cpu().numpy()
+    if not np.isfinite(got).all():
+        raise CheckFailed("decode: nonfinite output rejected before timing")
+    baselines = MoeGemmBaselines(L, dev, "Q6_K", HIDDEN, INTER, TOKENS)
+    base_out = {"decode_then_bf16_gemm": baselines.decode_then_gemm(), "predecoded_bf16_gemm": baselines.predecoded()}
+    check = None
+    cpu = None
+    if with_cpu:
+        log("CPU oracle leg: one decode step ...")
+        want, secs, n = cpu_oracle_moe(L, slice(None), ("Q6_K",) * 3, HIDDEN, INTER, reps=3)
+        check = check_close("decode", got, want)
+        for name, o in base_out.items():
+            check[name] = check_close(f"decode {name}", o.float().cpu().numpy(), want, exact_frac=0.0)
+    else:
+        for name, o in base_out.items():
+            check_finite(name, o)
+
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-
     # Whole-step throughput: K back-to-back steps between two synchronisations.
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -405,22 +747,15 @@ def main():
     wall = time.perf_counter() - wall0
     gpu_ms = start.elapsed_time(end)
     ms_per_step = max(wall * 1e3, gpu_ms) / args.steps
-    nbytes = step_bytes(active, routes)
+    nbytes = active * 3 * Q6_PROJ_BYTES + 2 * TOKENS * HIDDEN * 2 + TOKENS * TOP_K * (4 + 2)
     value = nbytes / (ms_per_step * 1e-3) / 1e9
 
     # Per-kernel durations with HIP events recorded between the launches.
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
-    for row in evs:
-        for ev in row:
-            ev.record()
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        step(i, events=evs[i])
-    torch.cuda.synchronize()
-    phase = np.array([[row[j].elapsed_time(row[j + 1]) for j in range(4)] for row in evs]) * 1e3  # us
-    ph = phase.mean(0)
-    gu_bytes = gate_up_bytes(active, routes)
-    achieved = gu_bytes / (ph[1] * 1e-6) / 1e9
+    ph = phase_means(step, args.steps)
+    gu_bytes = active * 2 * Q6_PROJ_BYTES + TOKENS * HIDDEN * 2 + routes * INTER * 2
+    # Interleaved repetitions: the fused step against the decode-then-GEMM baselines.
+    reps = timed_reps({"fused": step, "decode_then_bf16_gemm": baselines.decode_then_gemm,
+                       "predecoded_bf16_gemm": baselines.predecoded}, inner=20)
 
     result = {
         "metric": METRIC,
@@ -436,44 +771,44 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) activations/logits, N(0,0.02) weights quantized to Q6_K)",
         "config": {
-            "workload": "moe_decode_q6k_e128_top8_h2048_i768_b8",
+            "workload": "moe_decode_q6k_e128_top8_h2048_i768_b8_seed1",
             "experts": EXPERTS, "top_k": TOP_K, "hidden": HIDDEN, "intermediate": INTER,
             "tokens": TOKENS, "seed": SEED, "active_experts": active, "layer_copies": args.layers,
             "bytes_per_step": nbytes,
         },
+        "tokens_per_s": round(TOKENS / (ms_per_step * 1e-3), 1),
         "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
+        "step_us": reps["fused"],
         "phases_us": {k: round(float(v), 2) for k, v in zip(("pre", "gate_up", "down", "combine"), ph)},
-        "roofline": {
-            "kernel": "moe_dec_gate_up_kernel",
-            "bound": "hbm",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": TRAFFIC_BYTES["moe_dec_gate_up_kernel"],
-            "bytes_per_launch": gu_bytes,
-            "avg_launch_us": round(float(ph[1]), 3),
-        },
+        "roofline": roofline("q6moe::moe_dec_gate_up_kernel<0, true>", "hbm", gu_bytes, ph[1],
+                             work_unit="bytes_per_launch"),
+        "baselines_us_per_step": {k: v for k, v in reps.items() if k != "fused"},
     }
+    if check is not None:
+        result["check"] = check
+    if with_cpu:
+        result["cpu_baseline"] = {
+            "value": round(nbytes / secs / 1e9, 4), "unit": "GB/s", "cores": n, "kind": "port",
+            "tokens_per_s": round(TOKENS / secs, 2),
+            "sample": f"one full decode step of the same workload ({active} active experts decoded, SwiGLU FFN, "
+                      f"combine) by the NumPy oracle with {n} threads, median of 3 runs: {secs:.3f} s",
+        }
+    configs = {}
     if not args.no_prefill:
         log("timing the prefill step (4096 tokens, seed 2) ...")
-        result["prefill"] = measure_prefill(dev, steps=10, warmup=2)
+        configs["prefill"] = measure_prefill(dev, steps=10, warmup=2, with_cpu=with_cpu)
     if not args.no_extras:
-        log("timing the single projection, the Q4_K + shared layer, the Q8_0-down layer, the KV gather and attention ...")
-        result["extras"] = {"projection": measure_projection(dev), "q4k_shared": measure_q4_shared(dev),
-                            "q8_0_down": measure_q8_down(dev), "kv_gather": measure_kv_gather(dev),
-                            "kv_attention": measure_kv_attention(dev)}
-    if not args.no_cpu_baseline:
-        log("timing the CPU oracle on one step (one thread) ...")
-        secs = cpu_baseline(L)
-        result["cpu_baseline"] = {
-            "value": round(nbytes / secs / 1e9, 4),
-            "unit": "GB/s",
-            "cores": 1,
-            "kind": "port",
-            "sample": f"one full decode step of the same workload ({active} active experts decoded, "
-                      f"SwiGLU FFN, combine) by the NumPy oracle: {secs:.2f} s",
-        }
+        log("timing the single projection ...")
+        configs["projection"] = measure_projection(dev, with_cpu)
+        log("timing the Q4_K + shared layer (seed 3) ...")
+        configs["q4k_shared"] = measure_q4_shared(dev, with_cpu)
+        log("timing the paged KV gather and the fused decode attention (seed 4) ...")
+        configs["kv_gather"], kv_attention = measure_kv(dev, with_cpu)
+        log("timing the Q6_K gate/up + Q8_0 down step ...")
+        result["extras"] = {"q8_0_down": measure_q8_down(dev), "kv_attention": kv_attention}
+    if "prefill" in configs:
+        result["prefill"] = configs["prefill"]
+    result["configs"] = configs
     print(json.dumps(result), flush=True)
     return 0
 

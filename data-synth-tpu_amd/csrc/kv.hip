@@ -193,9 +193,44 @@ __global__ void __launch_bounds__(256) kv_write_kernel(KvQuant q, KvWrite w, int
   kv_store_scale(w.scales, q.scale_bf16, idx, s);
 }
 
+// gather_scale_plane (kaggle/qwen38_tpu/attention_cache.py:46-68): plane
+// [B*G, T] (2- or 4-byte values, copied bitwise), indices [B, S] (negative adds
+// T, then clamp, as a JAX gather) -> out [B, S, G]. One thread per output.
+template <typename V>
+__global__ void __launch_bounds__(256)
+    kv_gather_scales_kernel(const V* __restrict__ plane, const int32_t* __restrict__ idx, int64_t sel,
+                            int64_t groups, int64_t time, int64_t n, V* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int64_t g = i % groups, bs = i / groups, b = bs / sel;
+  int64_t t = idx[bs];
+  if (t < 0) t += time;
+  t = t < 0 ? 0 : (t >= time ? time - 1 : t);
+  out[i] = plane[(b * groups + g) * time + t];
+}
+
 }  // namespace q6moe
 
 using namespace q6moe;
+
+extern "C" int q6moe_kv_gather_scales(const void* plane, int plane_dtype, const int32_t* indices, int64_t batch,
+                                      int64_t selected, int64_t groups, int64_t time, void* out, void* stream) {
+  Q6MOE_REQUIRE(plane && indices && out, "kv_gather_scales: null pointer");
+  Q6MOE_REQUIRE(plane_dtype == Q6MOE_BF16 || plane_dtype == Q6MOE_F32, "kv_gather_scales: plane must be BF16 or F32");
+  Q6MOE_REQUIRE(batch >= 1 && selected >= 0 && groups >= 1 && time >= 1, "kv_gather_scales: bad shape");
+  const int64_t n = batch * selected * groups;
+  if (n == 0) return Q6MOE_OK;
+  const dim3 grid((unsigned)cdiv(n, 256));
+  if (plane_dtype == Q6MOE_BF16)
+    hipLaunchKernelGGL(kv_gather_scales_kernel<uint16_t>, grid, dim3(256), 0, (hipStream_t)stream,
+                       reinterpret_cast<const uint16_t*>(plane), indices, selected, groups, time, n,
+                       reinterpret_cast<uint16_t*>(out));
+  else
+    hipLaunchKernelGGL(kv_gather_scales_kernel<float>, grid, dim3(256), 0, (hipStream_t)stream,
+                       reinterpret_cast<const float*>(plane), indices, selected, groups, time, n,
+                       reinterpret_cast<float*>(out));
+  return check_launch("kv_gather_scales_kernel");
+}
 
 extern "C" int q6moe_kv_quantize(const void* x, int x_dtype, int64_t rows, int64_t chans, int64_t group,
                                  int8_t* codes, void* scales, int scale_dtype, void* stream) {

@@ -143,6 +143,7 @@ SIGNATURES = {
     "q6moe_moe_forward": (_int, [ctypes.POINTER(MoeArgs), _vp]),
     "q6moe_moe_forward_noalloc": (_int, [ctypes.POINTER(MoeArgs), _vp]),
     "q6moe_kv_read": (_int, [ctypes.POINTER(KvArgs), _vp]),
+    "q6moe_kv_gather_scales": (_int, [_vp, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "q6moe_kv_quantize": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _vp]),
     "q6moe_kv_write": (_int, [ctypes.POINTER(KvWriteArgs), _vp]),
     "q6moe_attn_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),

@@ -11,8 +11,8 @@ Mirrors kaggle/qwen38_tpu/attention_cache.py:15-81:
 ``read_paged`` / ``write_paged`` are the paged generalisation (page tables
 per sequence, FP32 per-token-per-head scales). Reads run the HIP kernel
 ``q6moe_kv_read``; ``quantize`` runs ``q6moe_kv_quantize`` and the writes
-``q6moe_kv_write``. ``gather_scale_plane`` keeps the reference contract and
-error messages.
+``q6moe_kv_write``, ``gather_scale_plane`` runs ``q6moe_kv_gather_scales``
+with the reference contract and error messages.
 """
 
 import ctypes
@@ -182,6 +182,11 @@ def read_paged(pool, scales, page_table, *, page_size, kv_heads, head_dim, group
     sel = cap if idx is None else idx.shape[1]
     if out is None:
         out = torch.empty((batch, sel, kv_heads, head_dim), dtype=dtype, device=pool.device)
+    elif (not isinstance(out, torch.Tensor) or out.dtype not in (torch.bfloat16, torch.float32)
+          or tuple(out.shape) != (batch, sel, kv_heads, head_dim) or out.device != pool.device
+          or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous BF16 or FP32 [{batch}, {sel}, {kv_heads}, {head_dim}] tensor "
+                         f"on {pool.device}")
     pool, scales = pool.contiguous(), scales.contiguous()
     a = _lib.KvArgs()
     a.codes, a.scales = pool.data_ptr(), scales.data_ptr()
@@ -225,11 +230,17 @@ def paged_decode_attention(q, k_pool, k_scales, v_pool, v_scales, page_table, le
     pps = table.shape[1]
     lib = _lib.load()
     need = int(lib.q6moe_attn_workspace_size(batch, hq, kv_heads, pps, page_size))
-    if workspace is None or workspace.numel() < need:
+    if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
-    if out is None:
-        out = torch.empty_like(q)
+    elif (not isinstance(workspace, torch.Tensor) or workspace.dtype != torch.uint8 or workspace.device != q.device
+          or not workspace.is_contiguous() or workspace.numel() < need):
+        raise ValueError(f"workspace must be a contiguous uint8 tensor of at least {need} bytes on {q.device}")
     q = q.contiguous()
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.bfloat16, device=q.device)
+    elif (not isinstance(out, torch.Tensor) or out.dtype != torch.bfloat16 or tuple(out.shape) != tuple(q.shape)
+          or out.device != q.device or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous BF16 {list(q.shape)} tensor on {q.device}")
     k_pool, v_pool, k_scales, v_scales = (t.contiguous() for t in (k_pool, v_pool, k_scales, v_scales))
     a = _lib.AttnArgs()
     a.q, a.k_codes, a.v_codes = q.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr()
@@ -246,15 +257,23 @@ def paged_decode_attention(q, k_pool, k_scales, v_pool, v_scales, page_table, le
 
 
 def gather_scale_plane(plane, indices, groups, *, method="indexed"):
-    """[B*G, T] scale plane, [B, S] indices -> [B, S, G] (attention_cache.py:46-68)."""
+    """[B*G, T] scale plane, [B, S] indices -> [B, S, G] (attention_cache.py:46-68),
+    on the GPU (``q6moe_kv_gather_scales``). Both reference methods ("indexed",
+    "rowwise") give the same values: a negative index adds T, then the index is
+    clamped into [0, T)."""
     if indices.ndim != 2 or plane.ndim != 2 or plane.shape[0] != indices.shape[0] * groups:
         raise ValueError("Scale plane must be [batch * groups, time] for [batch, selected] indices")
     if method not in ("indexed", "rowwise"):
         raise ValueError("Scale gather method must be indexed or rowwise")
-    time = plane.shape[1]
-    t = indices.to(torch.int64)
-    t = torch.where(t < 0, t + time, t).clamp(0, time - 1)
-    batch = indices.shape[0]
-    rows = (torch.arange(batch, device=plane.device)[:, None] * groups
-            + torch.arange(groups, device=plane.device)[None, :])
-    return plane[rows[:, None, :], t[:, :, None].to(plane.device)]
+    if not isinstance(plane, torch.Tensor) or plane.device.type != "cuda":
+        raise ValueError("plane must be a GPU tensor")
+    batch, sel = indices.shape
+    plane = plane.contiguous()
+    idx = indices.to(device=plane.device, dtype=torch.int32).contiguous()
+    out = torch.empty((batch, sel, groups), dtype=plane.dtype, device=plane.device)
+    lib = _lib.load()
+    with torch.cuda.device(plane.device):
+        rc = lib.q6moe_kv_gather_scales(plane.data_ptr(), _dtype_code(plane.dtype), idx.data_ptr(), batch, sel,
+                                        groups, plane.shape[1], out.data_ptr(), _lib.stream_handle(plane.device))
+    _lib.check(rc, "kv_gather_scales")
+    return out

@@ -25,21 +25,31 @@ BLOCK_LAYOUTS = {
     "IQ4_NL": (32, 18),
 }
 DEVICE_TYPES = ("Q6_K", "Q4_K", "Q8_0")
-_GGML_TYPE_NAMES = {0: "F32", 1: "F16", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 30: "BF16"}
+# GGMLQuantizationType values of the named formats (GGUF file format)
+_GGML_IDS = {0: "F32", 1: "F16", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 30: "BF16"}
 
 
 def normalize_qtype(qtype):
-    if hasattr(qtype, "name"):
-        name = str(qtype.name).upper()
-    elif isinstance(qtype, str):
-        name = qtype.rsplit(".", 1)[-1].upper()
-    else:
+    """Canonical format name of ``qtype``: an enum member (by its ``name``), a
+    string such as "q6_k" or "GGMLQuantizationType.Q6_K" (the part after the
+    last dot, upper-cased), or a GGML type id. Accepts the spellings of
+    gguf_quant.py:42-54 and raises its ValueError for anything else."""
+    def bad():
+        return ValueError(f"unsupported GGUF quantization type: {qtype!r}")
+
+    name = getattr(qtype, "name", None)
+    if name is None and isinstance(qtype, str):
+        name = qtype.split(".")[-1]
+    if name is None:
         try:
-            name = _GGML_TYPE_NAMES[int(qtype)]
-        except (TypeError, ValueError, KeyError) as exc:
-            raise ValueError(f"unsupported GGUF quantization type: {qtype!r}") from exc
+            name = _GGML_IDS.get(int(qtype))
+        except (TypeError, ValueError):
+            name = None
+        if name is None:
+            raise bad()
+    name = str(name).upper()
     if name not in BLOCK_LAYOUTS:
-        raise ValueError(f"unsupported GGUF quantization type: {qtype!r}")
+        raise bad()
     return name
 
 

@@ -227,6 +227,15 @@ typedef struct q6moe_kv_args {
 int q6moe_kv_read(const q6moe_kv_args* args, void* stream);
 
 /*
+ * gather_scale_plane (kaggle/qwen38_tpu/attention_cache.py:46-68): the scale
+ * plane [B*G, T] (BF16 or F32, values copied bitwise) at token indices [B, S]
+ * (a negative index adds T, then the index is clamped into [0, T)) ->
+ * out [B, S, G] of the plane's dtype.
+ */
+int q6moe_kv_gather_scales(const void* plane, int plane_dtype, const int32_t* indices, int64_t batch,
+                           int64_t selected, int64_t groups, int64_t time, void* out, void* stream);
+
+/*
  * INT8 block quantisation of KV rows (quantize, kaggle/qwen38_tpu/attention_cache.py:15-23):
  * x [rows, chans] (BF16 or F32 values) in groups of ``group`` channels ->
  * codes int8 [rows, chans] and scales [rows, chans/group]. With a BF16 scale,

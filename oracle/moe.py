@@ -47,7 +47,7 @@ def expert_contribution(x, gate_w, up_w, down_w):
     return bf16_round(_mm(a, down_w))
 
 
-def expert_ffn(gate, up, down, x, ids, weights, *, types, hidden, intermediate, shared=None):
+def expert_ffn(gate, up, down, x, ids, weights, *, types, hidden, intermediate, shared=None, workers=1):
     """x BF16 values [B, hidden] -> BF16 values [B, hidden] as FP32.
 
     gate/up/down: raw GGUF tables indexable by expert, each expert
@@ -55,21 +55,32 @@ def expert_ffn(gate, up, down, x, ids, weights, *, types, hidden, intermediate, 
     expert (dict of decoded BF16 matrices gate/up/down, optional per-token
     BF16 ``gate_scale``). As in engine.py:199-203 with math.py:282-284 the
     shared output is RNE(y_shared * gate_scale) in BF16 and is added to the
-    BF16 routed sum: RNE(f32(routed) + f32(shared)).
+    BF16 routed sum: RNE(f32(routed) + f32(shared)). ``workers`` > 1 computes
+    the experts' contributions on a thread pool; they are still added in
+    ascending expert id, so the result does not depend on it.
     """
     gt, ut, dt = types
     x = bf16_round(x)
     experts = len(gate)
     r = route_weights(ids, weights, experts)
-    out = np.zeros((x.shape[0], hidden), np.float32)
-    for e in range(experts):
+    active = [e for e in range(experts) if np.any(r[:, e])]
+
+    def contribution(e):
         rows = np.nonzero(r[:, e])[0]
-        if rows.size == 0:
-            continue
         gw = decode_expert(gate, e, gt, intermediate, hidden)
         uw = decode_expert(up, e, ut, intermediate, hidden)
         dw = decode_expert(down, e, dt, hidden, intermediate)
-        y = expert_contribution(x[rows], gw, uw, dw)
+        return rows, expert_contribution(x[rows], gw, uw, dw)
+
+    if workers > 1 and len(active) > 1:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(workers) as pool:
+            parts = list(pool.map(contribution, active))
+    else:
+        parts = [contribution(e) for e in active]
+    out = np.zeros((x.shape[0], hidden), np.float32)
+    for e, (rows, y) in zip(active, parts):
         out[rows] = (out[rows] + y * r[rows, e][:, None]).astype(np.float32)
     routed = bf16_round(out)
     if shared is None:

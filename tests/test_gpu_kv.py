@@ -94,3 +94,33 @@ def test_kv_pages_workload_reduced_shape(device):
                          torch.from_numpy(W["page_table"]).to(device), page_size=256, kv_heads=4, head_dim=128)
         want = oracle_kv.read_paged(W[name], W[name + "_scale"], W["page_table"], 256, 4, 128, 128)
         np.testing.assert_array_equal(_bits(got), bf16_bits(want))
+
+
+def test_gather_scale_plane_bf16_and_f32_planes_on_device(device):
+    # q6moe_kv_gather_scales: values copied bitwise, JAX index rules
+    rng = np.random.default_rng(630)
+    idx = rng.integers(-70, 70, (3, 41)).astype(np.int32)
+    for dt in (torch.bfloat16, torch.float32):
+        plane = torch.from_numpy(rng.normal(size=(3 * 8, 64)).astype(np.float32)).to(dt)
+        got = gather_scale_plane(plane.to(device), torch.from_numpy(idx).to(device), 8)
+        assert got.dtype == dt and tuple(got.shape) == (3, 41, 8)
+        want = oracle_kv.gather_scale_plane(plane.float().numpy(), idx, 8)
+        np.testing.assert_array_equal(got.float().cpu().numpy(), want)
+
+
+def test_decode_attention_output_for_a_permuted_query(device):
+    # a dense but permuted q: the output keeps the logical [B, Hq, 128] order
+    from q6moe.attention_cache import paged_decode_attention
+    from q6moe.synth import kv_pages
+
+    W = kv_pages(seed=8, batch=2, context=512, q_heads=8)
+    args = [torch.from_numpy(W[n]).to(device) for n in ("k", "k_scale", "v", "v_scale", "page_table")]
+    lengths = torch.tensor([512, 300], dtype=torch.int32, device=device)
+    q = torch.from_numpy(W["q"]).to(device).to(torch.bfloat16)
+    qp = q.permute(1, 0, 2).contiguous().permute(1, 0, 2)  # same values, permuted strides
+    a = paged_decode_attention(q, *args[:2], *args[2:4], args[4], lengths, page_size=256, kv_heads=4)
+    b = paged_decode_attention(qp, *args[:2], *args[2:4], args[4], lengths, page_size=256, kv_heads=4)
+    np.testing.assert_array_equal(_bits(a), _bits(b))
+    with pytest.raises(ValueError, match="out must be"):
+        paged_decode_attention(q, *args[:2], *args[2:4], args[4], lengths, page_size=256, kv_heads=4,
+                               out=torch.empty((2, 8, 64), dtype=torch.bfloat16, device=device))
