@@ -197,15 +197,15 @@ def clone_tables(tabs):
 
 def cpu_oracle_moe(L, rows, types, hidden, inter, shared=None, reps=1):
     """CPU baseline leg: the NumPy oracle on ``rows`` tokens of L with
-    cpu_threads() threads (BLAS threads and a pool over experts); returns
-    (output, seconds per run, threads)."""
+    cpu_threads() threads (a pool over experts, one BLAS thread each);
+    returns (output, seconds per run, threads)."""
     from threadpoolctl import threadpool_limits
 
     from oracle import moe as oracle_moe
 
     n = cpu_threads()
     times, out = [], None
-    with threadpool_limits(n):
+    with threadpool_limits(1):
         for _ in range(reps):
             t0 = time.perf_counter()
             out = oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"][rows], L["ids"][rows],
