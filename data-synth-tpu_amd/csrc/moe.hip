@@ -440,10 +440,10 @@ __global__ void __launch_bounds__(512)
     }
     // All RPW units of a K block are loaded before the first is decoded (row
     // groups past the matrix are clamped to its last one and not used); with
-    // four token groups, Q8_0 units are loaded one at a time (registers).
+    // four token groups, Q8_0, Q5_1 and Q5_K units are loaded one at a time (registers).
     // With one token group, two K blocks per pass, all their units in flight
     // together (the second block clamped to the first when it does not exist).
-    constexpr int kPre = FMT == FMT_Q8 && NT > 1 ? 1 : RPW;
+    constexpr int kPre = (FMT == FMT_Q8 || FMT == FMT_Q51 || FMT == FMT_Q5K) && NT > 1 ? 1 : RPW;
     constexpr int kBat = NT == 1 ? 2 : 1;
     for (int kb0 = wave; kb0 < down.kb; kb0 += kBat * kw) {
       Unit<FMT> udb[kBat][kPre];
@@ -637,11 +637,31 @@ static Proj make_proj(const q6moe_table& t, int rows, int k) {
 
 // Bytes of one expert's unit-major table.
 static int64_t unit_table_bytes(int qtype, int64_t rows, int64_t k) {
-  return cdiv(rows, 16) * cdiv(k, kQK) * (qtype == Q6MOE_Q6_K ? kQ6Unit : qtype == Q6MOE_Q4_K ? kQ4Unit : kQ8Unit);
+  int unit = 0;
+  switch (qtype) {
+    case Q6MOE_Q6_K: unit = kQ6Unit; break;
+    case Q6MOE_Q5_K: unit = kQ5KUnit; break;
+    case Q6MOE_Q4_K: unit = kQ4Unit; break;
+    case Q6MOE_Q8_0: unit = kQ8Unit; break;
+    case Q6MOE_Q5_1: unit = kQ51Unit; break;
+  }
+  return cdiv(rows, 16) * cdiv(k, kQK) * unit;
 }
 
-static bool expert_qtype(int q) { return q == Q6MOE_Q6_K || q == Q6MOE_Q4_K || q == Q6MOE_Q8_0; }
-static int fmt_of(int q) { return q == Q6MOE_Q6_K ? FMT_Q6 : q == Q6MOE_Q4_K ? FMT_Q4K : FMT_Q8; }
+static bool expert_qtype(int q) {
+  return q == Q6MOE_Q6_K || q == Q6MOE_Q5_K || q == Q6MOE_Q4_K || q == Q6MOE_Q8_0 || q == Q6MOE_Q5_1;
+}
+static bool gate_up_qtype(int q) { return q == Q6MOE_Q6_K || q == Q6MOE_Q5_K || q == Q6MOE_Q4_K || q == Q6MOE_Q8_0; }
+static bool block32_qtype(int q) { return q == Q6MOE_Q8_0 || q == Q6MOE_Q5_1; }  // 32-value blocks
+static int fmt_of(int q) {
+  switch (q) {
+    case Q6MOE_Q6_K: return FMT_Q6;
+    case Q6MOE_Q5_K: return FMT_Q5K;
+    case Q6MOE_Q4_K: return FMT_Q4K;
+    case Q6MOE_Q5_1: return FMT_Q51;
+    default: return FMT_Q8;
+  }
+}
 
 static int validate_table(const q6moe_table& t, const char* name, int64_t rows, int64_t k, int64_t experts) {
   std::string n(name);
@@ -650,7 +670,7 @@ static int validate_table(const q6moe_table& t, const char* name, int64_t rows, 
     return Q6MOE_ERR_INVALID;
   }
   if (!expert_qtype(t.qtype)) {
-    set_error(n + ": qtype must be Q6_K, Q4_K or Q8_0");
+    set_error(n + ": qtype must be Q6_K, Q5_K, Q4_K, Q8_0 or Q5_1");
     return Q6MOE_ERR_UNSUPPORTED;
   }
   const int64_t need = unit_table_bytes(t.qtype, rows, k);
@@ -700,16 +720,20 @@ __device__ __forceinline__ uint32_t q6_code_at(const uint8_t* blk, int p) {
 // One 4-byte word of a unit-major table per thread. Q6_K units are
 // bit-planar (see q6p_decode): code word g of chunk c of lane l (row l % 16,
 // sub-block 4g + l / 16) at 1024c + 16l + 4g, the lane's four sub-scales at
-// 3072 + 4l, the rows' FP16 scales at 3328. Q4_K units are the rows' 144-byte
-// blocks in 16-byte chunks (chunk c of row j at 16 * (16c + j)). Q8_0 units
-// hold lane l's 16 codes of chunk g at 1024g + 16l and the rows' 8 block
-// scales at 4096. Rows (and Q8_0 blocks) past the projection's are zero.
-// rblocks: GGUF blocks per row in raw (K/256 for Q6_K and Q4_K, K/32 for Q8_0).
+// 3072 + 4l, the rows' FP16 scales at 3328. Q4_K (Q5_K) units are the rows'
+// 144-byte (176-byte) blocks in 16-byte chunks (chunk c of row j at
+// 16 * (16c + j)). Q8_0 units hold lane l's 16 codes of chunk g at 1024g + 16l
+// and the rows' 8 block scales at 4096. Q5_1 units hold the 16 nibble bytes of
+// row j's block 2g + h at 512g + 256h + 16j, then its high word, d and m at
+// 2048 + 64j + 32h + 8g. Rows (and Q8_0 / Q5_1 blocks) past the projection's
+// are zero. rblocks: GGUF blocks per row in raw (K/256 for the K-quants, K/32
+// for Q8_0 and Q5_1).
 template <int FMT>
 __global__ void __launch_bounds__(256) moe_pack_kernel(const uint8_t* __restrict__ raw, int64_t raw_stride, int rows,
                                                        int kbs, int rblocks, uint8_t* __restrict__ dst,
                                                        int64_t dst_stride, int64_t words) {
-  constexpr int U = UnitBytes<FMT>::value, BS = FMT == FMT_Q6 ? 210 : FMT == FMT_Q4K ? 144 : 34;
+  constexpr int U = UnitBytes<FMT>::value;
+  constexpr int BS = FMT == FMT_Q6 ? 210 : FMT == FMT_Q4K ? 144 : FMT == FMT_Q5K ? 176 : FMT == FMT_Q51 ? 24 : 34;
   const int64_t wi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (wi >= words) return;
   const int64_t e = blockIdx.y, o = wi * 4;
@@ -718,7 +742,27 @@ __global__ void __launch_bounds__(256) moe_pack_kernel(const uint8_t* __restrict
   const int rg = (int)(unit / kbs), kb = (int)(unit - (int64_t)rg * kbs);
   auto block = [&](int row) { return raw + e * raw_stride + ((int64_t)(rg * 16 + row) * rblocks + kb) * BS; };
   uint32_t v = 0;
-  if (FMT == FMT_Q8) {
+  if (FMT == FMT_Q51) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int b = ob + t;
+      int j, blk, src;  // row in the group, Q5_1 block in the row, byte in the block
+      if (b < 2048) {
+        j = (b >> 4) & 15;
+        blk = 8 * kb + 2 * (b >> 9) + ((b >> 8) & 1);
+        src = 8 + (b & 15);
+      } else {
+        const int a = b - 2048, k = a & 7;
+        j = a >> 6;
+        blk = 8 * kb + 2 * ((a >> 3) & 3) + ((a >> 5) & 1);
+        src = k < 4 ? 4 + k : k - 4;  // high word, then d, then m
+      }
+      const int row = rg * 16 + j;
+      const uint32_t byte =
+          row < rows && blk < rblocks ? raw[e * raw_stride + ((int64_t)row * rblocks + blk) * BS + src] : 0u;
+      v |= byte << (8 * t);
+    }
+  } else if (FMT == FMT_Q8) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int b = ob + t;
@@ -803,7 +847,7 @@ using namespace q6moe;
 
 extern "C" size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width) {
   if (!expert_qtype(qtype) || rows < 1 || width < 1 || rows > (1 << 24) || width > (1 << 24) ||
-      (qtype == Q6MOE_Q8_0 && width % 32))
+      (block32_qtype(qtype) && width % 32))
     return 0;
   return (size_t)unit_table_bytes(qtype, rows, width);
 }
@@ -811,8 +855,9 @@ extern "C" size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width) 
 extern "C" int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, int64_t rows, int64_t width,
                               uint8_t* dst, void* stream) {
   Q6MOE_REQUIRE(raw && dst, "moe_pack: null pointer");
-  Q6MOE_REQUIRE(expert_qtype(qtype), "moe_pack: qtype must be Q6_K, Q4_K or Q8_0");
-  Q6MOE_REQUIRE(qtype != Q6MOE_Q8_0 || width % 32 == 0, "moe_pack: Q8_0 rows must hold whole 32-value blocks");
+  Q6MOE_REQUIRE(expert_qtype(qtype), "moe_pack: qtype must be Q6_K, Q5_K, Q4_K, Q8_0 or Q5_1");
+  Q6MOE_REQUIRE(!block32_qtype(qtype) || width % 32 == 0,
+                "moe_pack: Q8_0 and Q5_1 rows must hold whole 32-value blocks");
   Q6MOE_REQUIRE(experts >= 1 && experts <= 65535 && rows >= 1 && width >= 1 && rows <= (1 << 24) &&
                     width <= (1 << 24),
                 "moe_pack: bad shape");
@@ -827,6 +872,12 @@ extern "C" int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, in
   else if (qtype == Q6MOE_Q4_K)
     hipLaunchKernelGGL(moe_pack_kernel<FMT_Q4K>, grid, dim3(256), 0, (hipStream_t)stream, raw, rows * kbs * 144,
                        (int)rows, kbs, kbs, dst, bytes, words);
+  else if (qtype == Q6MOE_Q5_K)
+    hipLaunchKernelGGL(moe_pack_kernel<FMT_Q5K>, grid, dim3(256), 0, (hipStream_t)stream, raw, rows * kbs * 176,
+                       (int)rows, kbs, kbs, dst, bytes, words);
+  else if (qtype == Q6MOE_Q5_1)
+    hipLaunchKernelGGL(moe_pack_kernel<FMT_Q51>, grid, dim3(256), 0, (hipStream_t)stream, raw,
+                       rows * (width / 32) * 24, (int)rows, kbs, (int)(width / 32), dst, bytes, words);
   else
     hipLaunchKernelGGL(moe_pack_kernel<FMT_Q8>, grid, dim3(256), 0, (hipStream_t)stream, raw,
                        rows * (width / 32) * 34, (int)rows, kbs, (int)(width / 32), dst, bytes, words);
@@ -836,9 +887,9 @@ extern "C" int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, in
 extern "C" int q6moe_moe_unpack(const uint8_t* table, int qtype, int64_t experts, int64_t rows, int64_t width,
                                 int64_t stride, int path, uint16_t* out, void* stream) {
   Q6MOE_REQUIRE(table && out, "moe_unpack: null pointer");
-  Q6MOE_REQUIRE(expert_qtype(qtype), "moe_unpack: qtype must be Q6_K, Q4_K or Q8_0");
+  Q6MOE_REQUIRE(expert_qtype(qtype), "moe_unpack: qtype must be Q6_K, Q5_K, Q4_K, Q8_0 or Q5_1");
   Q6MOE_REQUIRE(experts >= 1 && experts <= 65535 && rows >= 1 && width >= 1 && rows <= (1 << 24) &&
-                    width <= (1 << 24) && (qtype != Q6MOE_Q8_0 || width % 32 == 0),
+                    width <= (1 << 24) && (!block32_qtype(qtype) || width % 32 == 0),
                 "moe_unpack: bad shape");
   Q6MOE_REQUIRE(path >= 0 && path <= 2, "moe_unpack: path must be 0 (generic), 1 (decode) or 2 (prefill)");
   Q6MOE_REQUIRE(path != 2 || qtype == Q6MOE_Q6_K, "moe_unpack: the prefill path decodes Q6_K only");
@@ -860,6 +911,10 @@ extern "C" int q6moe_moe_unpack(const uint8_t* table, int qtype, int64_t experts
     hipLaunchKernelGGL(moe_unit_unpack_kernel<FMT_Q6>, grid, dim3(64), 0, s, p, out);
   } else if (fmt == FMT_Q4K) {
     hipLaunchKernelGGL(moe_unit_unpack_kernel<FMT_Q4K>, grid, dim3(64), 0, s, p, out);
+  } else if (fmt == FMT_Q5K) {
+    hipLaunchKernelGGL(moe_unit_unpack_kernel<FMT_Q5K>, grid, dim3(64), 0, s, p, out);
+  } else if (fmt == FMT_Q51) {
+    hipLaunchKernelGGL(moe_unit_unpack_kernel<FMT_Q51>, grid, dim3(64), 0, s, p, out);
   } else {
     hipLaunchKernelGGL(moe_unit_unpack_kernel<FMT_Q8>, grid, dim3(64), 0, s, p, out);
   }
@@ -933,9 +988,8 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   Q6MOE_REQUIRE(H % 8 == 0 && I % 8 == 0, "moe_forward: hidden and intermediate must be multiples of 8");
   Q6MOE_REQUIRE(aligned(a->x, 16) && aligned(a->out, 16) && aligned(workspace, 256),
                 "moe_forward: x/out need 16-byte and workspace 256-byte alignment");
-  Q6MOE_REQUIRE(a->gate.qtype == a->up.qtype && (a->gate.qtype == Q6MOE_Q6_K || a->gate.qtype == Q6MOE_Q4_K) &&
-                    (a->down.qtype == a->gate.qtype || a->down.qtype == Q6MOE_Q8_0),
-                "moe_forward: gate and up must share Q6_K or Q4_K; down must be that type or Q8_0");
+  Q6MOE_REQUIRE(a->gate.qtype == a->up.qtype && gate_up_qtype(a->gate.qtype) && expert_qtype(a->down.qtype),
+                "moe_forward: gate and up must share Q6_K, Q5_K, Q4_K or Q8_0; down must be one of those or Q5_1");
   Q6MOE_REQUIRE(a->mode >= 0 && a->mode <= 2, "moe_forward: mode must be 0, 1 or 2");
   int rc;
   if ((rc = validate_table(a->gate, "gate", I, H, E)) || (rc = validate_table(a->up, "up", I, H, E)) ||
@@ -1000,20 +1054,16 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
     sh_scale = g;
   }
   auto mark = [&](int i) {
-    if (a->events && a->events[i]) hipEventRecord((hipEvent_t)a->events[i], s);
+    if (a->events && a->events[i]) (void)hipEventRecord((hipEvent_t)a->events[i], s);
   };
   const int fmt = fmt_of(a->gate.qtype), fmt_dn = fmt_of(a->down.qtype);
   // Generic (non-tiled) expert phases for the call's formats.
   auto phases = [&](const Proj& pg, const Proj& pu, const Proj& pd, const TokenSrc& src, int grid_x, int max_tok,
                     int inter, uint16_t* act_out, uint16_t* y_out, auto mk) {
-    if (fmt == FMT_Q6 && fmt_dn == FMT_Q6)
-      launch_phases<FMT_Q6, FMT_Q6>(pg, pu, pd, src, grid_x, max_tok, a->x, (int)H, inter, act_out, y_out, s, mk);
-    else if (fmt == FMT_Q6)
-      launch_phases<FMT_Q6, FMT_Q8>(pg, pu, pd, src, grid_x, max_tok, a->x, (int)H, inter, act_out, y_out, s, mk);
-    else if (fmt_dn == FMT_Q4K)
-      launch_phases<FMT_Q4K, FMT_Q4K>(pg, pu, pd, src, grid_x, max_tok, a->x, (int)H, inter, act_out, y_out, s, mk);
-    else
-      launch_phases<FMT_Q4K, FMT_Q8>(pg, pu, pd, src, grid_x, max_tok, a->x, (int)H, inter, act_out, y_out, s, mk);
+    dispatch_formats(fmt, fmt_dn, [&](auto fg, auto fd) {
+      launch_phases<decltype(fg)::value, decltype(fd)::value>(pg, pu, pd, src, grid_x, max_tok, a->x, (int)H, inter,
+                                                              act_out, y_out, s, mk);
+    });
   };
   if (decode) {
     mark(0);
@@ -1094,8 +1144,10 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
                        tiled_down);
     if (!tiled_down) {
       const int kw2 = d.kb < 8 ? d.kb : 8;
-      hipLaunchKernelGGL((moe_down_kernel<FMT_Q8, 4, 2>), dim3(slots, (unsigned)cdiv(H, 16 * 2)), dim3(64 * kw2), 0,
-                         s, d, routed, ws.act, (int)I, ws.y, (int)H, kw2);
+      dispatch_format(fmt_dn, [&](auto fd) {
+        hipLaunchKernelGGL((moe_down_kernel<decltype(fd)::value, 4, 2>), dim3(slots, (unsigned)cdiv(H, 16 * 2)),
+                           dim3(64 * kw2), 0, s, d, routed, ws.act, (int)I, ws.y, (int)H, kw2);
+      });
     }
   } else {
     phases(g, u, d, routed, slots, max_tokens, (int)I, ws.act, ws.y, mark);

@@ -1,11 +1,13 @@
 // Shared definitions of the routed-expert kernels (decode and grouped GEMM).
 #pragma once
+#include <type_traits>
+
 #include "q6moe_api.h"
 #include "q6moe_device.h"
 
 namespace q6moe {
 
-enum { FMT_Q6 = 0, FMT_Q4K = 1, FMT_Q8 = 2 };
+enum { FMT_Q6 = 0, FMT_Q4K = 1, FMT_Q8 = 2, FMT_Q5K = 3, FMT_Q51 = 4 };
 
 // Expert tables of the routed-expert kernels are unit-major: a unit is 16
 // output rows x one 256-wide K block, stored exactly as a wave stages it in
@@ -24,11 +26,44 @@ enum { FMT_Q6 = 0, FMT_Q4K = 1, FMT_Q8 = 2 };
 //                        K positions 64g + 16jA + [0, 16), i.e. codes 16(jA%2) + [0, 16)
 //                        of its block 2g + jA/2
 //     d     [4096, 4352) FP16 scale of row j's block 2g + h at 4096 + 8(2j + h) + 2g
-// (GGUF block formats: kaggle/glm53_offload/gguf_quant.py:111-173). Rows past
-// the matrix are zero.
+//   Q5_K unit (2816 B): chunk c (0..10) of row j's 176-byte block at 16*(16c + j)
+//   Q5_1 unit (3072 B: 16 rows x 8 blocks of 24 B, rearranged):
+//     qs    [0, 2048)    the 16 nibble bytes of row j's block 2g + h at 512g + 256h + 16j
+//     aux   [2048, 3072) row j's block 2g + h: high-bit word, FP16 d, FP16 m at
+//                        2048 + 64j + 32h + 8g
+// (GGUF block formats: kaggle/glm53_offload/gguf_quant.py:111-173,
+// kaggle/qwen38_tpu/quant.py:15-55). Rows (and Q8_0 / Q5_1 blocks) past the
+// matrix are zero.
 constexpr int kQ6Unit = 3360;
 constexpr int kQ4Unit = 2304;
 constexpr int kQ8Unit = 4352;
+constexpr int kQ5KUnit = 2816;
+constexpr int kQ51Unit = 3072;
+
+// Calls f(std::integral_constant<int, FMT>) for the runtime format ``fmt``
+// (host-side dispatch to the kernels' template instantiations).
+template <typename F>
+inline void dispatch_format(int fmt, F&& f) {
+  switch (fmt) {
+    case FMT_Q6: f(std::integral_constant<int, FMT_Q6>{}); break;
+    case FMT_Q4K: f(std::integral_constant<int, FMT_Q4K>{}); break;
+    case FMT_Q8: f(std::integral_constant<int, FMT_Q8>{}); break;
+    case FMT_Q5K: f(std::integral_constant<int, FMT_Q5K>{}); break;
+    default: f(std::integral_constant<int, FMT_Q51>{}); break;
+  }
+}
+// Gate/up format (Q6_K, Q4_K, Q5_K or Q8_0) x down format (any).
+template <typename F>
+inline void dispatch_formats(int fg, int fd, F&& f) {
+  dispatch_format(fd, [&](auto d) {
+    switch (fg) {
+      case FMT_Q6: f(std::integral_constant<int, FMT_Q6>{}, d); break;
+      case FMT_Q4K: f(std::integral_constant<int, FMT_Q4K>{}, d); break;
+      case FMT_Q5K: f(std::integral_constant<int, FMT_Q5K>{}, d); break;
+      default: f(std::integral_constant<int, FMT_Q8>{}, d); break;
+    }
+  });
+}
 
 template <int FMT>
 struct UnitBytes;
@@ -43,6 +78,14 @@ struct UnitBytes<1> {
 template <>
 struct UnitBytes<2> {
   static constexpr int value = kQ8Unit;
+};
+template <>
+struct UnitBytes<3> {
+  static constexpr int value = kQ5KUnit;
+};
+template <>
+struct UnitBytes<4> {
+  static constexpr int value = kQ51Unit;
 };
 
 // One projection's expert table: [rows x k] per expert.
@@ -121,7 +164,7 @@ struct DecArgs {
 };
 
 bool dec_supported(int64_t B, int64_t K, int64_t E);
-int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s);  // fmt_dn: fmt_gu or FMT_Q8
+int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s);
 
 // Unit-decode probes (q6moe_moe_unpack): the decode kernels' LDS-staged path
 // and the prefill kernels' whole-block register path, for the bit-exact tests.
@@ -229,6 +272,107 @@ struct Unit<FMT_Q8> {
     d = *reinterpret_cast<const u32x2*>(u + 4096 + 8 * (2 * (lane & 15) + (lane >> 5)));
   }
   __device__ __forceinline__ void decode(u32x4 a[8], int) const { q8_decode(c, d, a); }
+  static __device__ __forceinline__ int xoff(int f, int jA) { return q6_xfrag_offset(f, jA); }
+};
+
+// The (K-)scale and min of sub-block jsub of a Q4_K / Q5_K header chunk
+// (d, dmin, 12 packed 6-bit scale/min bytes; gguf_quant.py:118-135):
+// ds = d * sc, dm = -(dmin * m), both exact.
+__device__ __forceinline__ void k_scale_min(const u32x4& hdr, int jsub, float& ds, float& dm) {
+  const float d = half_bits_to_float(hdr[0] & 0xffff);
+  const float dmin = half_bits_to_float(hdr[0] >> 16);
+  int sc, mn;
+  if (jsub < 4) {
+    sc = (hdr[1] >> (8 * jsub)) & 63;
+    mn = (hdr[2] >> (8 * jsub)) & 63;
+  } else {
+    const int jj = jsub - 4;
+    const uint32_t xb = (hdr[3] >> (8 * jj)) & 0xff;
+    sc = (int)((xb & 15) | (((hdr[1] >> (8 * jj)) >> 2) & 48));
+    mn = (int)((xb >> 4) | (((hdr[2] >> (8 * jj)) >> 2) & 48));
+  }
+  ds = d * (float)sc;
+  dm = -(dmin * (float)mn);
+}
+
+// Q5_K unit: as Q4_K, with the 32 high-bit bytes (chunks 1-2; bit s of byte l
+// is bit 4 of sub-block s at position l) before the nibbles (chunks 3-10).
+// Lane (row l%16, jA = l/16) decodes qs bytes [32jA, 32jA+32): low nibbles are
+// sub-block 2jA, high nibbles 2jA+1 (kaggle/glm53_offload/gguf_quant.py:137-157).
+// w = fma(q, d*sc, -dmin*m): one rounding of the exact value, then RNE to BF16.
+template <>
+struct Unit<FMT_Q5K> {
+  u32x4 hdr, qh0, qh1, qa, qb;
+  __device__ __forceinline__ void load(const Proj& p, int64_t e, int rgroup, int kb, int lane) {
+    const uint8_t* u = unit_ptr<FMT_Q5K>(p, e, rgroup, kb);
+    const int j = lane & 15, jA = lane >> 4;
+    hdr = ld16_stream(u + 16 * j);
+    qh0 = ld16_stream(u + 16 * (16 + j));
+    qh1 = ld16_stream(u + 16 * (32 + j));
+    qa = ld16_stream(u + 16 * (16 * (3 + 2 * jA) + j));
+    qb = ld16_stream(u + 16 * (16 * (4 + 2 * jA) + j));
+  }
+  __device__ __forceinline__ void decode(u32x4 a[8], int lane) const {
+    const int jA = lane >> 4;
+    float ds[2], dm[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) k_scale_min(hdr, 2 * jA + h, ds[h], dm[h]);
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      const int hn = f >> 2, bg = f & 3, s = 2 * jA + hn;
+      const u32x4& src = bg < 2 ? qa : qb;
+      const u32x4& qh = bg < 2 ? qh0 : qh1;
+      uint32_t c0 = src[2 * (bg & 1)], c1 = src[2 * (bg & 1) + 1];
+      c0 = (hn ? c0 >> 4 : c0) & 0x0f0f0f0fu;
+      c1 = (hn ? c1 >> 4 : c1) & 0x0f0f0f0fu;
+      c0 |= ((qh[2 * (bg & 1)] >> s) & 0x01010101u) << 4;
+      c1 |= ((qh[2 * (bg & 1) + 1] >> s) & 0x01010101u) << 4;
+      a[f] = q6_frag(c0, c1, ds[hn], dm[hn]);
+    }
+  }
+  static __device__ __forceinline__ int xoff(int f, int jA) { return Unit<FMT_Q4K>::xoff(f, jA); }
+};
+
+// Bits 0-3 of ``h`` moved to bit 0 of bytes 0-3 (h * (1 + 2^7 + 2^14 + 2^21)
+// places bit i at 8i; the shifted copies do not overlap, so nothing carries).
+__device__ __forceinline__ uint32_t spread4(uint32_t h) { return ((h & 15u) * 0x00204081u) & 0x01010101u; }
+
+// Q5_1 unit: lane (row j = l%16, jA = l/16) owns K positions 64g + 16jA + [0, 16)
+// (fragments 2g, 2g+1): positions 16(jA%2) + [0, 16) of its block 2g + jA/2,
+// i.e. the low (jA even) or high (jA odd) nibbles of the block's 16 bytes, with
+// bit 16(jA%2) + i of the high word as bit 4. w = fma(q, d, m), one rounding of
+// d*q + m (kaggle/qwen38_tpu/quant.py:34-53), then RNE to BF16.
+template <>
+struct Unit<FMT_Q51> {
+  u32x4 q[4];
+  u32x4 aux0, aux1;  // blocks 2g + jA/2 for g = 0, 1 and 2, 3: (high word, d | m << 16)
+  __device__ __forceinline__ void load(const Proj& p, int64_t e, int rgroup, int kb, int lane) {
+    const uint8_t* u = unit_ptr<FMT_Q51>(p, e, rgroup, kb);
+    const int j = lane & 15, hb = lane >> 5;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[g] = ld16_stream(u + 512 * g + 256 * hb + 16 * j);
+    aux0 = ld16_stream(u + 2048 + 64 * j + 32 * hb);
+    aux1 = ld16_stream(u + 2048 + 64 * j + 32 * hb + 16);
+  }
+  __device__ __forceinline__ void decode(u32x4 a[8], int lane) const {
+    const int odd = (lane >> 4) & 1;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const u32x4& ax = g < 2 ? aux0 : aux1;
+      const uint32_t qh = ax[2 * (g & 1)], dm = ax[2 * (g & 1) + 1];
+      const float d = half_bits_to_float(dm & 0xffff), m = half_bits_to_float(dm >> 16);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        uint32_t c0 = q[g][2 * e], c1 = q[g][2 * e + 1];
+        c0 = (odd ? c0 >> 4 : c0) & 0x0f0f0f0fu;
+        c1 = (odd ? c1 >> 4 : c1) & 0x0f0f0f0fu;
+        const uint32_t hb8 = qh >> (16 * odd + 8 * e);
+        c0 |= spread4(hb8) << 4;
+        c1 |= spread4(hb8 >> 4) << 4;
+        a[2 * g + e] = q6_frag(c0, c1, d, m);
+      }
+    }
+  }
   static __device__ __forceinline__ int xoff(int f, int jA) { return q6_xfrag_offset(f, jA); }
 };
 

@@ -42,7 +42,8 @@ constexpr int kDownRows = 4;  // 16-row groups of down per wave
 constexpr int kPassTokens = 16;  // routes per weight pass (MFMA columns)
 
 // One ring stage holds a unit as it lies in the table (Q6_K 3360 B, Q4_K
-// 2304 B, Q8_0 4352 B), the Q6_K FP16 scales repeated up to the stage's end.
+// 2304 B, Q5_K 2816 B, Q5_1 3072 B, Q8_0 4352 B), the Q6_K FP16 scales
+// repeated up to the stage's end.
 template <int FMT>
 constexpr int stage_bytes() { return FMT == FMT_Q8 ? 4352 : 3584; }
 constexpr int kXLoads = 8;   // token-operand loads per K block (one per MFMA)
@@ -201,6 +202,69 @@ struct WStream<FMT_Q8> {
     for (int g = 0; g < 4; ++g) c[g] = *reinterpret_cast<const u32x4*>(st + 1024 * g + 16 * lane);
     const u32x2 d = *reinterpret_cast<const u32x2*>(st + 4096 + 8 * (2 * (lane & 15) + (lane >> 5)));
     q8_decode(c, d, a);
+  }
+};
+
+template <>
+struct WStream<FMT_Q5K> {
+  static constexpr int kDma = 5;
+  const uint8_t* data;
+  int kbs;
+  uint32_t v16, v4;
+  __device__ __forceinline__ WStream(const Proj& p, int64_t e, int lane) {
+    data = p.data + e * p.dstride;
+    kbs = p.kb;
+    v16 = opaque(16 * lane);
+    v4 = opaque(4 * lane);
+  }
+  // unit: chunks 0-7 (2 KB) and chunks 8-10 (768 B), copied as they lie
+  __device__ __forceinline__ void issue(int rg, int kb, uint8_t* st) const {
+    const uint8_t* u = data + ((int64_t)rg * kbs + kb) * kQ5KUnit;
+    dma16(u, v16, st);
+    dma16(u + 1024, v16, st + 1024);
+    dma4(u + 2048, v4, st + 2048);
+    dma4(u + 2304, v4, st + 2304);
+    dma4(u + 2560, v4, st + 2560);
+  }
+  static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {
+    const int jj = lane & 15, jA = lane >> 4;
+    auto chunk = [&](int c) -> u32x4 { return *reinterpret_cast<const u32x4*>(st + 16 * (c * 16 + jj)); };
+    Unit<FMT_Q5K> u;
+    u.hdr = chunk(0);
+    u.qh0 = chunk(1);
+    u.qh1 = chunk(2);
+    u.qa = chunk(3 + 2 * jA);
+    u.qb = chunk(4 + 2 * jA);
+    u.decode(a, lane);
+  }
+};
+
+template <>
+struct WStream<FMT_Q51> {
+  static constexpr int kDma = 3;
+  const uint8_t* data;
+  int kbs;
+  uint32_t v16;
+  __device__ __forceinline__ WStream(const Proj& p, int64_t e, int lane) {
+    data = p.data + e * p.dstride;
+    kbs = p.kb;
+    v16 = opaque(16 * lane);
+  }
+  // unit: three 1 KB runs, copied as they lie
+  __device__ __forceinline__ void issue(int rg, int kb, uint8_t* st) const {
+    const uint8_t* u = data + ((int64_t)rg * kbs + kb) * kQ51Unit;
+    dma16(u, v16, st);
+    dma16(u + 1024, v16, st + 1024);
+    dma16(u + 2048, v16, st + 2048);
+  }
+  static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {
+    const int j = lane & 15, hb = lane >> 5;
+    Unit<FMT_Q51> u;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) u.q[g] = *reinterpret_cast<const u32x4*>(st + 512 * g + 256 * hb + 16 * j);
+    u.aux0 = *reinterpret_cast<const u32x4*>(st + 2048 + 64 * j + 32 * hb);
+    u.aux1 = *reinterpret_cast<const u32x4*>(st + 2048 + 64 * j + 32 * hb + 16);
+    u.decode(a, lane);
   }
 };
 
@@ -762,8 +826,10 @@ static int launch_k(const DecArgs& A, hipStream_t s) {
 }
 
 int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s) {
-  if (fmt_gu == FMT_Q6) return fmt_dn == FMT_Q8 ? launch_k<FMT_Q6, FMT_Q8>(A, s) : launch_k<FMT_Q6, FMT_Q6>(A, s);
-  return fmt_dn == FMT_Q8 ? launch_k<FMT_Q4K, FMT_Q8>(A, s) : launch_k<FMT_Q4K, FMT_Q4K>(A, s);
+  int rc = Q6MOE_OK;
+  dispatch_formats(fmt_gu, fmt_dn,
+                   [&](auto fg, auto fd) { rc = launch_k<decltype(fg)::value, decltype(fd)::value>(A, s); });
+  return rc;
 }
 
 // Unit-decode probe of this path: one wave per unit copies the unit into an
@@ -791,6 +857,10 @@ int launch_dec_unpack(int fmt, const Proj& p, int experts, uint16_t* out, hipStr
     hipLaunchKernelGGL(moe_dec_unpack_kernel<FMT_Q6>, grid, dim3(64), 0, s, p, out);
   else if (fmt == FMT_Q4K)
     hipLaunchKernelGGL(moe_dec_unpack_kernel<FMT_Q4K>, grid, dim3(64), 0, s, p, out);
+  else if (fmt == FMT_Q5K)
+    hipLaunchKernelGGL(moe_dec_unpack_kernel<FMT_Q5K>, grid, dim3(64), 0, s, p, out);
+  else if (fmt == FMT_Q51)
+    hipLaunchKernelGGL(moe_dec_unpack_kernel<FMT_Q51>, grid, dim3(64), 0, s, p, out);
   else
     hipLaunchKernelGGL(moe_dec_unpack_kernel<FMT_Q8>, grid, dim3(64), 0, s, p, out);
   return Q6MOE_OK;

@@ -224,7 +224,6 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
       asm volatile("" : "+v"(w.c0), "+v"(w.c1), "+v"(w.c2), "+v"(w.sc), "+v"(w.d));
     }
     const bool more = s + kAhead < S;
-    const int h = s & 1;
     const uint8_t* xs = smem + slot * kHalfBytes;
     u32x4 a[kUnits][4];
 #pragma unroll

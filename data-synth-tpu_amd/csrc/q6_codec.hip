@@ -1,11 +1,12 @@
-// Q6_K / Q4_K / Q8_0 decode kernels and the on-device GGUF -> SoA repack.
+// Q6_K / Q5_K / Q4_K / Q8_0 / Q5_1 decode kernels and the on-device GGUF -> SoA repack.
 //
 //  * q6_soa_decode_kernel  -- whole-matrix decode of the packed SoA planes to
 //    BF16 through the unit decoder the matmul kernels use, in its exact-sign
 //    form ds * (c - 32) (kaggle/packed_q6/kernel.py:44-62); the matmul form
 //    differs only in the sign of exact zeros.
 //  * gguf_decode_kernel    -- dequantize_rows for raw GGUF rows
-//    (kaggle/glm53_offload/gguf_quant.py:111-173).
+//    (kaggle/glm53_offload/gguf_quant.py:111-173; Q5_1 from
+//    kaggle/qwen38_tpu/quant.py:15-55).
 //  * q6_pack_kernel        -- pack_q6's byte permutation
 //    (kaggle/packed_q6/layout.py:71-89).
 #include "q6moe_api.h"
@@ -56,12 +57,31 @@ __device__ __forceinline__ float rd_half(const uint8_t* p) {
   return half_bits_to_float((uint32_t)p[0] | ((uint32_t)p[1] << 8));
 }
 
-// One thread per 16 values of a Q6_K/Q4_K block (16 threads per block) or per
-// 32-value Q8_0 block.
+// One thread per 16 values of a Q6_K/Q4_K/Q5_K block (16 threads per block) or
+// per 32-value Q8_0/Q5_1 block.
 __global__ void gguf_decode_kernel(const uint8_t* __restrict__ raw, int qtype, int64_t rows,
                                    int width, int blocks, int block_bytes, void* __restrict__ out,
                                    int bf16) {
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (qtype == Q6MOE_Q5_1) {
+    // d, m (FP16), 32 high bits, 16 bytes of nibbles: position i < 16 takes the
+    // low nibble of byte i, i >= 16 the high nibble of byte i - 16; bit i of
+    // the high word is bit 4. w = d * q + m (kaggle/qwen38_tpu/quant.py:34-53).
+    if (gid >= rows * blocks) return;
+    const int64_t row = gid / blocks;
+    const int b = (int)(gid % blocks);
+    const uint8_t* blk = raw + gid * block_bytes;
+    const float d = rd_half(blk), m = rd_half(blk + 2);
+    const uint32_t qh = (uint32_t)blk[4] | ((uint32_t)blk[5] << 8) | ((uint32_t)blk[6] << 16) |
+                        ((uint32_t)blk[7] << 24);
+    for (int i = 0; i < 32; ++i) {
+      const int nib = i < 16 ? (blk[8 + i] & 15) : (blk[8 + i - 16] >> 4);
+      const int q = nib | (int)(((qh >> i) & 1u) << 4);
+      const int col = b * 32 + i;
+      if (col < width) store_val(out, row * width + col, __builtin_fmaf((float)q, d, m), bf16);
+    }
+    return;
+  }
   if (qtype == Q6MOE_Q8_0) {
     if (gid >= rows * blocks) return;
     const int64_t row = gid / blocks;
@@ -92,8 +112,9 @@ __global__ void gguf_decode_kernel(const uint8_t* __restrict__ raw, int qtype, i
       const int col = b * kQK + p;
       if (col < width) store_val(out, row * width + col, ds * (float)code, bf16);
     }
-  } else {  // Q4_K: 8 sub-blocks of 32; thread handles half of one
+  } else {  // Q4_K / Q5_K: 8 sub-blocks of 32; thread handles half of one
     const float d = rd_half(blk), dmin = rd_half(blk + 2);
+    const bool q5 = qtype == Q6MOE_Q5_K;
     const int j = sub >> 1;  // sub-block 0..7
     int sc, mn;
     if (j < 4) {
@@ -104,10 +125,13 @@ __global__ void gguf_decode_kernel(const uint8_t* __restrict__ raw, int qtype, i
       mn = (blk[12 + j - 4] >> 4) | ((blk[8 + j - 4] >> 2) & 48);
     }
     const float a = d * (float)sc, m = dmin * (float)mn;
-    const uint8_t* qs = blk + 16 + (j >> 1) * 32;
+    // Q5_K: 32 high-bit bytes at 16 (bit j of byte l is bit 4 of sub-block j's
+    // position l), then the nibbles (kaggle/glm53_offload/gguf_quant.py:137-151)
+    const uint8_t* qs = blk + (q5 ? 48 : 16) + (j >> 1) * 32;
     for (int i = 0; i < 16; ++i) {
       const int l = (sub & 1) * 16 + i;
-      const int q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 15);
+      int q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 15);
+      if (q5) q |= ((blk[16 + l] >> j) & 1) << 4;
       const int col = b * kQK + j * 32 + l;
       if (col < width) store_val(out, row * width + col, __builtin_fmaf(a, (float)q, -m), bf16);
     }
@@ -181,12 +205,14 @@ extern "C" int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, in
     case Q6MOE_Q6_K: vals = 256; bytes = 210; break;
     case Q6MOE_Q4_K: vals = 256; bytes = 144; break;
     case Q6MOE_Q8_0: vals = 32; bytes = 34; break;
+    case Q6MOE_Q5_K: vals = 256; bytes = 176; break;
+    case Q6MOE_Q5_1: vals = 32; bytes = 24; break;
     default:
-      set_error("gguf_decode: unsupported GGUF quantization type (Q6_K, Q4_K, Q8_0 only)");
+      set_error("gguf_decode: unsupported GGUF quantization type (Q6_K, Q5_K, Q4_K, Q8_0, Q5_1 only)");
       return Q6MOE_ERR_UNSUPPORTED;
   }
   const int blocks = (int)cdiv(width, vals);
-  const int64_t threads = qtype == Q6MOE_Q8_0 ? rows * blocks : rows * blocks * 16;
+  const int64_t threads = vals == 32 ? rows * blocks : rows * blocks * 16;
   hipLaunchKernelGGL(gguf_decode_kernel, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0,
                      (hipStream_t)stream, raw, qtype, rows, (int)width, blocks, bytes, out,
                      out_dtype == Q6MOE_BF16);

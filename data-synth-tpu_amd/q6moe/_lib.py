@@ -12,10 +12,12 @@ LIB_PATH = Path(__file__).resolve().parent / "libq6moe.so"
 
 F32 = 0
 BF16 = 1
+Q5_1 = 7
 Q8_0 = 8
 Q4_K = 12
+Q5_K = 13
 Q6_K = 14
-QTYPE_CODES = {"Q8_0": Q8_0, "Q4_K": Q4_K, "Q6_K": Q6_K}
+QTYPE_CODES = {"Q5_1": Q5_1, "Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
 
 ERRORS = {-1: "invalid argument", -2: "HIP error", -3: "unsupported"}
 

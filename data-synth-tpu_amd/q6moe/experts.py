@@ -34,8 +34,8 @@ from . import _lib
 from .quant import BLOCK_LAYOUTS
 
 EXPERT_ROW_TILE = 128
-SUPPORTED = ("Q6_K", "Q4_K", "Q8_0")  # tables pack_experts takes
-GATE_UP_TYPES = ("Q6_K", "Q4_K")       # gate/up types the kernels run; down is that type or Q8_0
+SUPPORTED = ("Q6_K", "Q5_K", "Q4_K", "Q8_0", "Q5_1")  # tables pack_experts takes
+GATE_UP_TYPES = ("Q6_K", "Q5_K", "Q4_K", "Q8_0")       # gate/up types the kernels run; down: any of SUPPORTED
 
 
 @dataclass(frozen=True)
@@ -362,9 +362,9 @@ def expert_parallel(
         raise ValueError("Tensor parallel size must divide the device count")
     if intermediate % tensor_parallel or (intermediate // tensor_parallel) % BLOCK_LAYOUTS[down_type][0]:
         raise ValueError("Tensor slices must contain whole down quantization blocks")
-    if gate_type != up_type or gate_type not in GATE_UP_TYPES or down_type not in (gate_type, "Q8_0"):
+    if gate_type != up_type or gate_type not in GATE_UP_TYPES or down_type not in SUPPORTED:
         raise NotImplementedError(
-            f"this build runs Q6_K or Q4_K gate/up with down of the same type or Q8_0; got "
+            f"this build runs gate/up of one type in {GATE_UP_TYPES} with down in {SUPPORTED}; got "
             f"{gate_type}/{up_type}/{down_type}"
         )
     if compute == "int8_q8":

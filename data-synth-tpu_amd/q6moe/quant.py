@@ -1,8 +1,9 @@
 """GGUF row decoding on the GPU: ``block_layout`` and ``dequantize_rows``.
 
 Mirrors kaggle/glm53_offload/gguf_quant.py:57-60,180-216 (and the layout
-table of kaggle/qwen38_tpu/quant.py:7-8) with a ``backend="hip"`` decoder for
-the expert formats Q6_K, Q4_K and Q8_0. Output is FP32 or BF16 (RNE of the
+table and Q5_1 decoder of kaggle/qwen38_tpu/quant.py:7-55) with a
+``backend="hip"`` decoder for the expert formats Q6_K, Q5_K, Q4_K, Q8_0 and
+Q5_1. Output is FP32 or BF16 (RNE of the
 FP32 value, as ``astype(bfloat16)`` does).
 """
 
@@ -24,7 +25,7 @@ BLOCK_LAYOUTS = {
     "Q5_1": (32, 24),
     "IQ4_NL": (32, 18),
 }
-DEVICE_TYPES = ("Q6_K", "Q4_K", "Q8_0")
+DEVICE_TYPES = ("Q6_K", "Q5_K", "Q4_K", "Q8_0", "Q5_1")
 # GGMLQuantizationType values of the named formats (GGUF file format)
 _GGML_IDS = {0: "F32", 1: "F16", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 30: "BF16"}
 

@@ -17,6 +17,10 @@ bytes alone.
   s = (max w + m) / 15; d = fp16(max s / 63), dmin = fp16(max m / 63);
   6-bit sc = rint(s / d), mn = rint(m / dmin); codes
   clip(rint((w + dmin * mn) / (d * sc)), 0, 15).
+* ``quantize_q5_k``: as Q4_K with 31 levels, the code's bit 4 in the 32
+  high-bit bytes.
+* ``quantize_q5_1``: per 32 values m = min w, d = (max w - m) / 31 (FP16),
+  codes clip(rint((w - m) / d), 0, 31).
 * ``quantize_q8_0``: kaggle/qwen38_tpu/compute.py:41-49 (``pack_q8``).
 
 Rows whose width is not a multiple of the block size are zero-padded.
@@ -78,13 +82,14 @@ def quantize_q6_k(w):
     return out
 
 
-def _q4_rows(w):
+def _k_rows(w, levels):
+    """Q4_K (levels 15) / Q5_K (levels 31) scales, mins and codes of [rows, width]."""
     rows = w.shape[0]
     sub = w.reshape(rows, -1, 8, 32)
     lo = np.minimum(sub.min(-1), 0).astype(np.float32)
     hi = sub.max(-1).astype(np.float32)
     m = (-lo).astype(np.float32)
-    s = ((hi - lo) / np.float32(15)).astype(np.float32)
+    s = ((hi - lo) / np.float32(levels)).astype(np.float32)
     d16 = (s.max(-1) / np.float32(63)).astype(np.float16)
     dm16 = (m.max(-1) / np.float32(63)).astype(np.float16)
     d, dm = d16.astype(np.float32), dm16.astype(np.float32)
@@ -92,15 +97,33 @@ def _q4_rows(w):
     mn = np.clip(np.rint(_safe_div(m, dm[..., None])), 0, 63).astype(np.uint8)
     a = (d[..., None] * sc).astype(np.float32)
     b = (dm[..., None] * mn).astype(np.float32)
-    q = np.clip(np.rint(_safe_div(sub + b[..., None], a[..., None])), 0, 15).astype(np.uint8)
-    out = np.empty((rows, q.shape[1], 144), np.uint8)
-    out[..., 0:2] = d16.view(np.uint8).reshape(rows, -1, 2)
-    out[..., 2:4] = dm16.view(np.uint8).reshape(rows, -1, 2)
-    out[..., 4:8] = (sc[..., :4] & 63) | ((sc[..., 4:] >> 4) << 6)
-    out[..., 8:12] = (mn[..., :4] & 63) | ((mn[..., 4:] >> 4) << 6)
-    out[..., 12:16] = (sc[..., 4:] & 15) | ((mn[..., 4:] & 15) << 4)
-    out[..., 16:144] = (q[:, :, 0::2] | (q[:, :, 1::2] << 4)).reshape(rows, -1, 128)
-    return out
+    q = np.clip(np.rint(_safe_div(sub + b[..., None], a[..., None])), 0, levels).astype(np.uint8)
+    head = np.empty((rows, q.shape[1], 16), np.uint8)
+    head[..., 0:2] = d16.view(np.uint8).reshape(rows, -1, 2)
+    head[..., 2:4] = dm16.view(np.uint8).reshape(rows, -1, 2)
+    head[..., 4:8] = (sc[..., :4] & 63) | ((sc[..., 4:] >> 4) << 6)
+    head[..., 8:12] = (mn[..., :4] & 63) | ((mn[..., 4:] >> 4) << 6)
+    head[..., 12:16] = (sc[..., 4:] & 15) | ((mn[..., 4:] & 15) << 4)
+    return head, q
+
+
+def _nibbles(q):
+    """Codes [rows, nb, 8, 32] -> 128 bytes per block: chunk i holds sub-block 2i
+    in the low nibbles and 2i + 1 in the high nibbles (gguf_quant.py:137-141)."""
+    return ((q[:, :, 0::2] & 15) | ((q[:, :, 1::2] & 15) << 4)).reshape(q.shape[0], -1, 128)
+
+
+def _q4_rows(w):
+    head, q = _k_rows(w, 15)
+    return np.concatenate((head, _nibbles(q)), axis=-1)
+
+
+def _q5k_rows(w):
+    head, q = _k_rows(w, 31)
+    qh = np.zeros(q.shape[:2] + (32,), np.uint8)
+    for j in range(8):  # bit j of byte l: bit 4 of sub-block j's code l (gguf_quant.py:142-147)
+        qh |= ((q[:, :, j] >> 4) & 1) << j
+    return np.concatenate((head, qh, _nibbles(q)), axis=-1)
 
 
 def quantize_q4_k(w):
@@ -109,6 +132,38 @@ def quantize_q4_k(w):
     out = np.empty((rows, nb, 144), np.uint8)
     for r0 in range(0, rows, _CHUNK_ROWS):
         out[r0 : r0 + _CHUNK_ROWS] = _q4_rows(w[r0 : r0 + _CHUNK_ROWS])
+    return out
+
+
+def quantize_q5_k(w):
+    """FP32 [rows, width] -> GGUF Q5_K bytes [rows, ceil(width/256), 176]."""
+    w, rows, nb = _blocks(w, 256)
+    out = np.empty((rows, nb, 176), np.uint8)
+    for r0 in range(0, rows, _CHUNK_ROWS):
+        out[r0 : r0 + _CHUNK_ROWS] = _q5k_rows(w[r0 : r0 + _CHUNK_ROWS])
+    return out
+
+
+def quantize_q5_1(w):
+    """FP32 [rows, width] -> GGUF Q5_1 bytes [rows, width/32, 24]: per 32 values
+    m = fp16(min), d = fp16((max - min) / 31), codes clip(rint((w - m) / d), 0, 31);
+    bytes d, m, the 32 high bits, then byte i = code i | code i+16 << 4
+    (the layout kaggle/qwen38_tpu/quant.py:34-53 decodes)."""
+    w, rows, nb = _blocks(w, 32)
+    g = w.reshape(rows, nb, 32)
+    m16 = g.min(-1).astype(np.float16)
+    d16 = ((g.max(-1) - m16.astype(np.float32)) / np.float32(31)).astype(np.float16)
+    d, m = d16.astype(np.float32), m16.astype(np.float32)
+    q = np.clip(np.rint(_safe_div(g - m[..., None], np.broadcast_to(d[..., None], g.shape))), 0, 31)
+    q = q.astype(np.uint32)
+    qh = np.zeros((rows, nb), np.uint32)
+    for i in range(32):
+        qh |= ((q[..., i] >> 4) & 1) << i
+    out = np.empty((rows, nb, 24), np.uint8)
+    out[..., 0:2] = d16.view(np.uint8).reshape(rows, nb, 2)
+    out[..., 2:4] = m16.view(np.uint8).reshape(rows, nb, 2)
+    out[..., 4:8] = qh.astype("<u4").view(np.uint8).reshape(rows, nb, 4)
+    out[..., 8:24] = ((q[..., :16] & 15) | ((q[..., 16:] & 15) << 4)).astype(np.uint8)
     return out
 
 
@@ -123,4 +178,5 @@ def quantize_q8_0(w):
     )
 
 
-QUANTIZERS = {"Q6_K": quantize_q6_k, "Q4_K": quantize_q4_k, "Q8_0": quantize_q8_0}
+QUANTIZERS = {"Q6_K": quantize_q6_k, "Q5_K": quantize_q5_k, "Q4_K": quantize_q4_k, "Q8_0": quantize_q8_0,
+              "Q5_1": quantize_q5_1}

@@ -398,3 +398,20 @@ def test_out_and_workspace_are_validated(device):
             fn(*tabs, x, ids, w, out=bad)
     with pytest.raises(ValueError, match="workspace holds"):
         fn(*tabs, x, ids, w, workspace=torch.empty(16, dtype=torch.uint8, device=device))
+
+
+@pytest.mark.parametrize("qtype,down,tokens,mode", [
+    ("Q4_K", "Q5_1", 8, 1), ("Q4_K", "Q5_1", 100, 2), ("Q5_K", "Q8_0", 8, 1), ("Q5_K", "Q8_0", 100, 2),
+    ("Q8_0", "Q8_0", 8, 1), ("Q8_0", "Q8_0", 100, 2), ("Q6_K", "Q5_1", 20, 1), ("Q6_K", "Q5_1", 300, 0),
+    ("Q5_K", "Q5_K", 33, 1)])
+def test_checkpoint_format_mixes_match_oracle(device, qtype, down, tokens, mode):
+    # The real checkpoints' layer mixes (kaggle/qwen38_tpu/checkpoints/q4.json, q6.json,
+    # q8.json): Q4_K gate/up with Q5_1 down (43 of 48 Q4 layers), Q5_K gate/up with
+    # Q8_0 down, all-Q8_0 layers; plus Q6_K with Q5_1 down and an all-Q5_K layer,
+    # through the decode kernels (mode 1) and the grouped path (mode 2 / 0).
+    L = moe_layer(seed=71 + tokens, experts=8, top_k=3, hidden=512, intermediate=256, tokens=tokens,
+                  qtype=qtype, down_qtype=down, sigma=0.02, shared_intermediate=512 if mode == 1 else 0,
+                  pack=False)
+    sh = L.get("shared")
+    got, _ = _run(L, device, mode=mode, shared=sh)
+    assert_moe_close(got, _oracle(L, shared=sh))

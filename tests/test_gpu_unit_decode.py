@@ -26,7 +26,7 @@ pytestmark = pytest.mark.gpu
 # FP16 scale bits: normal values across the range, subnormals, signed zeros
 _SCALE_BITS = np.array([0x0000, 0x8000, 0x0001, 0x83FF, 0x0400, 0x1C00, 0x2E66, 0xAE66, 0x3C00, 0xBC00,
                         0x2400, 0x1400, 0x5640, 0xD640, 0x7BFF, 0xFBFF], np.uint16)
-_SCALE_FIELDS = {"Q6_K": (208,), "Q4_K": (0, 2), "Q8_0": (0,)}
+_SCALE_FIELDS = {"Q6_K": (208,), "Q5_K": (0, 2), "Q4_K": (0, 2), "Q8_0": (0,), "Q5_1": (0, 2)}
 
 
 def _random_table(qtype, experts, rows, width, seed):
@@ -53,7 +53,7 @@ def _check(got_bf16, want):
     np.testing.assert_array_equal(gb, wb)
 
 
-@pytest.mark.parametrize("qtype", ["Q6_K", "Q4_K", "Q8_0"])
+@pytest.mark.parametrize("qtype", ["Q6_K", "Q5_K", "Q4_K", "Q8_0", "Q5_1"])
 @pytest.mark.parametrize("path", ["generic", "decode"])
 @pytest.mark.parametrize("rows,width", [(16, 256), (40, 512), (33, 768)])
 def test_unit_decoders_are_bit_exact(device, qtype, path, rows, width):
@@ -69,10 +69,11 @@ def test_prefill_unit_decoder_is_bit_exact(device, rows, width):
     _check(unpack_experts(table, "prefill"), _want(raw, "Q6_K", rows, width))
 
 
-@pytest.mark.parametrize("qtype,down", [("Q6_K", "Q6_K"), ("Q4_K", "Q4_K"), ("Q6_K", "Q8_0")])
+@pytest.mark.parametrize("qtype,down", [("Q6_K", "Q6_K"), ("Q4_K", "Q4_K"), ("Q6_K", "Q8_0"), ("Q4_K", "Q5_1"),
+                                        ("Q5_K", "Q8_0")])
 def test_workload_expert_tables_decode_bit_exact(device, qtype, down):
     # Quantized N(0, 0.02) experts of the headline layer shapes (gate [768, 2048],
-    # down [2048, 768]) and the Q4_K layer (gate [1024, 4096], down [4096, 1024]).
+    # down [2048, 768]) and the Q4 layer shapes (gate [1024, 4096], down [4096, 1024]).
     H, I = (2048, 768) if qtype == "Q6_K" else (4096, 1024)
     rng = np.random.default_rng(5)
     for rows, width, q in ((I, H, qtype), (H, I, down)):

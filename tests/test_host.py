@@ -9,7 +9,7 @@ import pytest
 
 from oracle import gguf, packed_q6
 from q6moe import _lib, layout, pack_q6, unpack_q6
-from q6moe.quantize import quantize_q4_k, quantize_q6_k, quantize_q8_0
+from q6moe.quantize import quantize_q4_k, quantize_q5_1, quantize_q5_k, quantize_q6_k, quantize_q8_0
 
 from .conftest import ROOT
 
@@ -84,7 +84,8 @@ def test_q6_matmul_contract_rejected_before_any_device_work():
 
 @pytest.mark.parametrize(
     "qtype,fn,bound",
-    [("Q6_K", quantize_q6_k, 0.03), ("Q4_K", quantize_q4_k, 0.12), ("Q8_0", quantize_q8_0, 0.01)],
+    [("Q6_K", quantize_q6_k, 0.03), ("Q5_K", quantize_q5_k, 0.06), ("Q4_K", quantize_q4_k, 0.12),
+     ("Q8_0", quantize_q8_0, 0.01), ("Q5_1", quantize_q5_1, 0.06)],
 )
 def test_quantizers_round_trip_within_format_error(qtype, fn, bound):
     rng = np.random.default_rng(1)
