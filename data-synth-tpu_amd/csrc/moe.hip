@@ -576,7 +576,7 @@ __global__ void __launch_bounds__(64)
 // ---------------------------------------------------------------------------
 struct WsLayout {
   size_t hdr, active, act_off, tile, ent_r, route_tok, route_w, tok_pos, act,
-      y, sh_act, sh_y, sh_gate, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, chunk_cnt, total;
+      y, sh_act, sh_y, sh_gate, xq, xq_s, aq, aq_s, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, chunk_cnt, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -618,6 +618,11 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
     L.tok_pos = take(4 * n);
     L.y = take(2 * n * H);
     L.chunk_cnt = take(4 * (cdiv(B, kChunk) + 1) * E);
+    // the int8_q8 policy's quantised x and SwiGLU activations (codes, FP32 scales)
+    L.xq = take(B * H);
+    L.xq_s = take(4 * B * (H / 32));
+    L.aq = take(n * I);
+    L.aq_s = take(4 * n * (I / 32));
   }
   L.total = o;
   return L;
@@ -683,26 +688,195 @@ static int validate_table(const q6moe_table& t, const char* name, int64_t rows, 
 }
 
 // FG: gate/up table format, FD: down table format.
+template <int FG>
+static void launch_gate_up(const Proj& g, const Proj& u, const TokenSrc& src, int grid_x, int max_tokens,
+                           const uint16_t* x, int H, int I, uint16_t* act, hipStream_t s) {
+  const int kw1 = g.kb < 8 ? g.kb : 8;
+  const unsigned rb1 = (unsigned)cdiv(I, 16);
+  if (max_tokens <= 16)
+    hipLaunchKernelGGL((moe_gate_up_kernel<FG, 1, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
+                       H, act, I, kw1);
+  else
+    hipLaunchKernelGGL((moe_gate_up_kernel<FG, 4, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
+                       H, act, I, kw1);
+}
+
+template <int FD>
+static void launch_down(const Proj& d, const TokenSrc& src, int grid_x, int max_tokens, const uint16_t* act,
+                        int H, int I, uint16_t* y, hipStream_t s) {
+  const int kw2 = d.kb < 8 ? d.kb : 8;
+  if (max_tokens <= 16)  // one token group: one row group per workgroup (twice the workgroups)
+    hipLaunchKernelGGL((moe_down_kernel<FD, 1, 1>), dim3(grid_x, (unsigned)cdiv(H, 16)), dim3(64 * kw2), 0, s, d,
+                       src, act, I, y, H, kw2);
+  else
+    hipLaunchKernelGGL((moe_down_kernel<FD, 4, 2>), dim3(grid_x, (unsigned)cdiv(H, 16 * 2)), dim3(64 * kw2), 0, s,
+                       d, src, act, I, y, H, kw2);
+}
+
 template <int FG, int FD, typename Mark>
 static void launch_phases(const Proj& g, const Proj& u, const Proj& d, const TokenSrc& src, int grid_x,
                           int max_tokens, const uint16_t* x, int H, int I, uint16_t* act, uint16_t* y,
                           hipStream_t s, Mark mark) {
-  const int kw1 = g.kb < 8 ? g.kb : 8;
-  const int kw2 = d.kb < 8 ? d.kb : 8;
-  const unsigned rb1 = (unsigned)cdiv(I, 16), rb2 = (unsigned)cdiv(H, 16 * 2);
-  if (max_tokens <= 16) {  // one token group: one row group per down workgroup (twice the workgroups)
-    hipLaunchKernelGGL((moe_gate_up_kernel<FG, 1, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
-                       H, act, I, kw1);
-    mark(2);
-    hipLaunchKernelGGL((moe_down_kernel<FD, 1, 1>), dim3(grid_x, (unsigned)cdiv(H, 16)), dim3(64 * kw2), 0, s, d,
-                       src, act, I, y, H, kw2);
-  } else {
-    hipLaunchKernelGGL((moe_gate_up_kernel<FG, 4, 1>), dim3(grid_x, rb1), dim3(64 * kw1), 0, s, g, u, src, x,
-                       H, act, I, kw1);
-    mark(2);
-    hipLaunchKernelGGL((moe_down_kernel<FD, 4, 2>), dim3(grid_x, rb2), dim3(64 * kw2), 0, s, d, src, act, I, y,
-                       H, kw2);
+  launch_gate_up<FG>(g, u, src, grid_x, max_tokens, x, H, I, act, s);
+  mark(2);
+  launch_down<FD>(d, src, grid_x, max_tokens, act, H, I, y, s);
+}
+
+// ---------------------------------------------------------------------------
+// W8A8 policy for Q8_0 tables: kaggle/qwen38_tpu/compute.py:20-34 (q8_matmul).
+// The activations are quantised per row and 32-value group -- scale
+// s = max|x| / 127 in FP32, codes clip(rint(x / (s ? s : 1)), -127, 127) --
+// and each group's INT8 x INT8 dot products (INT32, exact) are scaled as
+// (f32(partial) * s) * d_weight and summed over the groups in FP32; the sum is
+// rounded to BF16.
+// ---------------------------------------------------------------------------
+
+// One thread per (row, group): 32 BF16 values -> 32 codes and the FP32 scale.
+// ``row_count`` (device, may be NULL) bounds the rows that hold data.
+__global__ void __launch_bounds__(256)
+    moe_act_q8_kernel(const uint16_t* __restrict__ src, int64_t groups_total, int groups_per_row,
+                      const int* __restrict__ row_count, int8_t* __restrict__ codes, float* __restrict__ scales) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= groups_total || (row_count && gid / groups_per_row >= *row_count)) return;
+  const u32x4* p = reinterpret_cast<const u32x4*>(src + gid * 32);  // rows are whole groups
+  u32x4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = p[i];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(bf16_to_float((uint16_t)(v[i >> 3][(i >> 1) & 3] >> (16 * (i & 1))))));
+  const float sc = m / 127.f;
+  const float div = sc == 0.f ? 1.f : sc;
+  uint32_t w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float x = bf16_to_float((uint16_t)(v[i >> 3][(i >> 1) & 3] >> (16 * (i & 1))));
+    const float q = fminf(fmaxf(__builtin_rintf(x / div), -127.f), 127.f);
+    w[i >> 2] |= ((uint32_t)(int32_t)q & 0xffu) << (8 * (i & 3));
   }
+  u32x4* o = reinterpret_cast<u32x4*>(codes + gid * 32);
+  o[0] = u32x4{w[0], w[1], w[2], w[3]};
+  o[1] = u32x4{w[4], w[5], w[6], w[7]};
+  scales[gid] = sc;
+}
+
+// Quantised activations: codes [rows, k] and scales [rows, k / 32].
+struct W8Src {
+  const int8_t* codes;
+  const float* scales;
+  int k;
+};
+
+__device__ __forceinline__ i32x4 mfma_i8(uint64_t a, uint64_t b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, c, 0, 0, 0);
+}
+
+// W8A8 projection(s) of a slot's tokens over Q8_0 unit-major tables, on the
+// INT8 matrix cores (v_mfma_i32_16x16x32_i8: one MFMA per 32-value group).
+// PAIR: gate p0 and up p1 with the SwiGLU epilogue a = RNE(RNE(g*sig(g)) * u)
+// into out [routes, rows]; otherwise one projection y = RNE(acc) into
+// out [routes or tokens, rows]. Activation row of token q of the slot: q
+// (dense), the route's token (routed gate/up) or the route position (routed
+// down, ``route_rows``). The waves of a workgroup split the K blocks; their
+// partial sums meet in LDS and are added in wave order.
+// Lane (column j = lane % 16, k-group kq = lane / 16) feeds codes 8kq..8kq+7 of
+// each group: in a Q8_0 unit those of row j, block 2g + h sit at
+// 1024g + 16(16(2h + kq/2) + j) + 8(kq % 2) (moe_common.h).
+template <bool PAIR>
+__global__ void __launch_bounds__(512)
+    moe_w8_kernel(Proj p0, Proj p1, TokenSrc src, int route_rows, W8Src a, uint16_t* __restrict__ out, int kw) {
+  __shared__ float red[8][2][256];
+  SlotInfo si;
+  if (!slot_info(src, blockIdx.x, si)) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kq = lane >> 4, j = lane & 15;
+  const int rg = blockIdx.y;
+  const int rows = p0.rows, groups = a.k / 32;
+  constexpr int NU = PAIR ? 2 : 1;
+  for (int tc = 0; tc < si.cnt; tc += 16) {
+    const int q = tc + j;
+    int64_t arow = -1;
+    if (q < si.cnt) arow = src.dense ? q : (route_rows ? si.t0 + q : src.route_tok[si.t0 + q]);
+    f32x4 acc[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = wave; kb < p0.kb; kb += kw) {
+      const int ng = groups - 8 * kb < 8 ? groups - 8 * kb : 8;  // groups of this K block
+      uint64_t b[8];
+      float sa[8];
+#pragma unroll
+      for (int G = 0; G < 8; ++G) {
+        const bool ok = arow >= 0 && G < ng;
+        b[G] = ok ? *reinterpret_cast<const uint64_t*>(a.codes + arow * a.k + kb * kQK + 32 * G + 8 * kq) : 0ull;
+        sa[G] = ok ? a.scales[arow * groups + 8 * kb + G] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const Proj& p = u ? p1 : p0;
+        const uint8_t* un = unit_ptr<FMT_Q8>(p, si.expert, rg, kb);
+        u32x4 sw[4];  // block scales of rows 4kq + i: half 4h + g of the row's 16-byte line
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sw[i] = *reinterpret_cast<const u32x4*>(un + 4096 + 16 * (4 * kq + i));
+#pragma unroll
+        for (int G = 0; G < 8; ++G) {
+          if (G >= ng) break;
+          const int g = G >> 1, h = G & 1;
+          const uint64_t w = *reinterpret_cast<const uint64_t*>(
+              un + 1024 * g + 16 * (16 * (2 * h + (kq >> 1)) + j) + 8 * (kq & 1));
+          const i32x4 pr = mfma_i8(w, b[G], i32x4{0, 0, 0, 0});
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t word = sw[i][h * 2 + (g >> 1)];
+            const float dw = half_bits_to_float((word >> (16 * (g & 1))) & 0xffffu);
+            acc[u][i] += ((float)pr[i] * sa[G]) * dw;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave][u][lane * 4 + i] = acc[u][i];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 256; idx += blockDim.x) {
+      float v[NU];
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        v[u] = 0.f;
+        for (int w = 0; w < kw; ++w) v[u] += red[w][u][idx];
+      }
+      const int ln = idx >> 2;
+      const int row = rg * 16 + 4 * (ln >> 4) + (idx & 3);
+      const int qq = tc + (ln & 15);
+      if (row < rows && qq < si.cnt) {
+        const int64_t orow = src.dense ? qq : si.t0 + qq;
+        if (PAIR) {
+          const float g = bf16_round(v[0]), uu = bf16_round(v[NU - 1]);
+          out[orow * rows + row] = bf16_bits(bf16_round(g * sigmoid_acc(g)) * uu);
+        } else {
+          out[orow * rows + row] = bf16_bits(v[0]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+static void launch_act_q8(const uint16_t* src, int64_t rows, int k, const int* row_count, int8_t* codes,
+                          float* scales, hipStream_t s) {
+  const int64_t groups = rows * (k / 32);
+  hipLaunchKernelGGL(moe_act_q8_kernel, dim3((unsigned)cdiv(groups, 256)), dim3(256), 0, s, src, groups, k / 32,
+                     row_count, codes, scales);
+}
+
+static void launch_w8(bool pair, const Proj& p0, const Proj& p1, const TokenSrc& src, int grid_x, int route_rows,
+                      const W8Src& a, uint16_t* out, hipStream_t s) {
+  const int kw = p0.kb < 8 ? p0.kb : 8;
+  const dim3 grid((unsigned)grid_x, (unsigned)cdiv(p0.rows, 16));
+  if (pair)
+    hipLaunchKernelGGL(moe_w8_kernel<true>, grid, dim3(64 * kw), 0, s, p0, p1, src, route_rows, a, out, kw);
+  else
+    hipLaunchKernelGGL(moe_w8_kernel<false>, grid, dim3(64 * kw), 0, s, p0, p1, src, route_rows, a, out, kw);
 }
 
 // GGUF expert tables [experts][rows][K blocks][block bytes] -> unit-major
@@ -1008,11 +1182,14 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
         (rc = validate_table(a->shared_down, "shared_down", H, Is, 1)))
       return rc;
   }
+  Q6MOE_REQUIRE(a->compute == 0 || a->compute == 1, "moe_forward: compute must be 0 (bf16) or 1 (int8_q8)");
+  const bool w8 = a->compute == 1;
+  Q6MOE_REQUIRE(!(w8 && a->mode == 1), "moe_forward: the int8_q8 policy runs on the grouped kernels (mode 0 or 2)");
   if (a->mode == 1 && !dec_supported(B, K, E)) {
     set_error("moe_forward: decode mode needs tokens*top_k <= 1024, top_k <= 32, experts <= 256");
     return Q6MOE_ERR_INVALID;
   }
-  const bool decode = dec_supported(B, K, E) && (a->mode == 1 || (a->mode == 0 && B <= 64));
+  const bool decode = !w8 && dec_supported(B, K, E) && (a->mode == 1 || (a->mode == 0 && B <= 64));
   const WsLayout L = ws_layout(B, K, E, H, I, Is, kPrefillTile, decode);
   if (workspace_bytes < L.total) {
     if (static_ws)
@@ -1130,27 +1307,43 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   const Proj g = make_proj(a->gate, (int)I, (int)H), u = make_proj(a->up, (int)I, (int)H),
              d = make_proj(a->down, (int)H, (int)I);
   const int max_tokens = (int)B;  // an expert sees each token at most once
+  // int8_q8 policy: the Q8_0 projections run W8A8 (compute.py:20-34)
+  const bool w8_gu = w8 && fmt == FMT_Q8, w8_dn = w8 && fmt_dn == FMT_Q8;
   // The tiled MFMA path addresses token rows with 32-bit byte offsets.
   const bool tiled = pf_supported(fmt, H, I) && B * H * 2 < (1ll << 31) && B * K * I * 2 < (1ll << 31);
-  if (tiled) {
+  // gate/up + SwiGLU
+  bool down_done = false;
+  if (w8_gu) {
+    int8_t* xq = reinterpret_cast<int8_t*>(w + L.xq);
+    float* xq_s = reinterpret_cast<float*>(w + L.xq_s);
+    launch_act_q8(a->x, B, (int)H, nullptr, xq, xq_s, s);
+    launch_w8(true, g, u, routed, slots, 0, W8Src{xq, xq_s, (int)H}, ws.act, s);
+    mark(2);
+  } else if (tiled) {
     if (pf_tile_routes() != kPrefillTile) {
       set_error("moe_forward: prefill tile size mismatch");
       return Q6MOE_ERR_HIP;
     }
     const int max_tiles = (int)(E + B * K / kPrefillTile + 1);
-    // Q8_0 down: the tiled gate/up, then the generic down over the same routes
-    const bool tiled_down = fmt_dn == FMT_Q6;
+    down_done = fmt_dn == FMT_Q6 && !w8_dn;  // a Q6_K down runs tiled in the same call
     launch_moe_prefill(g, u, d, ws, max_tiles, a->x, (int)H, (int)I, s, a->events ? a->events[2] : nullptr,
-                       tiled_down);
-    if (!tiled_down) {
-      const int kw2 = d.kb < 8 ? d.kb : 8;
-      dispatch_format(fmt_dn, [&](auto fd) {
-        hipLaunchKernelGGL((moe_down_kernel<decltype(fd)::value, 4, 2>), dim3(slots, (unsigned)cdiv(H, 16 * 2)),
-                           dim3(64 * kw2), 0, s, d, routed, ws.act, (int)I, ws.y, (int)H, kw2);
-      });
-    }
+                       down_done);
   } else {
-    phases(g, u, d, routed, slots, max_tokens, (int)I, ws.act, ws.y, mark);
+    dispatch_format(fmt, [&](auto fg) {
+      launch_gate_up<decltype(fg)::value>(g, u, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, s);
+    });
+    mark(2);
+  }
+  // down projection
+  if (w8_dn) {
+    int8_t* aq = reinterpret_cast<int8_t*>(w + L.aq);
+    float* aq_s = reinterpret_cast<float*>(w + L.aq_s);
+    launch_act_q8(ws.act, B * K, (int)I, ws.hdr + 1, aq, aq_s, s);  // rows beyond the routes are skipped
+    launch_w8(false, d, d, routed, slots, 1, W8Src{aq, aq_s, (int)I}, ws.y, s);
+  } else if (!down_done) {
+    dispatch_format(fmt_dn, [&](auto fd) {
+      launch_down<decltype(fd)::value>(d, routed, slots, max_tokens, ws.act, (int)H, (int)I, ws.y, s);
+    });
   }
   if ((rc = check_launch("moe expert kernels"))) return rc;
   if (Is) {
@@ -1181,4 +1374,40 @@ extern "C" int q6moe_moe_forward_noalloc(const q6moe_moe_args* a, void* stream) 
   const int rc = static_scratch(&ptr);
   if (rc) return rc;
   return moe_forward_impl(a, ptr, kStaticScratchBytes, stream, true);
+}
+
+// Workspace of q6moe_q8_matmul: the quantised x (codes, FP32 scales).
+static size_t q8_ws(int64_t m, int64_t k, size_t* scales_at) {
+  const size_t codes = align256((size_t)(m * k));
+  if (scales_at) *scales_at = codes;
+  return codes + align256((size_t)(m * (k / 32) * 4));
+}
+
+extern "C" size_t q6moe_q8_matmul_workspace_size(int64_t m, int64_t k) {
+  if (m < 1 || k < 32 || k % 32) return 0;
+  return q8_ws(m, k, nullptr);
+}
+
+extern "C" int q6moe_q8_matmul(const uint16_t* x, int64_t m, int64_t k, const uint8_t* table, int64_t n, uint16_t* y,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  Q6MOE_REQUIRE(x && table && y && workspace, "q8_matmul: null pointer");
+  Q6MOE_REQUIRE(m >= 1 && n >= 1 && k >= 32 && k % 32 == 0, "q8_matmul: need m, n >= 1 and k a multiple of 32");
+  Q6MOE_REQUIRE(m <= (1 << 24) && n <= (1 << 24) && k <= (1 << 24), "q8_matmul: dimension too large");
+  Q6MOE_REQUIRE(aligned(x, 16) && aligned(table, 16) && aligned(workspace, 256),
+                "q8_matmul: x and table need 16-byte and workspace 256-byte alignment");
+  size_t scales_at = 0;
+  const size_t need = q8_ws(m, k, &scales_at);
+  if (workspace_bytes < need) {
+    set_error("q8_matmul: workspace too small (need " + std::to_string(need) + " bytes)");
+    return Q6MOE_ERR_INVALID;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  int8_t* codes = reinterpret_cast<int8_t*>(workspace);
+  float* scales = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + scales_at);
+  launch_act_q8(x, m, (int)k, nullptr, codes, scales, s);
+  q6moe_table t{Q6MOE_Q8_0, table, (int64_t)unit_table_bytes(Q6MOE_Q8_0, n, k), nullptr, 0};
+  const Proj p = make_proj(t, (int)n, (int)k);
+  TokenSrc dense{1, (int)m, nullptr, nullptr, nullptr, nullptr};
+  launch_w8(false, p, p, dense, 1, 0, W8Src{codes, scales, (int)k}, y, s);
+  return check_launch("q8_matmul kernels");
 }

@@ -7,6 +7,7 @@ Host surface mirrors the reference operators of AhmadSaeedZaidi/data-synth-tpu:
 * ``block_layout`` / ``dequantize_rows``       (kaggle/glm53_offload/gguf_quant.py)
 * ``expert_parallel`` / ``grouped_expert_parallel`` (kaggle/qwen38_tpu/experts.py,
   grouped_experts.py)
+* ``q8_matmul`` / ``bf16_q8_matmul`` / ``pack_q8`` (kaggle/qwen38_tpu/compute.py)
 * ``quantize`` / ``gather_scale_plane`` / ``read_quantized``
   (kaggle/qwen38_tpu/attention_cache.py)
 
@@ -33,6 +34,10 @@ def __getattr__(name):
         from . import experts
 
         return getattr(experts, name)
+    if name in ("q8_matmul", "bf16_q8_matmul", "pack_q8"):
+        from . import compute
+
+        return getattr(compute, name)
     if name in ("quantize", "gather_scale_plane", "read_quantized", "read_paged"):
         from . import attention_cache
 

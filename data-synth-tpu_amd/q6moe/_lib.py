@@ -61,6 +61,7 @@ class MoeArgs(ctypes.Structure):
         ("mode", _int),
         ("events", ctypes.POINTER(_vp)),
         ("shared_router", _vp),
+        ("compute", _int),
     ]
 
 
@@ -144,6 +145,8 @@ SIGNATURES = {
     "q6moe_moe_workspace_size": (_size, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "q6moe_moe_forward": (_int, [ctypes.POINTER(MoeArgs), _vp]),
     "q6moe_moe_forward_noalloc": (_int, [ctypes.POINTER(MoeArgs), _vp]),
+    "q6moe_q8_matmul_workspace_size": (_size, [_i64, _i64]),
+    "q6moe_q8_matmul": (_int, [_vp, _i64, _i64, _vp, _i64, _vp, _vp, _size, _vp]),
     "q6moe_kv_read": (_int, [ctypes.POINTER(KvArgs), _vp]),
     "q6moe_kv_gather_scales": (_int, [_vp, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp]),
     "q6moe_kv_quantize": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _int, _vp]),

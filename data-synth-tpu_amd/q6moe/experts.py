@@ -7,6 +7,10 @@ the numerics contract of the reference (BF16 weights decoded exactly, FP32
 accumulation, BF16 rounding of g, u, silu(g), the SwiGLU product and the
 down output, FP32 weighted sum over experts in ascending id, BF16 result).
 
+``compute="int8_q8"`` runs the Q8_0 projections W8A8 on the INT8 matrix
+cores, as the reference's ``q8_matmul`` (compute.py:20-34, experts.py:85-101);
+other projections stay BF16.
+
 One GPU holds every expert, so ``mesh``, ``group_size`` and
 ``tensor_parallel`` do not change the computation (the reference's grouped
 and tensor-parallel variants are defined to produce the same values); they
@@ -151,13 +155,14 @@ class _PackCache:
     def __init__(self):
         self.entries = {}
 
-    def get(self, raw, qtype, rows, width):
+    def get(self, raw, qtype, rows, width, single=False):
+        """``single``: ``raw`` is one projection [rows, blocks, bytes], packed as one expert."""
         key = id(raw)
-        sig = (raw._version, raw.data_ptr(), tuple(raw.shape), tuple(raw.stride()), qtype, rows, width)
+        sig = (raw._version, raw.data_ptr(), tuple(raw.shape), tuple(raw.stride()), qtype, rows, width, single)
         hit = self.entries.get(key)
         if hit is not None and hit[0] == sig:
             return hit[1]
-        table = pack_experts(raw, qtype, rows, width, raw.device)
+        table = pack_experts(raw.reshape(1, -1) if single else raw, qtype, rows, width, raw.device)
         if hit is None:
             weakref.finalize(raw, self.entries.pop, key, None)
         self.entries[key] = (sig, table)
@@ -220,12 +225,13 @@ def _check_workspace(workspace, need, device):
 class ExpertFFN:
     """Callable returned by ``expert_parallel``."""
 
-    def __init__(self, qtype, hidden, intermediate, mode=0, down_qtype=None):
+    def __init__(self, qtype, hidden, intermediate, mode=0, down_qtype=None, compute="bf16"):
         self.qtype = qtype
         self.down_qtype = down_qtype or qtype
         self.hidden = hidden
         self.intermediate = intermediate
         self.mode = mode
+        self.compute = compute
 
     def workspace_bytes(self, tokens, top_k, experts, shared_intermediate=0):
         return int(_lib.load().q6moe_moe_workspace_size(
@@ -326,6 +332,7 @@ class ExpertFFN:
         out = _check_bf16_out(out, (B, H), x.device)
         args.out = out.data_ptr()
         args.mode = self.mode
+        args.compute = 1 if self.compute == "int8_q8" else 0
         if events is not None:
             if len(events) != 5:
                 raise ValueError("events must hold 5 timing events")
@@ -367,9 +374,7 @@ def expert_parallel(
             f"this build runs gate/up of one type in {GATE_UP_TYPES} with down in {SUPPORTED}; got "
             f"{gate_type}/{up_type}/{down_type}"
         )
-    if compute == "int8_q8":
-        raise NotImplementedError("the int8_q8 (W8A8) policy is not part of this build")
-    return ExpertFFN(gate_type, hidden, intermediate, down_qtype=down_type)
+    return ExpertFFN(gate_type, hidden, intermediate, down_qtype=down_type, compute=compute)
 
 
 def grouped_expert_parallel(mesh=None, *, gate_type, up_type, down_type, hidden, intermediate,

@@ -20,6 +20,7 @@
  *  - q6moe_gguf_decode    kaggle/glm53_offload/gguf_quant.py:180-216 (dequantize_rows)
  *  - q6moe_moe_forward    kaggle/qwen38_tpu/experts.py:17-140 (expert_parallel's fn)
  *                         kaggle/qwen38_tpu/grouped_experts.py:21-163
+ *  - q6moe_q8_matmul      kaggle/qwen38_tpu/compute.py:20-34    (q8_matmul, W8A8)
  *  - q6moe_kv_read        kaggle/qwen38_tpu/attention_cache.py:71-81 (read_quantized)
  *                         kaggle/qwen38_tpu/attention_cache.py:46-68 (gather_scale_plane)
  *  - q6moe_kv_quantize    kaggle/qwen38_tpu/attention_cache.py:15-23 (quantize)
@@ -168,6 +169,10 @@ typedef struct q6moe_moe_args {
      output is scaled per token by RNE(sigmoid(RNE(x . shared_router))), computed on the
      device; NULL: shared_scale (or 1) is used. Not both. */
   const uint16_t* shared_router;
+  /* expert compute policy (kaggle/qwen38_tpu/experts.py:85-101): 0 "bf16" (decoded BF16 weights,
+     FP32 accumulation); 1 "int8_q8": projections whose table is Q8_0 run W8A8 as q8_matmul does
+     (kaggle/qwen38_tpu/compute.py:20-34), on the grouped kernels (mode 0 or 2) */
+  int compute;
 } q6moe_moe_args;
 
 #define Q6MOE_MOE_EVENTS 5
@@ -202,6 +207,18 @@ int q6moe_moe_forward(const q6moe_moe_args* args, void* stream);
  */
 #define Q6MOE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int q6moe_moe_forward_noalloc(const q6moe_moe_args* args, void* stream);
+
+/*
+ * W8A8 projection of the int8_q8 policy, q8_matmul (kaggle/qwen38_tpu/compute.py:20-34):
+ * y BF16 [m, n] = RNE(sum over 32-value groups g of (f32(sum_k xq[:, g, k] * w[:, g, k]) *
+ * xs[:, g]) * d[:, g]) with x BF16 [m, k] quantised per row and group (xs = max|x| / 127,
+ * xq = clip(rint(x / (xs ? xs : 1)), -127, 127)) and w, d the INT8 codes and FP16 scales of
+ * a Q8_0 table [n rows, k] in the unit-major layout (q6moe_moe_pack, one expert), on the
+ * INT8 matrix cores. k a multiple of 32; workspace >= q6moe_q8_matmul_workspace_size(m, k).
+ */
+size_t q6moe_q8_matmul_workspace_size(int64_t m, int64_t k);
+int q6moe_q8_matmul(const uint16_t* x, int64_t m, int64_t k, const uint8_t* table, int64_t n, uint16_t* y,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* INT8 KV cache gather + dequant (read_quantized).                         */

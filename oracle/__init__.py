@@ -36,5 +36,10 @@ moe.expert_ffn              brute-force per-token loop (routing_validation
                             and poisoned-expert invariants.
 kv.*                        closed forms from the reference's KV tests
                             (rounded-divisor case, zero groups, clipping).
+compute.q8_matmul           exact closed form on power-of-two scales and
+                            integer codes (equals x . dequant(W) in FP64);
+                            zero rows give exact zeros.
+moe.shared_gate             closed forms (one-hot routers, sigmoid(0),
+                            saturation, the BF16 rounding of the logit).
 ==========================  ==================================================
 """

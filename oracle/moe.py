@@ -27,15 +27,24 @@ from .routing import route_weights
 
 
 def _mm(a, w):
+    """a @ w.T for decoded weights (FP64 sums, FP32 result), or w(a) for a
+    projection given as a function (the W8A8 policy's integer dot)."""
+    if callable(w):
+        return w(np.asarray(a, np.float32))
     return (np.asarray(a, np.float64) @ np.asarray(w, np.float64).T).astype(np.float32)
 
 
-def decode_expert(table, e, qtype, rows, width):
-    """One expert's weight matrix [rows, width] as BF16 values in FP32."""
+def decode_expert(table, e, qtype, rows, width, policy="bf16"):
+    """One expert's weight matrix [rows, width] as BF16 values in FP32; under
+    the int8_q8 policy a Q8_0 projection is instead the function running the
+    W8A8 integer dot on its bytes (experts.py:85-101, compute.py:20-34)."""
+    from .compute import q8_matmul
     from .gguf import block_layout
 
     values, size = block_layout(qtype)
     raw = np.asarray(table[e]).reshape(rows, -(-width // values), size)
+    if policy == "int8_q8" and qtype == "Q8_0":
+        return lambda a: q8_matmul(a, raw)
     return bf16_round(dequantize_rows(raw, qtype, width))
 
 
@@ -47,7 +56,8 @@ def expert_contribution(x, gate_w, up_w, down_w):
     return bf16_round(_mm(a, down_w))
 
 
-def expert_ffn(gate, up, down, x, ids, weights, *, types, hidden, intermediate, shared=None, workers=1):
+def expert_ffn(gate, up, down, x, ids, weights, *, types, hidden, intermediate, shared=None, workers=1,
+               policy="bf16"):
     """x BF16 values [B, hidden] -> BF16 values [B, hidden] as FP32.
 
     gate/up/down: raw GGUF tables indexable by expert, each expert
@@ -55,7 +65,8 @@ def expert_ffn(gate, up, down, x, ids, weights, *, types, hidden, intermediate, 
     expert (dict of decoded BF16 matrices gate/up/down, optional per-token
     BF16 ``gate_scale``). As in engine.py:199-203 with math.py:282-284 the
     shared output is RNE(y_shared * gate_scale) in BF16 and is added to the
-    BF16 routed sum: RNE(f32(routed) + f32(shared)). ``workers`` > 1 computes
+    BF16 routed sum: RNE(f32(routed) + f32(shared)). ``policy`` "int8_q8" runs
+    the routed experts' Q8_0 projections as W8A8 integer dots. ``workers`` > 1 computes
     the experts' contributions on a thread pool; they are still added in
     ascending expert id, so the result does not depend on it.
     """
@@ -67,9 +78,9 @@ def expert_ffn(gate, up, down, x, ids, weights, *, types, hidden, intermediate, 
 
     def contribution(e):
         rows = np.nonzero(r[:, e])[0]
-        gw = decode_expert(gate, e, gt, intermediate, hidden)
-        uw = decode_expert(up, e, ut, intermediate, hidden)
-        dw = decode_expert(down, e, dt, hidden, intermediate)
+        gw = decode_expert(gate, e, gt, intermediate, hidden, policy)
+        uw = decode_expert(up, e, ut, intermediate, hidden, policy)
+        dw = decode_expert(down, e, dt, hidden, intermediate, policy)
         return rows, expert_contribution(x[rows], gw, uw, dw)
 
     if workers > 1 and len(active) > 1:

@@ -1,0 +1,130 @@
+"""The int8_q8 (W8A8) policy on the GPU against the oracle.
+
+* ``q8_matmul`` as the reference's own test (kaggle/tests/test_qwen38_compute.py:80-99):
+  x [8, 256] with a zero row, outlier groups and a row of 127s, weights
+  pack_q8(N(0, 1) [64, 256]); oracle numpy_q8_matmul (oracle/compute.py) rounded
+  to BF16; tolerance atol 0.5, rtol 0.004 (the reference's BF16 bound) and the
+  zero row exactly zero. Also a tight check: >= 90 % bit-identical and max
+  relative error 1e-2 (the FP32 group sums are added in another order).
+* The routed FFN with compute="int8_q8" on the reference's routing validation
+  case and on the checkpoints' Q8_0 layers, against the oracle's int8_q8 policy.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import compute as oracle_compute
+from oracle import moe as oracle_moe
+from oracle.packed_q6 import bf16_round
+from q6moe.compute import bf16_q8_matmul, pack_q8, q8_matmul
+from q6moe.experts import expert_parallel
+from q6moe.synth import moe_layer
+
+from .test_gpu_moe import assert_moe_close
+from .test_gpu_workloads import _routing_validation_case
+
+pytestmark = pytest.mark.gpu
+
+
+def test_q8_matmul_reference_case(device):
+    rng = np.random.default_rng(837)
+    x = rng.normal(size=(8, 256)).astype(np.float32)
+    x[0] = 0
+    x[1, ::32] *= 20
+    x[2] = 127
+    raw = pack_q8(rng.normal(size=(64, 256)).astype(np.float32))
+    token = torch.from_numpy(x).to(device).to(torch.bfloat16)
+    got = q8_matmul(token, torch.from_numpy(raw).to(device)).float().cpu().numpy()
+    want = bf16_round(oracle_compute.q8_matmul(token.float().cpu().numpy(), raw))
+    np.testing.assert_allclose(got, want, atol=0.5, rtol=0.004)
+    np.testing.assert_array_equal(got[0], 0)
+    assert_moe_close(got, want, ref_gate=False)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 32, 16), (17, 768, 40), (64, 2048, 96)])
+def test_q8_matmul_shapes(device, m, k, n):
+    rng = np.random.default_rng(m + k + n)
+    x = rng.normal(size=(m, k)).astype(np.float32)
+    raw = pack_q8(rng.normal(0, 0.05, (n, k)).astype(np.float32))
+    token = torch.from_numpy(x).to(device).to(torch.bfloat16)
+    packed = torch.from_numpy(raw).to(device)
+    got = q8_matmul(token, packed).float().cpu().numpy()
+    want = bf16_round(oracle_compute.q8_matmul(token.float().cpu().numpy(), raw))
+    assert_moe_close(got, want, ref_gate=False)
+    # the BF16 policy's product of the same weights stays close to the W8A8 one
+    # (the activation quantisation error: compute.py:108-123 requires <= 1.2 %)
+    base = bf16_q8_matmul(token, packed).float().cpu().numpy()
+    assert np.linalg.norm(got - base) / np.linalg.norm(base) < 0.012
+
+
+def _w8_expected(packed, ids, weights, x, hidden, inter, count):
+    """routing_validation.py:52-71 with the int8_q8 policy: the Q8_0 down runs
+    numpy_q8_matmul, rounded to BF16."""
+    from oracle.gguf import dequantize_rows
+
+    x = bf16_round(x)
+    routing = bf16_round(weights)
+    expected = np.zeros((x.shape[0], hidden), np.float32)
+    for e in range(count):
+        route = np.sum(np.where(ids == e, routing, 0).astype(np.float32), -1)
+
+        def project(value, name):
+            raw = packed[name][e]
+            if name == "down":
+                return bf16_round(oracle_compute.q8_matmul(value.astype(np.float32), raw))
+            matrix = bf16_round(dequantize_rows(raw, "Q6_K", hidden))
+            return bf16_round(value.astype(np.float32) @ matrix.T)
+
+        gate = project(x, "gate")
+        activated = bf16_round(gate / (1 + np.exp(-gate)))
+        product = bf16_round(activated * project(x, "up"))
+        expected += project(product, "down") * route[:, None]
+    return bf16_round(expected)
+
+
+@pytest.mark.parametrize("batch,mode", [(273, 0), (1, 0), (64, 2)])
+def test_reference_routing_validation_gate_int8_q8(device, batch, mode):
+    packed, ids, weights, source, hidden, inter, count = _routing_validation_case(batch)
+    want = _w8_expected(packed, ids, weights, source, hidden, inter, count)
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q8_0", hidden=hidden,
+                         intermediate=inter, compute="int8_q8")
+    tabs = fn.prepare(*(packed[n].reshape(count, -1) for n in ("gate", "up", "down")), device)
+    x = torch.from_numpy(source).to(device).to(torch.bfloat16)
+    i = torch.from_numpy(ids).to(device)
+    w = torch.from_numpy(weights).to(device).to(torch.bfloat16)
+    fn.mode = mode
+    try:
+        got = fn(*tabs, x, i, w).float().cpu().numpy()
+        zeros = fn(*tabs, x, i, torch.zeros_like(w)).float().cpu().numpy()
+    finally:
+        fn.mode = 0
+    np.testing.assert_allclose(got, want, atol=3e-3, rtol=3e-3)
+    np.testing.assert_array_equal(got[np.all(weights == 0, axis=-1)], 0)
+    np.testing.assert_array_equal(zeros, 0)
+
+
+@pytest.mark.parametrize("qtype,tokens,mode", [("Q6_K", 8, 0), ("Q6_K", 300, 0), ("Q8_0", 8, 0), ("Q8_0", 100, 2),
+                                               ("Q4_K", 20, 2)])
+def test_int8_q8_policy_matches_oracle(device, qtype, tokens, mode):
+    # Q8_0 down under Q6_K (q6.json) or Q4_K gate/up, and all-Q8_0 layers (q8.json):
+    # every Q8_0 projection W8A8, the others BF16.
+    L = moe_layer(seed=91 + tokens, experts=8, top_k=3, hidden=512, intermediate=256, tokens=tokens, qtype=qtype,
+                  down_qtype="Q8_0", sigma=0.02, pack=False)
+    fn = expert_parallel(None, gate_type=qtype, up_type=qtype, down_type="Q8_0", hidden=512, intermediate=256,
+                         compute="int8_q8")
+    tabs = fn.prepare(*(L[n].reshape(8, -1) for n in ("gate", "up", "down")), device)
+    x = torch.from_numpy(L["x"]).to(device).to(torch.bfloat16)
+    ids = torch.from_numpy(L["ids"]).to(device)
+    w = torch.from_numpy(L["weights"]).to(device).to(torch.bfloat16)
+    fn.mode = mode
+    try:
+        got = fn(*tabs, x, ids, w).float().cpu().numpy()
+    finally:
+        fn.mode = 0
+    want = oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"], L["ids"], L["weights"],
+                                 types=(qtype, qtype, "Q8_0"), hidden=512, intermediate=256, policy="int8_q8")
+    assert_moe_close(got, want)
+    bf16 = oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"], L["ids"], L["weights"],
+                                 types=(qtype, qtype, "Q8_0"), hidden=512, intermediate=256)
+    assert not np.array_equal(want, bf16)  # the policy changes the arithmetic

@@ -337,3 +337,35 @@ def test_shared_gate_oracle_closed_forms():
     assert moe.shared_gate(x[3:], r2)[0] == want
     unrounded = packed_q6.bf16_round(np.float32(1.0 / (1.0 + np.exp(-(1.0 + 17 * 2.0**-12)))))
     assert want != unrounded
+
+
+def test_q8_matmul_oracle_closed_form():
+    # Activation groups whose max is 127 * 2^e quantise without rounding
+    # (codes = x / 2^e), and power-of-two weight scales keep every product and
+    # sum exact: the W8A8 dot then equals x . dequant(W) in FP64 exactly. A
+    # transposed operand, a wrong group index or a missing scale fails it.
+    from oracle import compute
+    from q6moe.quantize import quantize_q8_0
+
+    rng = np.random.default_rng(837)
+    codes = rng.integers(-127, 128, (5, 4, 32)).astype(np.float32)
+    codes[:, :, 0] = 127
+    e = rng.integers(-4, 3, (5, 4)).astype(np.float32)
+    x = (codes * np.exp2(e)[..., None]).reshape(5, 128)
+    x[3] = 0
+    wcodes = rng.integers(-127, 128, (7, 4, 32)).astype(np.float32)
+    ws = np.exp2(rng.integers(-9, -3, (7, 4))).astype(np.float32)
+    raw = np.concatenate([ws.astype("<f2").view(np.uint8).reshape(7, 4, 2),
+                          wcodes.astype(np.int8).view(np.uint8)], axis=-1)
+    w = (wcodes * ws[..., None]).reshape(7, 128)
+    got = compute.q8_matmul(x, raw)
+    np.testing.assert_array_equal(got, (x.astype(np.float64) @ w.T.astype(np.float64)).astype(np.float32))
+    assert np.all(got[3] == 0)
+    # and it matches the pack_q8 quantizer's bytes decoded (compute.py:41-65)
+    wf = rng.normal(size=(3, 64)).astype(np.float32)
+    raw = quantize_q8_0(wf)
+    assert raw.shape == (3, 2, 34)
+    xf = rng.normal(size=(2, 64)).astype(np.float32)
+    ref = compute.q8_matmul(xf, raw)
+    dq = gguf.dequantize_rows(raw, "Q8_0", 64)
+    assert np.max(np.abs(ref - xf @ dq.T)) < 0.05 * np.abs(xf @ dq.T).max()
