@@ -1244,7 +1244,9 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   };
   if (decode) {
     mark(0);
-    if (Is) {
+    // up to kDecSharedTokens tokens the shared expert runs inside the decode launches
+    const bool fused_shared = Is && B <= kDecSharedTokens;
+    if (Is && !fused_shared) {
       TokenSrc dense{1, (int)B, nullptr, nullptr, nullptr, nullptr};
       const Proj sg = make_proj(a->shared_gate, (int)Is, (int)H), su = make_proj(a->shared_up, (int)Is, (int)H),
                  sd = make_proj(a->shared_down, (int)H, (int)Is);
@@ -1273,6 +1275,15 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
     D.sh_y = ws.sh_y;
     D.sh_scale = sh_scale;
     D.out = a->out;
+    D.S = DecShared{};
+    if (fused_shared) {
+      D.S.gate = make_proj(a->shared_gate, (int)Is, (int)H);
+      D.S.up = make_proj(a->shared_up, (int)Is, (int)H);
+      D.S.down = make_proj(a->shared_down, (int)H, (int)Is);
+      D.S.is = (int)Is;
+      D.S.act = ws.sh_act;
+      D.S.y = ws.sh_y;
+    }
     D.after_gate_up = a->events ? a->events[2] : nullptr;
     D.after_down = a->events ? a->events[3] : nullptr;
     if ((rc = launch_moe_decode(fmt, fmt_dn, D, s))) return rc;

@@ -148,10 +148,21 @@ struct DecTables {
   int* route_dst;    // [routes] token-major slot b*K + rank (rank = ascending expert id)
 };
 
+// The always-on shared expert inside the decode-step launches (tokens <= 16):
+// its gate/up items run in the gate/up launch and its down items in the down
+// launch, ahead of the routed ones. is == 0: no shared expert there.
+struct DecShared {
+  Proj gate, up, down;  // one expert: gate/up [is, H], down [H, is]
+  int is;
+  uint16_t* act;        // [B, is] SwiGLU activations
+  uint16_t* y;          // [B, H] BF16 output
+};
+
 struct DecArgs {
   Proj gate, up, down;
   DecRoute R;
   DecTables T;
+  DecShared S;
   const uint16_t* x;
   int H, I, max_slots;
   uint16_t* act;
@@ -164,6 +175,7 @@ struct DecArgs {
 };
 
 bool dec_supported(int64_t B, int64_t K, int64_t E);
+constexpr int kDecSharedTokens = 16;  // the shared expert joins the decode launches up to this many tokens
 int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s);
 
 // Unit-decode probes (q6moe_moe_unpack): the decode kernels' LDS-staged path

@@ -639,24 +639,22 @@ __device__ __forceinline__ void split_reduce(uint8_t* smem, int ns, int wave, f3
   __syncthreads();
 }
 
+// One gate/up item: row group rg of an expert's gate and up, over its tokens
+// tok[0..cnt) in passes of 16; a = RNE(RNE(g*sig(g)) * u) into act rows
+// t0 + q (row stride ``inter``).
 template <int FMT, bool kFullK>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
-    moe_dec_gate_up_kernel(Proj gate, Proj up, DecRoute R, DecTables T, const uint16_t* __restrict__ x,
-                           int hidden, uint16_t* __restrict__ act, int inter) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+__device__ __forceinline__ void dec_gate_up_item(uint8_t* smem, uint8_t* ring, const Proj& gate, const Proj& up,
+                                                 int64_t expert, int rg, int t0, int cnt, const int* tok,
+                                                 const uint16_t* __restrict__ x, int nx, int hidden,
+                                                 uint16_t* __restrict__ act, int inter) {
   const int ns = split_waves(), wave = split_wave();
-  uint8_t* ring = smem + wave * wave_lds<FMT>();
-  int* tok = reinterpret_cast<int*>(ring + kStages * stage_bytes<FMT>());
-  const int rg = blockIdx.x, slot = blockIdx.y;
   const int lane = threadIdx.x & 63, jA = lane >> 4, j = lane & 15;
-  SlotRoute sr;
-  if (!dec_route(R, slot, rg == 0 && wave == 0, T, ring, tok, sr)) return;
-  const WStream<FMT> wg(gate, sr.expert, lane), wu(up, sr.expert, lane);
+  const WStream<FMT> wg(gate, expert, lane), wu(up, expert, lane);
   const int kb0 = wave * gate.kb / ns, kb1 = (wave + 1) * gate.kb / ns;
-  for (int tc = 0; tc < sr.cnt; tc += kPassTokens) {
-    const int nt = sr.cnt - tc < kPassTokens ? sr.cnt - tc : kPassTokens;
+  for (int tc = 0; tc < cnt; tc += kPassTokens) {
+    const int nt = cnt - tc < kPassTokens ? cnt - tc : kPassTokens;
     if (tc) wait_vm<0>();  // the previous pass's stores
-    const XStream<FMT, kFullK> xs(x, R.B, hidden, tok[tc + (j < nt ? j : nt - 1)], lane);
+    const XStream<FMT, kFullK> xs(x, nx, hidden, tok[tc + (j < nt ? j : nt - 1)], lane);
     f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     if (kb1 > kb0)
       stream_units<FMT, kFullK, 2>(
@@ -671,27 +669,88 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
           const float g = bf16_round(acc[0][q]);
           const float uu = bf16_round(acc[1][q]);
           const float sg = bf16_round(g * sigmoid_acc(g));
-          act[(int64_t)(sr.t0 + tc + j) * inter + row] = bf16_bits(sg * uu);
+          act[(int64_t)(t0 + tc + j) * inter + row] = bf16_bits(sg * uu);
         }
       }
     }
   }
 }
 
+// Items: the shared expert's row groups first (sh.is > 0), then (row group,
+// expert slot) with the row group fastest.
+template <int FMT, bool kFullK>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+    moe_dec_gate_up_kernel(Proj gate, Proj up, DecRoute R, DecTables T, const uint16_t* __restrict__ x,
+                           int hidden, uint16_t* __restrict__ act, int inter, DecShared sh) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int wave = split_wave();
+  uint8_t* ring = smem + wave * wave_lds<FMT>();
+  int* tok = reinterpret_cast<int*>(ring + kStages * stage_bytes<FMT>());
+  const int sh_items = sh.is ? (sh.is + 15) / 16 : 0;
+  const int item = blockIdx.x;
+  if (item < sh_items) {
+    // every token, weight 1: the token list is 0..B-1
+    const int lane = threadIdx.x & 63;
+    if (lane < R.B) tok[lane] = lane;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the list is in LDS before the ring fills
+    dec_gate_up_item<FMT, kFullK>(smem, ring, sh.gate, sh.up, 0, item, 0, R.B, tok, x, R.B, hidden, sh.act, sh.is);
+    return;
+  }
+  const int groups_i = (inter + 15) / 16;
+  const int rg = (item - sh_items) % groups_i, slot = (item - sh_items) / groups_i;
+  SlotRoute sr;
+  if (!dec_route(R, slot, rg == 0 && wave == 0, T, ring, tok, sr)) return;
+  dec_gate_up_item<FMT, kFullK>(smem, ring, gate, up, sr.expert, rg, sr.t0, sr.cnt, tok, x, R.B, hidden, act, inter);
+}
+
+// Items: the shared expert's down (kShRows row groups each, output BF16
+// y = RNE(acc) into sh.y [B, H]) first, then (block of kDownRows row groups,
+// expert slot), which store the exact FP32 product f32(RNE(y)) * f32(r)
+// token-major at the route's rank among its token's experts.
+constexpr int kShRows = 2;
+
 template <int FMT, bool kFullK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     moe_dec_down_kernel(Proj down, DecTables T, const uint16_t* __restrict__ act, int inter,
-                        float* __restrict__ contrib, int hidden) {
+                        float* __restrict__ contrib, int hidden, DecShared sh, int tokens) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int ns = split_waves(), wave = split_wave();
   uint8_t* ring = smem + wave * wave_lds<FMT>();
-  const int slot = blockIdx.y;
+  const int lane = threadIdx.x & 63, jA = lane >> 4, j = lane & 15;
+  const int groups = (hidden + 15) / 16;
+  const int sh_items = sh.is ? (groups + kShRows - 1) / kShRows : 0;
+  const int item = blockIdx.x;
+  if (item < sh_items) {
+    const int rg0 = item * kShRows;
+    const int kb0 = wave * sh.down.kb / ns, kb1 = (wave + 1) * sh.down.kb / ns;
+    const WStream<FMT> wd(sh.down, 0, lane);
+    const int nt = tokens;  // <= 16: one pass
+    const XStream<FMT, kFullK> xs(sh.act, tokens, sh.is, j < nt ? j : nt - 1, lane);
+    f32x4 acc[kShRows];
+#pragma unroll
+    for (int r = 0; r < kShRows; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (kb1 > kb0)
+      stream_units<FMT, kFullK, kShRows>(
+          ring, kb0, kb1 - kb0, xs,
+          [&](int p, int kb, uint8_t* st) { wd.issue(rg0 + p < groups ? rg0 + p : groups - 1, kb, st); }, acc);
+    split_reduce<kShRows, wave_lds<FMT>()>(smem, ns, wave, acc);
+    if (wave == 0 && j < nt) {
+#pragma unroll
+      for (int r = 0; r < kShRows; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = (rg0 + r) * 16 + 4 * jA + q;
+          if (row < hidden) sh.y[(int64_t)j * hidden + row] = bf16_bits(acc[r][q]);
+        }
+    }
+    return;
+  }
+  const int dn_x = (groups + kDownRows - 1) / kDownRows;
+  const int slot = (item - sh_items) / dn_x;
   if (slot >= T.hdr[0]) return;
   const int t0 = T.slot_t0[slot], cnt = T.slot_cnt[slot];
-  const int lane = threadIdx.x & 63, jA = lane >> 4, j = lane & 15;
   const WStream<FMT> wd(down, T.slot_e[slot], lane);
-  const int groups = (hidden + 15) / 16;
-  const int rg0 = blockIdx.x * kDownRows;
+  const int rg0 = ((item - sh_items) % dn_x) * kDownRows;
   const int kb0 = wave * down.kb / ns, kb1 = (wave + 1) * down.kb / ns;
   for (int tc = 0; tc < cnt; tc += kPassTokens) {
     const int nt = cnt - tc < kPassTokens ? cnt - tc : kPassTokens;
@@ -803,12 +862,14 @@ static int launch(const DecArgs& A, hipStream_t s) {
     attr_done = true;
   }
   const int dn_x = (int)cdiv(groups_h, kDownRows);
-  const int ns_gu = split_for((int64_t)groups_i * A.max_slots), ns_dn = split_for((int64_t)dn_x * A.max_slots);
-  hipLaunchKernelGGL((moe_dec_gate_up_kernel<FG, kFullK>), dim3((unsigned)groups_i, A.max_slots), dim3(64 * ns_gu),
-                     ns_gu * lds_gu, s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I);
+  const int sh_gu = A.S.is ? (int)cdiv(A.S.is, 16) : 0, sh_dn = A.S.is ? (int)cdiv(groups_h, kShRows) : 0;
+  const int64_t items_gu = (int64_t)groups_i * A.max_slots + sh_gu, items_dn = (int64_t)dn_x * A.max_slots + sh_dn;
+  const int ns_gu = split_for(items_gu), ns_dn = split_for(items_dn);
+  hipLaunchKernelGGL((moe_dec_gate_up_kernel<FG, kFullK>), dim3((unsigned)items_gu), dim3(64 * ns_gu),
+                     ns_gu * lds_gu, s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I, A.S);
   if (A.after_gate_up) (void)hipEventRecord((hipEvent_t)A.after_gate_up, s);
-  hipLaunchKernelGGL((moe_dec_down_kernel<FD, kFullK>), dim3((unsigned)dn_x, A.max_slots), dim3(64 * ns_dn),
-                     ns_dn * lds_dn, s, A.down, A.T, A.act, A.I, A.contrib, A.H);
+  hipLaunchKernelGGL((moe_dec_down_kernel<FD, kFullK>), dim3((unsigned)items_dn), dim3(64 * ns_dn),
+                     ns_dn * lds_dn, s, A.down, A.T, A.act, A.I, A.contrib, A.H, A.S, A.R.B);
   if (A.after_down) (void)hipEventRecord((hipEvent_t)A.after_down, s);
   hipLaunchKernelGGL(moe_dec_combine_kernel, dim3(A.R.B, (unsigned)cdiv(A.H, 256)), dim3(64), 0, s, A.T,
                      A.contrib, A.H, A.R.K, A.sh_y, A.sh_scale, A.out);
@@ -821,7 +882,7 @@ bool dec_supported(int64_t B, int64_t K, int64_t E) {
 
 template <int FG, int FD>
 static int launch_k(const DecArgs& A, hipStream_t s) {
-  const bool full = A.H % kQK == 0 && A.I % kQK == 0;
+  const bool full = A.H % kQK == 0 && A.I % kQK == 0 && (A.S.is == 0 || A.S.is % kQK == 0);
   return full ? launch<FG, FD, true>(A, s) : launch<FG, FD, false>(A, s);
 }
 
