@@ -87,15 +87,19 @@ def stats(samples):
             "max": round(float(v.max()), 3), "mean": round(float(v.mean()), 3), "n": int(v.size)}
 
 
-def traffic_of(kernel):
+def traffic_of(kernel, tag=None):
     """HBM-side bytes per dispatch of ``kernel`` and the summary they come from:
     the last column of its row in a committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (profiles/*__hbm_bytes.txt, MB per dispatch after scaling by a
-    device copy of known size). (None, None) when no summary lists it."""
+    device copy of known size); ``tag`` picks the row whose note names that
+    workload. (None, None) when no summary lists it."""
     for f in sorted(PROFILES.glob("*__hbm_bytes.txt")):
         for line in f.read_text().splitlines():
             cells = [c.strip() for c in line.strip().strip("|").split("|")]
-            if line.startswith("|") and len(cells) >= 3 and cells[0].split(" (")[0] == kernel:
+            if not line.startswith("|") or len(cells) < 3:
+                continue
+            name, _, note = cells[0].partition(" (")
+            if name == kernel and (tag is None or tag in note):
                 try:
                     return int(round(float(cells[-1]) * 1e6)), f"profiles/{f.name}"
                 except ValueError:
@@ -103,14 +107,14 @@ def traffic_of(kernel):
     return None, None
 
 
-def roofline(kernel, bound, work, avg_us, *, work_unit):
+def roofline(kernel, bound, work, avg_us, *, work_unit, tag=None):
     """Roofline block of one kernel: ``work`` algorithmic bytes (or FLOPs) per
     launch over its average launch duration."""
     if bound == "hbm":
         achieved, peak, unit = work / (avg_us * 1e-6) / 1e9, HBM_PEAK_GBS, "GB/s"
     else:
         achieved, peak, unit = work / (avg_us * 1e-6) / 1e12, MFMA_PEAK_TFLOPS, "TFLOP/s"
-    traffic, source = traffic_of(kernel)
+    traffic, source = traffic_of(kernel, tag)
     return {"kernel": kernel, "bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_source": source,
             work_unit: int(work), "avg_launch_us": round(float(avg_us), 3)}
@@ -496,14 +500,17 @@ def measure_q4_shared(dev, with_cpu):
         us = t["fused"]["median"]
         ph = phase_means(call, 50)
         gu_bytes = active * 2 * proj_bytes + b * H4 * 2 + routes * I4 * 2  # gate+up, x, SwiGLU rows
+        if b <= 16:  # the shared expert's gate/up run in the same launch
+            gu_bytes += 2 * IS * (H4 // 256) * 144 + b * IS * 2
         row.update({"us_per_step": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
                     "tokens_per_s": round(b / (us * 1e-6), 1),
                     "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "step_us": t["fused"],
                     "phases_us": {k: round(float(v), 2) for k, v in
-                                  zip(("shared", "routed_gate_up", "routed_down", "combine"), ph)},
+                                  zip(("pre", "gate_up", "down", "combine") if b <= 16 else
+                                      ("shared", "routed_gate_up", "routed_down", "combine"), ph)},
                     "active_experts": active, "bytes_per_step": nbytes, "layer_copies": want_copies,
                     "roofline": roofline("q6moe::moe_dec_gate_up_kernel<1, true>", "hbm", gu_bytes, ph[1],
-                                         work_unit="bytes_per_launch")})
+                                         work_unit="bytes_per_launch", tag=f"{b} token")})
         out["batches"][str(b)] = row
     return out
 
