@@ -500,13 +500,13 @@ def measure_q4_shared(dev, with_cpu):
         us = t["fused"]["median"]
         ph = phase_means(call, 50)
         gu_bytes = active * 2 * proj_bytes + b * H4 * 2 + routes * I4 * 2  # gate+up, x, SwiGLU rows
-        if b <= 16:  # the shared expert's gate/up run in the same launch
+        if b <= 64:  # the shared expert's gate/up run in the same launch
             gu_bytes += 2 * IS * (H4 // 256) * 144 + b * IS * 2
         row.update({"us_per_step": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
                     "tokens_per_s": round(b / (us * 1e-6), 1),
                     "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "step_us": t["fused"],
                     "phases_us": {k: round(float(v), 2) for k, v in
-                                  zip(("pre", "gate_up", "down", "combine") if b <= 16 else
+                                  zip(("pre", "gate_up", "down", "combine") if b <= 64 else
                                       ("shared", "routed_gate_up", "routed_down", "combine"), ph)},
                     "active_experts": active, "bytes_per_step": nbytes, "layer_copies": want_copies,
                     "roofline": roofline("q6moe::moe_dec_gate_up_kernel<1, true>", "hbm", gu_bytes, ph[1],

@@ -148,9 +148,10 @@ struct DecTables {
   int* route_dst;    // [routes] token-major slot b*K + rank (rank = ascending expert id)
 };
 
-// The always-on shared expert inside the decode-step launches (tokens <= 16):
-// its gate/up items run in the gate/up launch and its down items in the down
-// launch, ahead of the routed ones. is == 0: no shared expert there.
+// The always-on shared expert inside the decode-step launches (tokens <=
+// kDecSharedTokens): its gate/up items run in the gate/up launch and its down
+// items in the down launch, ahead of the routed ones, one item per 16-token
+// pass. is == 0: no shared expert there.
 struct DecShared {
   Proj gate, up, down;  // one expert: gate/up [is, H], down [H, is]
   int is;
@@ -175,7 +176,7 @@ struct DecArgs {
 };
 
 bool dec_supported(int64_t B, int64_t K, int64_t E);
-constexpr int kDecSharedTokens = 16;  // the shared expert joins the decode launches up to this many tokens
+constexpr int kDecSharedTokens = 64;  // the shared expert joins the decode launches up to this many tokens
 int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s);
 
 // Unit-decode probes (q6moe_moe_unpack): the decode kernels' LDS-staged path

@@ -676,8 +676,8 @@ __device__ __forceinline__ void dec_gate_up_item(uint8_t* smem, uint8_t* ring, c
   }
 }
 
-// Items: the shared expert's row groups first (sh.is > 0), then (row group,
-// expert slot) with the row group fastest.
+// Items: the shared expert's (row group, pass of 16 tokens) first (sh.is > 0),
+// then (row group, expert slot) with the row group fastest.
 template <int FMT, bool kFullK>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     moe_dec_gate_up_kernel(Proj gate, Proj up, DecRoute R, DecTables T, const uint16_t* __restrict__ x,
@@ -686,14 +686,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
   const int wave = split_wave();
   uint8_t* ring = smem + wave * wave_lds<FMT>();
   int* tok = reinterpret_cast<int*>(ring + kStages * stage_bytes<FMT>());
-  const int sh_items = sh.is ? (sh.is + 15) / 16 : 0;
+  const int sh_groups = (sh.is + 15) / 16, passes = (R.B + kPassTokens - 1) / kPassTokens;
+  const int sh_items = sh.is ? sh_groups * passes : 0;
   const int item = blockIdx.x;
   if (item < sh_items) {
-    // every token, weight 1: the token list is 0..B-1
+    // every token, weight 1; item (row group, pass of 16 tokens)
     const int lane = threadIdx.x & 63;
-    if (lane < R.B) tok[lane] = lane;
+    const int rg = item % sh_groups, t0 = (item / sh_groups) * kPassTokens;
+    const int cnt = R.B - t0 < kPassTokens ? R.B - t0 : kPassTokens;
+    if (lane < cnt) tok[lane] = t0 + lane;
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the list is in LDS before the ring fills
-    dec_gate_up_item<FMT, kFullK>(smem, ring, sh.gate, sh.up, 0, item, 0, R.B, tok, x, R.B, hidden, sh.act, sh.is);
+    dec_gate_up_item<FMT, kFullK>(smem, ring, sh.gate, sh.up, 0, rg, t0, cnt, tok, x, R.B, hidden, sh.act, sh.is);
     return;
   }
   const int groups_i = (inter + 15) / 16;
@@ -703,8 +706,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
   dec_gate_up_item<FMT, kFullK>(smem, ring, gate, up, sr.expert, rg, sr.t0, sr.cnt, tok, x, R.B, hidden, act, inter);
 }
 
-// Items: the shared expert's down (kShRows row groups each, output BF16
-// y = RNE(acc) into sh.y [B, H]) first, then (block of kDownRows row groups,
+// Items: the shared expert's down (kShRows row groups and 16 tokens each,
+// output BF16 y = RNE(acc) into sh.y [B, H]) first, then (block of kDownRows row groups,
 // expert slot), which store the exact FP32 product f32(RNE(y)) * f32(r)
 // token-major at the route's rank among its token's experts.
 constexpr int kShRows = 2;
@@ -718,14 +721,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
   uint8_t* ring = smem + wave * wave_lds<FMT>();
   const int lane = threadIdx.x & 63, jA = lane >> 4, j = lane & 15;
   const int groups = (hidden + 15) / 16;
-  const int sh_items = sh.is ? (groups + kShRows - 1) / kShRows : 0;
+  const int sh_blocks = (groups + kShRows - 1) / kShRows, passes = (tokens + kPassTokens - 1) / kPassTokens;
+  const int sh_items = sh.is ? sh_blocks * passes : 0;
   const int item = blockIdx.x;
   if (item < sh_items) {
-    const int rg0 = item * kShRows;
+    // item (block of kShRows row groups, pass of 16 tokens)
+    const int rg0 = (item % sh_blocks) * kShRows, t0 = (item / sh_blocks) * kPassTokens;
     const int kb0 = wave * sh.down.kb / ns, kb1 = (wave + 1) * sh.down.kb / ns;
     const WStream<FMT> wd(sh.down, 0, lane);
-    const int nt = tokens;  // <= 16: one pass
-    const XStream<FMT, kFullK> xs(sh.act, tokens, sh.is, j < nt ? j : nt - 1, lane);
+    const int nt = tokens - t0 < kPassTokens ? tokens - t0 : kPassTokens;
+    const XStream<FMT, kFullK> xs(sh.act, tokens, sh.is, t0 + (j < nt ? j : nt - 1), lane);
     f32x4 acc[kShRows];
 #pragma unroll
     for (int r = 0; r < kShRows; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -740,7 +745,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const int row = (rg0 + r) * 16 + 4 * jA + q;
-          if (row < hidden) sh.y[(int64_t)j * hidden + row] = bf16_bits(acc[r][q]);
+          if (row < hidden) sh.y[(int64_t)(t0 + j) * hidden + row] = bf16_bits(acc[r][q]);
         }
     }
     return;
@@ -862,7 +867,9 @@ static int launch(const DecArgs& A, hipStream_t s) {
     attr_done = true;
   }
   const int dn_x = (int)cdiv(groups_h, kDownRows);
-  const int sh_gu = A.S.is ? (int)cdiv(A.S.is, 16) : 0, sh_dn = A.S.is ? (int)cdiv(groups_h, kShRows) : 0;
+  const int passes = (int)cdiv(A.R.B, kPassTokens);
+  const int sh_gu = A.S.is ? (int)cdiv(A.S.is, 16) * passes : 0;
+  const int sh_dn = A.S.is ? (int)cdiv(groups_h, kShRows) * passes : 0;
   const int64_t items_gu = (int64_t)groups_i * A.max_slots + sh_gu, items_dn = (int64_t)dn_x * A.max_slots + sh_dn;
   const int ns_gu = split_for(items_gu), ns_dn = split_for(items_dn);
   hipLaunchKernelGGL((moe_dec_gate_up_kernel<FG, kFullK>), dim3((unsigned)items_gu), dim3(64 * ns_gu),
