@@ -138,6 +138,120 @@ __global__ void gguf_decode_kernel(const uint8_t* __restrict__ raw, int qtype, i
   }
 }
 
+// Vectorised row decode: a workgroup stages NB consecutive blocks (NB * BYTES
+// bytes, a multiple of 4) in LDS with coalesced dword loads, then each thread
+// decodes 16 consecutive values of one block with the formulas of
+// gguf_decode_kernel and stores them as 16-byte vectors. QT: the GGUF type.
+template <int QT>
+struct BlockFmt;
+template <> struct BlockFmt<Q6MOE_Q6_K> { static constexpr int vals = 256, bytes = 210; };
+template <> struct BlockFmt<Q6MOE_Q5_K> { static constexpr int vals = 256, bytes = 176; };
+template <> struct BlockFmt<Q6MOE_Q4_K> { static constexpr int vals = 256, bytes = 144; };
+template <> struct BlockFmt<Q6MOE_Q8_0> { static constexpr int vals = 32, bytes = 34; };
+template <> struct BlockFmt<Q6MOE_Q5_1> { static constexpr int vals = 32, bytes = 24; };
+
+__device__ __forceinline__ float lds_half(const uint8_t* p) {
+  return half_bits_to_float((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+}
+
+// 16 values [part*16, part*16 + 16) of the block at ``b`` (LDS).
+template <int QT>
+__device__ __forceinline__ void decode16(const uint8_t* b, int part, float v[16]) {
+  if constexpr (QT == Q6MOE_Q6_K) {
+    const int p0 = part * 16, h = p0 >> 7, q = (p0 & 127) >> 5, l0 = p0 & 31;
+    const float ds = lds_half(b + 208) * (float)(int8_t)b[192 + part];
+    const uint8_t* ql = b + h * 64 + (q & 1) * 32 + l0;
+    const uint8_t* qh = b + 128 + h * 32 + l0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int lo = (ql[i] >> (4 * (q >> 1))) & 15, hi = (qh[i] >> (2 * q)) & 3;
+      v[i] = ds * (float)((lo | (hi << 4)) - 32);
+    }
+  } else if constexpr (QT == Q6MOE_Q4_K || QT == Q6MOE_Q5_K) {
+    const int j = part >> 1, l0 = (part & 1) * 16;  // sub-block, first position
+    const float d = lds_half(b), dmin = lds_half(b + 2);
+    int sc, mn;
+    if (j < 4) {
+      sc = b[4 + j] & 63;
+      mn = b[8 + j] & 63;
+    } else {
+      sc = (b[12 + j - 4] & 15) | ((b[4 + j - 4] >> 2) & 48);
+      mn = (b[12 + j - 4] >> 4) | ((b[8 + j - 4] >> 2) & 48);
+    }
+    const float a = d * (float)sc, m = dmin * (float)mn;
+    const uint8_t* qs = b + (QT == Q6MOE_Q5_K ? 48 : 16) + (j >> 1) * 32 + l0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      int q = (j & 1) ? (qs[i] >> 4) : (qs[i] & 15);
+      if constexpr (QT == Q6MOE_Q5_K) q |= ((b[16 + l0 + i] >> j) & 1) << 4;
+      v[i] = __builtin_fmaf(a, (float)q, -m);
+    }
+  } else if constexpr (QT == Q6MOE_Q8_0) {
+    const float d = lds_half(b);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = d * (float)(int8_t)b[2 + part * 16 + i];
+  } else {  // Q5_1
+    const float d = lds_half(b), m = lds_half(b + 2);
+    const uint32_t qh = (uint32_t)b[4] | ((uint32_t)b[5] << 8) | ((uint32_t)b[6] << 16) | ((uint32_t)b[7] << 24);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int pos = part * 16 + i;
+      const int nib = part ? (b[8 + i] >> 4) : (b[8 + i] & 15);
+      v[i] = __builtin_fmaf((float)(nib | (int)(((qh >> pos) & 1u) << 4)), d, m);
+    }
+  }
+}
+
+template <int QT>
+__global__ void __launch_bounds__(256)
+    gguf_decode_vec_kernel(const uint8_t* __restrict__ raw, int64_t total_blocks, int blocks, int width,
+                           void* __restrict__ out, int bf16, int vec_out) {
+  constexpr int VALS = BlockFmt<QT>::vals, BYTES = BlockFmt<QT>::bytes;
+  constexpr int TPB = VALS / 16, NB = 256 / TPB;  // threads per block, blocks per workgroup
+  static_assert((NB * BYTES) % 4 == 0, "whole dwords per workgroup");
+  __shared__ __attribute__((aligned(16))) uint8_t st[NB * BYTES];
+  const int64_t b0 = (int64_t)blockIdx.x * NB;
+  const int nb = total_blocks - b0 < NB ? (int)(total_blocks - b0) : NB;
+  const int nbytes = nb * BYTES;
+  const uint8_t* src = raw + b0 * BYTES;
+  for (int i = threadIdx.x; i * 4 < nbytes; i += 256) {
+    if (i * 4 + 4 <= nbytes) {
+      *reinterpret_cast<uint32_t*>(st + 4 * i) = *reinterpret_cast<const uint32_t*>(src + 4 * i);
+    } else {
+      for (int k = 4 * i; k < nbytes; ++k) st[k] = src[k];  // the buffer's last partial dword
+    }
+  }
+  __syncthreads();
+  const int bl = threadIdx.x / TPB, part = threadIdx.x % TPB;
+  if (bl >= nb) return;
+  float v[16];
+  decode16<QT>(st + bl * BYTES, part, v);
+  const int64_t gb = b0 + bl, row = gb / blocks;
+  const int col = (int)(gb - row * blocks) * VALS + part * 16;
+  const int64_t at = row * width + col;
+  if (vec_out && col + 16 <= width && (at & 7) == 0) {
+    if (bf16) {
+      u32x4 o0, o1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o0[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+        o1[i] = pack_bf16x2(v[8 + 2 * i], v[8 + 2 * i + 1]);
+      }
+      u32x4* o = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(out) + at);
+      o[0] = o0;
+      o[1] = o1;
+    } else {
+      f32x4* o = reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + at);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = f32x4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (col + i < width) store_val(out, at + i, v[i], bf16);
+  }
+}
+
 // One thread per (padded row, K block): moves the 208 code/sub-scale bytes into
 // the three regions of its tile and the FP16 d into the scale plane.
 __global__ void q6_pack_kernel(const uint8_t* __restrict__ raw, int n, int kb_count, int tiles,
@@ -212,9 +326,39 @@ extern "C" int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, in
       return Q6MOE_ERR_UNSUPPORTED;
   }
   const int blocks = (int)cdiv(width, vals);
-  const int64_t threads = vals == 32 ? rows * blocks : rows * blocks * 16;
-  hipLaunchKernelGGL(gguf_decode_kernel, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0,
-                     (hipStream_t)stream, raw, qtype, rows, (int)width, blocks, bytes, out,
-                     out_dtype == Q6MOE_BF16);
+  hipStream_t s = (hipStream_t)stream;
+  const int bf16 = out_dtype == Q6MOE_BF16;
+  const int64_t total = rows * blocks;
+  const int vec = aligned(out, 16);
+  if (aligned(raw, 4)) {  // staged through LDS with dword loads
+    const int per_wg = vals == 256 ? 16 : 128;
+    const dim3 grid((unsigned)cdiv(total, per_wg));
+    switch (qtype) {
+      case Q6MOE_Q6_K:
+        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q6_K>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
+                           out, bf16, vec);
+        break;
+      case Q6MOE_Q5_K:
+        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q5_K>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
+                           out, bf16, vec);
+        break;
+      case Q6MOE_Q4_K:
+        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q4_K>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
+                           out, bf16, vec);
+        break;
+      case Q6MOE_Q8_0:
+        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q8_0>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
+                           out, bf16, vec);
+        break;
+      default:
+        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q5_1>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
+                           out, bf16, vec);
+        break;
+    }
+    return check_launch("gguf_decode_vec_kernel");
+  }
+  const int64_t threads = vals == 32 ? total : total * 16;
+  hipLaunchKernelGGL(gguf_decode_kernel, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, s, raw, qtype, rows,
+                     (int)width, blocks, bytes, out, bf16);
   return check_launch("gguf_decode_kernel");
 }

@@ -198,3 +198,26 @@ def test_reference_packer_planes_decode_and_repack_on_device(device, case):
     y = q6_matmul(xb, tdata, tscales, output_features=outputs).cpu().numpy()
     ref_y = packed_q6.projection_reference(xb.float().cpu().numpy(), raw)
     np.testing.assert_allclose(y, ref_y, rtol=2e-5, atol=2e-4)
+
+
+@pytest.mark.parametrize("qtype", ["Q6_K", "Q5_K", "Q4_K", "Q8_0", "Q5_1"])
+def test_dequantize_rows_hip_staged_and_fallback_paths(device, qtype):
+    # 4-byte aligned rows take the LDS-staged vector path, an offset view the
+    # byte path; both are bit-exact, with whole and ragged widths and many
+    # workgroups (more blocks than one workgroup stages).
+    values, size = gguf.block_layout(qtype)
+    rng = np.random.default_rng(19)
+    rows, nb = 70, 5
+    raw = rng.integers(0, 256, (rows, nb, size), dtype=np.uint8)
+    for off in {"Q6_K": (208,), "Q5_K": (0, 2), "Q4_K": (0, 2), "Q8_0": (0,), "Q5_1": (0, 2)}[qtype]:
+        raw[..., off : off + 2] = rng.uniform(-0.3, 0.3, (rows, nb)).astype("<f2").view(np.uint8).reshape(rows, nb, 2)
+    for width in (nb * values, nb * values - 3):
+        want = gguf.dequantize_rows(raw, qtype, width)
+        dev = torch.from_numpy(raw).to(device)
+        got = dequantize_rows(dev, qtype, width).cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        buf = torch.empty(raw.size + 1, dtype=torch.uint8, device=device)
+        buf[1:] = dev.reshape(-1)
+        shifted = buf[1:].view(rows, nb, size)  # 1-byte offset: the byte path
+        got = dequantize_rows(shifted, qtype, width, dtype=torch.bfloat16)
+        np.testing.assert_array_equal(_bf16_bits(got), packed_q6.bf16_bits(want))
