@@ -4,11 +4,14 @@
 //    BF16 through the unit decoder the matmul kernels use, in its exact-sign
 //    form ds * (c - 32) (kaggle/packed_q6/kernel.py:44-62); the matmul form
 //    differs only in the sign of exact zeros.
-//  * gguf_decode_kernel    -- dequantize_rows for raw GGUF rows
-//    (kaggle/glm53_offload/gguf_quant.py:111-173; Q5_1 from
-//    kaggle/qwen38_tpu/quant.py:15-55).
+//  * gguf_decode_vec_kernel / gguf_decode_bytes_kernel / gguf_plain_kernel
+//    -- dequantize_rows for raw GGUF rows of every type the reference decodes
+//    (kaggle/glm53_offload/gguf_quant.py:111-173 and the Q4_0/Q4_1/Q5_0/Q5_1/
+//    IQ4_NL decoder of kaggle/qwen38_tpu/quant.py:15-55).
 //  * q6_pack_kernel        -- pack_q6's byte permutation
 //    (kaggle/packed_q6/layout.py:71-89).
+#include <type_traits>
+
 #include "q6moe_api.h"
 #include "q6moe_device.h"
 
@@ -57,91 +60,7 @@ __device__ __forceinline__ float rd_half(const uint8_t* p) {
   return half_bits_to_float((uint32_t)p[0] | ((uint32_t)p[1] << 8));
 }
 
-// One thread per 16 values of a Q6_K/Q4_K/Q5_K block (16 threads per block) or
-// per 32-value Q8_0/Q5_1 block.
-__global__ void gguf_decode_kernel(const uint8_t* __restrict__ raw, int qtype, int64_t rows,
-                                   int width, int blocks, int block_bytes, void* __restrict__ out,
-                                   int bf16) {
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (qtype == Q6MOE_Q5_1) {
-    // d, m (FP16), 32 high bits, 16 bytes of nibbles: position i < 16 takes the
-    // low nibble of byte i, i >= 16 the high nibble of byte i - 16; bit i of
-    // the high word is bit 4. w = d * q + m (kaggle/qwen38_tpu/quant.py:34-53).
-    if (gid >= rows * blocks) return;
-    const int64_t row = gid / blocks;
-    const int b = (int)(gid % blocks);
-    const uint8_t* blk = raw + gid * block_bytes;
-    const float d = rd_half(blk), m = rd_half(blk + 2);
-    const uint32_t qh = (uint32_t)blk[4] | ((uint32_t)blk[5] << 8) | ((uint32_t)blk[6] << 16) |
-                        ((uint32_t)blk[7] << 24);
-    for (int i = 0; i < 32; ++i) {
-      const int nib = i < 16 ? (blk[8 + i] & 15) : (blk[8 + i - 16] >> 4);
-      const int q = nib | (int)(((qh >> i) & 1u) << 4);
-      const int col = b * 32 + i;
-      if (col < width) store_val(out, row * width + col, __builtin_fmaf((float)q, d, m), bf16);
-    }
-    return;
-  }
-  if (qtype == Q6MOE_Q8_0) {
-    if (gid >= rows * blocks) return;
-    const int64_t row = gid / blocks;
-    const int b = (int)(gid % blocks);
-    const uint8_t* blk = raw + gid * block_bytes;
-    const float d = rd_half(blk);
-    for (int i = 0; i < 32; ++i) {
-      const int col = b * 32 + i;
-      if (col < width) store_val(out, row * width + col, d * (float)(int8_t)blk[2 + i], bf16);
-    }
-    return;
-  }
-  if (gid >= rows * blocks * 16) return;
-  const int sub = (int)(gid & 15);
-  const int64_t rb = gid >> 4;
-  const int64_t row = rb / blocks;
-  const int b = (int)(rb % blocks);
-  const uint8_t* blk = raw + rb * block_bytes;
-  if (qtype == Q6MOE_Q6_K) {
-    const float d = rd_half(blk + 208);
-    const float ds = d * (float)(int8_t)blk[192 + sub];
-    for (int i = 0; i < 16; ++i) {
-      const int p = sub * 16 + i;
-      const int h = p >> 7, q = (p & 127) >> 5, l = p & 31;
-      const int lo = (blk[h * 64 + (q & 1) * 32 + l] >> (4 * (q >> 1))) & 15;
-      const int hi = (blk[128 + h * 32 + l] >> (2 * q)) & 3;
-      const int code = (lo | (hi << 4)) - 32;
-      const int col = b * kQK + p;
-      if (col < width) store_val(out, row * width + col, ds * (float)code, bf16);
-    }
-  } else {  // Q4_K / Q5_K: 8 sub-blocks of 32; thread handles half of one
-    const float d = rd_half(blk), dmin = rd_half(blk + 2);
-    const bool q5 = qtype == Q6MOE_Q5_K;
-    const int j = sub >> 1;  // sub-block 0..7
-    int sc, mn;
-    if (j < 4) {
-      sc = blk[4 + j] & 63;
-      mn = blk[8 + j] & 63;
-    } else {
-      sc = (blk[12 + j - 4] & 15) | ((blk[4 + j - 4] >> 2) & 48);
-      mn = (blk[12 + j - 4] >> 4) | ((blk[8 + j - 4] >> 2) & 48);
-    }
-    const float a = d * (float)sc, m = dmin * (float)mn;
-    // Q5_K: 32 high-bit bytes at 16 (bit j of byte l is bit 4 of sub-block j's
-    // position l), then the nibbles (kaggle/glm53_offload/gguf_quant.py:137-151)
-    const uint8_t* qs = blk + (q5 ? 48 : 16) + (j >> 1) * 32;
-    for (int i = 0; i < 16; ++i) {
-      const int l = (sub & 1) * 16 + i;
-      int q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 15);
-      if (q5) q |= ((blk[16 + l] >> j) & 1) << 4;
-      const int col = b * kQK + j * 32 + l;
-      if (col < width) store_val(out, row * width + col, __builtin_fmaf(a, (float)q, -m), bf16);
-    }
-  }
-}
-
-// Vectorised row decode: a workgroup stages NB consecutive blocks (NB * BYTES
-// bytes, a multiple of 4) in LDS with coalesced dword loads, then each thread
-// decodes 16 consecutive values of one block with the formulas of
-// gguf_decode_kernel and stores them as 16-byte vectors. QT: the GGUF type.
+// Block geometry of the quantized GGUF types: values and bytes per block.
 template <int QT>
 struct BlockFmt;
 template <> struct BlockFmt<Q6MOE_Q6_K> { static constexpr int vals = 256, bytes = 210; };
@@ -149,17 +68,36 @@ template <> struct BlockFmt<Q6MOE_Q5_K> { static constexpr int vals = 256, bytes
 template <> struct BlockFmt<Q6MOE_Q4_K> { static constexpr int vals = 256, bytes = 144; };
 template <> struct BlockFmt<Q6MOE_Q8_0> { static constexpr int vals = 32, bytes = 34; };
 template <> struct BlockFmt<Q6MOE_Q5_1> { static constexpr int vals = 32, bytes = 24; };
+template <> struct BlockFmt<Q6MOE_Q5_0> { static constexpr int vals = 32, bytes = 22; };
+template <> struct BlockFmt<Q6MOE_Q4_1> { static constexpr int vals = 32, bytes = 20; };
+template <> struct BlockFmt<Q6MOE_Q4_0> { static constexpr int vals = 32, bytes = 18; };
+template <> struct BlockFmt<Q6MOE_IQ4_NL> { static constexpr int vals = 32, bytes = 18; };
 
-__device__ __forceinline__ float lds_half(const uint8_t* p) {
-  return half_bits_to_float((uint32_t)p[0] | ((uint32_t)p[1] << 8));
+// The 16 IQ4_NL levels (-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25,
+// 38, 53, 69, 89, 113; kaggle/qwen38_tpu/quant.py:7) as the bytes of four words.
+__device__ __forceinline__ int iq4_level(int nib) {
+  const uint32_t w = nib < 8 ? (nib < 4 ? 0xBFAD9881u : 0xF6EADDCFu) : (nib < 12 ? 0x26190D01u : 0x71594535u);
+  return (int)(int8_t)(w >> (8 * (nib & 3)));
 }
 
-// 16 values [part*16, part*16 + 16) of the block at ``b`` (LDS).
+// 16 values [part*16, part*16 + 16) of the block at ``b`` (LDS or global).
+//  * Q6_K: ds * (code - 32), ds = d * int8 sub-scale (gguf_quant.py:158-173).
+//  * Q4_K/Q5_K: fma(d*sc, q, -(dmin*m)) with the 6-bit packed sub-scales and
+//    mins; Q5_K's 32 high-bit bytes at 16 (bit j of byte l is bit 4 of
+//    sub-block j's position l), then the nibbles (gguf_quant.py:115-157).
+//  * Q8_0: d * int8 code (gguf_quant.py:111-114).
+//  * 32-value nibble types (kaggle/qwen38_tpu/quant.py:15-55): d (FP16), then
+//    m (FP16) for the affine Q4_1/Q5_1, then 32 high bits for Q5_0/Q5_1, then
+//    16 bytes whose low nibbles are positions 0-15 and high nibbles 16-31; bit
+//    i of the high word is bit 4 of position i. w = d*q + m (affine), d*(q-8)
+//    (Q4_0), d*(q-16) (Q5_0), d*level[q] (IQ4_NL). Every product d*q here has
+//    at most 18 significant bits, so it is exact in FP32 and the affine sum is
+//    one rounding, as in the reference's two-step d*q then +m.
 template <int QT>
 __device__ __forceinline__ void decode16(const uint8_t* b, int part, float v[16]) {
   if constexpr (QT == Q6MOE_Q6_K) {
     const int p0 = part * 16, h = p0 >> 7, q = (p0 & 127) >> 5, l0 = p0 & 31;
-    const float ds = lds_half(b + 208) * (float)(int8_t)b[192 + part];
+    const float ds = rd_half(b + 208) * (float)(int8_t)b[192 + part];
     const uint8_t* ql = b + h * 64 + (q & 1) * 32 + l0;
     const uint8_t* qh = b + 128 + h * 32 + l0;
 #pragma unroll
@@ -169,7 +107,7 @@ __device__ __forceinline__ void decode16(const uint8_t* b, int part, float v[16]
     }
   } else if constexpr (QT == Q6MOE_Q4_K || QT == Q6MOE_Q5_K) {
     const int j = part >> 1, l0 = (part & 1) * 16;  // sub-block, first position
-    const float d = lds_half(b), dmin = lds_half(b + 2);
+    const float d = rd_half(b), dmin = rd_half(b + 2);
     int sc, mn;
     if (j < 4) {
       sc = b[4 + j] & 63;
@@ -187,21 +125,63 @@ __device__ __forceinline__ void decode16(const uint8_t* b, int part, float v[16]
       v[i] = __builtin_fmaf(a, (float)q, -m);
     }
   } else if constexpr (QT == Q6MOE_Q8_0) {
-    const float d = lds_half(b);
+    const float d = rd_half(b);
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = d * (float)(int8_t)b[2 + part * 16 + i];
-  } else {  // Q5_1
-    const float d = lds_half(b), m = lds_half(b + 2);
-    const uint32_t qh = (uint32_t)b[4] | ((uint32_t)b[5] << 8) | ((uint32_t)b[6] << 16) | ((uint32_t)b[7] << 24);
+  } else {
+    constexpr bool affine = QT == Q6MOE_Q4_1 || QT == Q6MOE_Q5_1;
+    constexpr bool wide = QT == Q6MOE_Q5_0 || QT == Q6MOE_Q5_1;
+    constexpr int hi_at = affine ? 4 : 2, lo_at = hi_at + (wide ? 4 : 0);
+    const float d = rd_half(b);
+    const float m = affine ? rd_half(b + 2) : 0.0f;
+    uint32_t qh = 0;
+    if constexpr (wide)
+      qh = (uint32_t)b[hi_at] | ((uint32_t)b[hi_at + 1] << 8) | ((uint32_t)b[hi_at + 2] << 16) |
+           ((uint32_t)b[hi_at + 3] << 24);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int pos = part * 16 + i;
-      const int nib = part ? (b[8 + i] >> 4) : (b[8 + i] & 15);
-      v[i] = __builtin_fmaf((float)(nib | (int)(((qh >> pos) & 1u) << 4)), d, m);
+      const int nib = part ? (b[lo_at + i] >> 4) : (b[lo_at + i] & 15);
+      const int q = wide ? nib | (int)(((qh >> (part * 16 + i)) & 1u) << 4) : nib;
+      if constexpr (QT == Q6MOE_IQ4_NL)
+        v[i] = d * (float)iq4_level(nib);
+      else if constexpr (affine)
+        v[i] = __builtin_fmaf((float)q, d, m);
+      else
+        v[i] = d * (float)(q - (wide ? 16 : 8));
     }
   }
 }
 
+// Stores the 16 values of (row, col) as 16-byte vectors when the target is
+// aligned and whole, else value by value (the row's tail).
+__device__ __forceinline__ void store16(void* out, int64_t at, int col, int width, const float v[16], int bf16,
+                                        int vec_out) {
+  if (vec_out && col + 16 <= width && (at & 7) == 0) {
+    if (bf16) {
+      u32x4 o0, o1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o0[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
+        o1[i] = pack_bf16x2(v[8 + 2 * i], v[8 + 2 * i + 1]);
+      }
+      u32x4* o = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(out) + at);
+      o[0] = o0;
+      o[1] = o1;
+    } else {
+      f32x4* o = reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + at);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = f32x4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (col + i < width) store_val(out, at + i, v[i], bf16);
+  }
+}
+
+// Row decode for 4-byte aligned input: a workgroup stages NB consecutive blocks
+// (NB * BYTES bytes, a multiple of 4) in LDS with coalesced dword loads, then
+// each thread decodes 16 consecutive values of one block.
 template <int QT>
 __global__ void __launch_bounds__(256)
     gguf_decode_vec_kernel(const uint8_t* __restrict__ raw, int64_t total_blocks, int blocks, int width,
@@ -228,28 +208,43 @@ __global__ void __launch_bounds__(256)
   decode16<QT>(st + bl * BYTES, part, v);
   const int64_t gb = b0 + bl, row = gb / blocks;
   const int col = (int)(gb - row * blocks) * VALS + part * 16;
-  const int64_t at = row * width + col;
-  if (vec_out && col + 16 <= width && (at & 7) == 0) {
-    if (bf16) {
-      u32x4 o0, o1;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        o0[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
-        o1[i] = pack_bf16x2(v[8 + 2 * i], v[8 + 2 * i + 1]);
-      }
-      u32x4* o = reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(out) + at);
-      o[0] = o0;
-      o[1] = o1;
-    } else {
-      f32x4* o = reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + at);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = f32x4{v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
-    }
+  store16(out, row * width + col, col, width, v, bf16, vec_out);
+}
+
+// Row decode for input at any byte address: one thread per 16 values, reading
+// its block's bytes from global memory.
+template <int QT>
+__global__ void __launch_bounds__(256)
+    gguf_decode_bytes_kernel(const uint8_t* __restrict__ raw, int64_t total_blocks, int blocks, int width,
+                             void* __restrict__ out, int bf16, int vec_out) {
+  constexpr int VALS = BlockFmt<QT>::vals, BYTES = BlockFmt<QT>::bytes, TPB = VALS / 16;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= total_blocks * TPB) return;
+  const int64_t gb = gid / TPB;
+  const int part = (int)(gid % TPB);
+  float v[16];
+  decode16<QT>(raw + gb * BYTES, part, v);
+  const int64_t row = gb / blocks;
+  const int col = (int)(gb - row * blocks) * VALS + part * 16;
+  store16(out, row * width + col, col, width, v, bf16, vec_out);
+}
+
+// Unquantized rows (F32, F16, BF16; one value per "block"): the float value,
+// then the output rounding. Little-endian element bytes at any alignment.
+__global__ void __launch_bounds__(256) gguf_plain_kernel(const uint8_t* __restrict__ raw, int qtype, int64_t n,
+                                                         void* __restrict__ out, int bf16) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float v;
+  if (qtype == Q6MOE_GGUF_F32) {
+    const uint8_t* p = raw + 4 * i;
+    v = __uint_as_float((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24));
   } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i)
-      if (col + i < width) store_val(out, at + i, v[i], bf16);
+    const uint8_t* p = raw + 2 * i;
+    const uint32_t h = (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+    v = qtype == Q6MOE_GGUF_F16 ? half_bits_to_float(h) : __uint_as_float(h << 16);
   }
+  store_val(out, i, v, bf16);
 }
 
 // One thread per (padded row, K block): moves the 208 code/sub-scale bytes into
@@ -314,51 +309,44 @@ extern "C" int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, in
   Q6MOE_REQUIRE(raw && out, "gguf_decode: null pointer");
   Q6MOE_REQUIRE(rows >= 1 && width >= 1 && width <= (1 << 30), "gguf_decode: bad shape");
   Q6MOE_REQUIRE(out_dtype == Q6MOE_F32 || out_dtype == Q6MOE_BF16, "gguf_decode: out dtype");
-  int vals, bytes;
-  switch (qtype) {
-    case Q6MOE_Q6_K: vals = 256; bytes = 210; break;
-    case Q6MOE_Q4_K: vals = 256; bytes = 144; break;
-    case Q6MOE_Q8_0: vals = 32; bytes = 34; break;
-    case Q6MOE_Q5_K: vals = 256; bytes = 176; break;
-    case Q6MOE_Q5_1: vals = 32; bytes = 24; break;
-    default:
-      set_error("gguf_decode: unsupported GGUF quantization type (Q6_K, Q5_K, Q4_K, Q8_0, Q5_1 only)");
-      return Q6MOE_ERR_UNSUPPORTED;
-  }
-  const int blocks = (int)cdiv(width, vals);
   hipStream_t s = (hipStream_t)stream;
   const int bf16 = out_dtype == Q6MOE_BF16;
-  const int64_t total = rows * blocks;
-  const int vec = aligned(out, 16);
-  if (aligned(raw, 4)) {  // staged through LDS with dword loads
-    const int per_wg = vals == 256 ? 16 : 128;
-    const dim3 grid((unsigned)cdiv(total, per_wg));
-    switch (qtype) {
-      case Q6MOE_Q6_K:
-        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q6_K>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
-                           out, bf16, vec);
-        break;
-      case Q6MOE_Q5_K:
-        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q5_K>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
-                           out, bf16, vec);
-        break;
-      case Q6MOE_Q4_K:
-        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q4_K>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
-                           out, bf16, vec);
-        break;
-      case Q6MOE_Q8_0:
-        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q8_0>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
-                           out, bf16, vec);
-        break;
-      default:
-        hipLaunchKernelGGL(gguf_decode_vec_kernel<Q6MOE_Q5_1>, grid, dim3(256), 0, s, raw, total, blocks, (int)width,
-                           out, bf16, vec);
-        break;
-    }
-    return check_launch("gguf_decode_vec_kernel");
+  if (qtype == Q6MOE_GGUF_F32 || qtype == Q6MOE_GGUF_F16 || qtype == Q6MOE_GGUF_BF16) {
+    const int64_t n = rows * width;
+    hipLaunchKernelGGL(gguf_plain_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, s, raw, qtype, n, out, bf16);
+    return check_launch("gguf_plain_kernel");
   }
-  const int64_t threads = vals == 32 ? total : total * 16;
-  hipLaunchKernelGGL(gguf_decode_kernel, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, s, raw, qtype, rows,
-                     (int)width, blocks, bytes, out, bf16);
-  return check_launch("gguf_decode_kernel");
+  const int vec = aligned(out, 16);
+  const bool staged = aligned(raw, 4);  // staged through LDS with dword loads
+  int rc = Q6MOE_ERR_UNSUPPORTED;
+  auto run = [&](auto qt) {
+    constexpr int QT = decltype(qt)::value, VALS = BlockFmt<QT>::vals;
+    const int blocks = (int)cdiv(width, VALS);
+    const int64_t total = rows * blocks;
+    if (staged) {
+      hipLaunchKernelGGL(gguf_decode_vec_kernel<QT>, dim3((unsigned)cdiv(total, 256 / (VALS / 16))), dim3(256), 0,
+                         s, raw, total, blocks, (int)width, out, bf16, vec);
+      rc = check_launch("gguf_decode_vec_kernel");
+    } else {
+      hipLaunchKernelGGL(gguf_decode_bytes_kernel<QT>, dim3((unsigned)cdiv(total * (VALS / 16), 256)), dim3(256),
+                         0, s, raw, total, blocks, (int)width, out, bf16, vec);
+      rc = check_launch("gguf_decode_bytes_kernel");
+    }
+  };
+  switch (qtype) {
+    case Q6MOE_Q6_K: run(std::integral_constant<int, Q6MOE_Q6_K>{}); break;
+    case Q6MOE_Q5_K: run(std::integral_constant<int, Q6MOE_Q5_K>{}); break;
+    case Q6MOE_Q4_K: run(std::integral_constant<int, Q6MOE_Q4_K>{}); break;
+    case Q6MOE_Q8_0: run(std::integral_constant<int, Q6MOE_Q8_0>{}); break;
+    case Q6MOE_Q5_1: run(std::integral_constant<int, Q6MOE_Q5_1>{}); break;
+    case Q6MOE_Q5_0: run(std::integral_constant<int, Q6MOE_Q5_0>{}); break;
+    case Q6MOE_Q4_1: run(std::integral_constant<int, Q6MOE_Q4_1>{}); break;
+    case Q6MOE_Q4_0: run(std::integral_constant<int, Q6MOE_Q4_0>{}); break;
+    case Q6MOE_IQ4_NL: run(std::integral_constant<int, Q6MOE_IQ4_NL>{}); break;
+    default:
+      set_error("gguf_decode: unsupported GGUF type (F32, F16, BF16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, "
+                "Q6_K, IQ4_NL)");
+      return Q6MOE_ERR_UNSUPPORTED;
+  }
+  return rc;
 }

@@ -17,7 +17,10 @@ Q8_0 = 8
 Q4_K = 12
 Q5_K = 13
 Q6_K = 14
+# expert-table formats of the routed FFN
 QTYPE_CODES = {"Q5_1": Q5_1, "Q8_0": Q8_0, "Q4_K": Q4_K, "Q5_K": Q5_K, "Q6_K": Q6_K}
+# every GGUF tensor type q6moe_gguf_decode takes (GGMLQuantizationType values)
+GGUF_TYPE_CODES = dict(QTYPE_CODES, F32=0, F16=1, Q4_0=2, Q4_1=3, Q5_0=6, IQ4_NL=20, BF16=30)
 
 ERRORS = {-1: "invalid argument", -2: "HIP error", -3: "unsupported"}
 

@@ -1,10 +1,9 @@
 """GGUF row decoding on the GPU: ``block_layout`` and ``dequantize_rows``.
 
 Mirrors kaggle/glm53_offload/gguf_quant.py:57-60,180-216 (and the layout
-table and Q5_1 decoder of kaggle/qwen38_tpu/quant.py:7-55) with a
-``backend="hip"`` decoder for the expert formats Q6_K, Q5_K, Q4_K, Q8_0 and
-Q5_1. Output is FP32 or BF16 (RNE of the
-FP32 value, as ``astype(bfloat16)`` does).
+table and Q4_0/Q4_1/Q5_0/Q5_1/IQ4_NL decoder of kaggle/qwen38_tpu/quant.py:7-55)
+with a ``backend="hip"`` decoder for every type in ``BLOCK_LAYOUTS``. Output is
+FP32 or BF16 (RNE of the FP32 value, as ``astype(bfloat16)`` does).
 """
 
 import torch
@@ -25,7 +24,7 @@ BLOCK_LAYOUTS = {
     "Q5_1": (32, 24),
     "IQ4_NL": (32, 18),
 }
-DEVICE_TYPES = ("Q6_K", "Q5_K", "Q4_K", "Q8_0", "Q5_1")
+DEVICE_TYPES = tuple(BLOCK_LAYOUTS)
 # GGMLQuantizationType values of the named formats (GGUF file format)
 _GGML_IDS = {0: "F32", 1: "F16", 8: "Q8_0", 12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 30: "BF16"}
 
@@ -96,7 +95,7 @@ def dequantize_rows(raw, qtype, row_width, dtype=None, backend="hip"):
     lib = _lib.load()
     with torch.cuda.device(raw.device):
         rc = lib.q6moe_gguf_decode(
-            _lib.ptr(raw.contiguous()), _lib.QTYPE_CODES[name], rows, row_width, _lib.ptr(out),
+            _lib.ptr(raw.contiguous()), _lib.GGUF_TYPE_CODES[name], rows, row_width, _lib.ptr(out),
             _lib.BF16 if dtype == torch.bfloat16 else _lib.F32, _lib.stream_handle(raw.device),
         )
     _lib.check(rc, "dequantize_rows")

@@ -45,12 +45,19 @@ extern "C" {
 #define Q6MOE_F32 0
 #define Q6MOE_BF16 1
 
-/* GGUF block types (values of GGMLQuantizationType) */
+/* GGUF tensor types (values of GGMLQuantizationType) */
+#define Q6MOE_GGUF_F32 0
+#define Q6MOE_GGUF_F16 1
+#define Q6MOE_Q4_0 2
+#define Q6MOE_Q4_1 3
+#define Q6MOE_Q5_0 6
 #define Q6MOE_Q5_1 7
 #define Q6MOE_Q8_0 8
 #define Q6MOE_Q4_K 12
 #define Q6MOE_Q5_K 13
 #define Q6MOE_Q6_K 14
+#define Q6MOE_IQ4_NL 20
+#define Q6MOE_GGUF_BF16 30
 
 /* Library version (major*10000 + minor*100 + patch). */
 int q6moe_version(void);
@@ -87,9 +94,10 @@ int q6moe_q6_pack(const uint8_t* raw, int64_t n, int64_t k, uint8_t* data, uint8
                   void* stream);
 
 /*
- * dequantize_rows(raw, qtype, width) for Q6_K, Q5_K, Q4_K, Q8_0 and Q5_1 on device
- * (kaggle/glm53_offload/gguf_quant.py:180-216, kaggle/qwen38_tpu/quant.py:15-55):
- * raw [rows, ceil(width/vals), bytes]
+ * dequantize_rows(raw, qtype, width) on device for every type the reference decodes:
+ * Q6_K, Q5_K, Q4_K, Q8_0 (kaggle/glm53_offload/gguf_quant.py:180-216), Q4_0, Q4_1,
+ * Q5_0, Q5_1, IQ4_NL (kaggle/qwen38_tpu/quant.py:15-55) and F32, F16, BF16:
+ * raw [rows, ceil(width/vals), bytes] (any byte alignment)
  * -> out [rows, width] as FP32 or BF16 (RNE of the FP32 value).
  */
 int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, int64_t width, void* out,

@@ -17,15 +17,19 @@ gguf.dequantize_rows        gguf-py 0.19.0 frozen vectors
                             data file the reference ships) for Q4_K, Q5_K,
                             Q6_K, Q8_0, F16, BF16, F32; the scalar per-position
                             Q6_K oracle below; closed-form Q5_1/IQ4_NL
-                            enumerations from the reference's tests.
+                            enumerations from the reference's tests; scalar
+                            per-value Q4_0/Q4_1/Q5_0 restatements of the GGML
+                            block definitions with random FP16 d and m.
 packed_q6.decode_reference  agreement with gguf.dequantize_rows (independent
                             formulation) and the gguf-py vectors.
 packed_q6.bf16_round        exhaustive: every BF16 bin at 0x0000/0x7FFF/
                             0x8000/0x8001 low halves against torch's RNE cast.
 packed_q6.fp16_bits_to_f32  exhaustive over all 63 488 finite FP16 patterns
                             against numpy's IEEE conversion.
-packed_q6.soa_offsets       round trip against the product packer plus a
-                            hand-worked byte map (a plain permutation).
+packed_q6.soa_offsets       planes written by the reference's own pack_q6
+                            (tests/golden/packed_q6_soa_reference.npz, made
+                            by tests/golden/make_soa_golden.py); round trip
+                            against the product packer; a plain permutation.
 packed_q6.projection_ref    FP64 dot of BF16-rounded operands; closed-form
                             checks (identity-like weights, linearity in x).
 numerics.sigmoid/softmax    FP64 closed form, 2-ulp budget.

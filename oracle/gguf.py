@@ -95,7 +95,7 @@ def _decode_block(raw, qtype):
             *raw.shape[:-1], 16, 16
         ).astype(np.float32)
         return w.reshape(*raw.shape[:-1], 256)
-    if qtype in ("Q4_0", "Q4_1", "Q5_0", "Q5_1", "IQ4_NL"):  # quant.py:234-274
+    if qtype in ("Q4_0", "Q4_1", "Q5_0", "Q5_1", "IQ4_NL"):  # kaggle/qwen38_tpu/quant.py:28-55
         affine = qtype in ("Q4_1", "Q5_1")
         base = 4 if affine else 2
         wide = qtype.startswith("Q5")

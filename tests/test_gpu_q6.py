@@ -152,22 +152,46 @@ def test_device_pack_matches_host_pack(device, outputs, inputs):
     np.testing.assert_array_equal(scales.cpu().numpy(), host.scales)
 
 
-@pytest.mark.parametrize("qtype", ["Q6_K", "Q5_K", "Q4_K", "Q8_0", "Q5_1"])
+ALL_GGUF_TYPES = ["Q6_K", "Q5_K", "Q4_K", "Q8_0", "Q5_1", "Q5_0", "Q4_1", "Q4_0", "IQ4_NL", "F16", "BF16", "F32"]
+_SCALE_AT = {"Q6_K": (208,), "Q5_K": (0, 2), "Q4_K": (0, 2), "Q8_0": (0,), "Q5_1": (0, 2), "Q5_0": (0,),
+             "Q4_1": (0, 2), "Q4_0": (0,), "IQ4_NL": (0,)}
+
+
+def _random_rows(qtype, rows, nb, rng):
+    """Random GGUF rows of ``nb`` blocks with finite FP16 scales; for the
+    unquantized types finite values incl. signed zeros, subnormals and +-inf."""
+    values, size = gguf.block_layout(qtype)
+    if qtype in _SCALE_AT:
+        raw = rng.integers(0, 256, (rows, nb, size), dtype=np.uint8)
+        for off in _SCALE_AT[qtype]:
+            raw[..., off : off + 2] = rng.uniform(-0.3, 0.3, (rows, nb)).astype("<f2").view(np.uint8).reshape(
+                rows, nb, 2)
+        return raw
+    special = np.array([0.0, -0.0, np.inf, -np.inf, 1e-40, -3e-39, 6e-8, 65504.0], np.float32)
+    v = rng.normal(0, 100, (rows, nb)).astype(np.float32)
+    v.reshape(-1)[:: 7] = special[rng.integers(0, special.size, v.reshape(-1)[:: 7].size)]
+    if qtype == "F32":
+        return v.astype("<f4").view(np.uint8).reshape(rows, nb, 4)
+    if qtype == "F16":
+        return v.astype("<f2").view(np.uint8).reshape(rows, nb, 2)
+    return (v.view(np.uint32) >> 16).astype("<u2").view(np.uint8).reshape(rows, nb, 2)  # BF16 (truncated)
+
+
+@pytest.mark.parametrize("qtype", ALL_GGUF_TYPES)
 def test_dequantize_rows_hip_matches_oracle_and_frozen_vectors(device, qtype):
     from .conftest import GOLDEN
 
     values, size = gguf.block_layout(qtype)
     ref = np.load(GOLDEN / "gguf_py_decoder_reference.npz")
-    if f"{qtype}_raw" in ref.files:  # gguf-py 0.19.0 vectors (none exist for Q5_1)
+    if f"{qtype}_raw" in ref.files:  # gguf-py 0.19.0 vectors (Q6_K, Q5_K, Q4_K, Q8_0, F16, BF16, F32)
         raw = ref[f"{qtype}_raw"]
         width = raw.shape[-2] * values
         got = dequantize_rows(torch.from_numpy(raw).to(device), qtype, width).cpu().numpy()
         np.testing.assert_array_equal(got.view(np.uint32), ref[f"{qtype}_expected"].view(np.uint32))
     rng = np.random.default_rng(8)
-    raw = rng.integers(0, 256, (37, 3, size), dtype=np.uint8)
-    for off in {"Q6_K": (208,), "Q5_K": (0, 2), "Q4_K": (0, 2), "Q8_0": (0,), "Q5_1": (0, 2)}[qtype]:
-        raw[..., off : off + 2] = rng.uniform(-0.3, 0.3, (37, 3)).astype("<f2").view(np.uint8).reshape(37, 3, 2)
-    width = 3 * values - 5
+    nb = 3 if values > 1 else 301
+    raw = _random_rows(qtype, 37, nb, rng)
+    width = nb * values - (5 if values > 1 else 0)
     want = gguf.dequantize_rows(raw, qtype, width)
     got = dequantize_rows(torch.from_numpy(raw).to(device), qtype, width).cpu().numpy()
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
@@ -200,18 +224,16 @@ def test_reference_packer_planes_decode_and_repack_on_device(device, case):
     np.testing.assert_allclose(y, ref_y, rtol=2e-5, atol=2e-4)
 
 
-@pytest.mark.parametrize("qtype", ["Q6_K", "Q5_K", "Q4_K", "Q8_0", "Q5_1"])
+@pytest.mark.parametrize("qtype", ALL_GGUF_TYPES)
 def test_dequantize_rows_hip_staged_and_fallback_paths(device, qtype):
     # 4-byte aligned rows take the LDS-staged vector path, an offset view the
     # byte path; both are bit-exact, with whole and ragged widths and many
     # workgroups (more blocks than one workgroup stages).
     values, size = gguf.block_layout(qtype)
     rng = np.random.default_rng(19)
-    rows, nb = 70, 5
-    raw = rng.integers(0, 256, (rows, nb, size), dtype=np.uint8)
-    for off in {"Q6_K": (208,), "Q5_K": (0, 2), "Q4_K": (0, 2), "Q8_0": (0,), "Q5_1": (0, 2)}[qtype]:
-        raw[..., off : off + 2] = rng.uniform(-0.3, 0.3, (rows, nb)).astype("<f2").view(np.uint8).reshape(rows, nb, 2)
-    for width in (nb * values, nb * values - 3):
+    rows, nb = 70, (5 if values > 1 else 333)
+    raw = _random_rows(qtype, rows, nb, rng)
+    for width in ((nb * values, nb * values - 3) if values > 1 else (nb,)):
         want = gguf.dequantize_rows(raw, qtype, width)
         dev = torch.from_numpy(raw).to(device)
         got = dequantize_rows(dev, qtype, width).cpu().numpy()

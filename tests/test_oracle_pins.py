@@ -123,6 +123,41 @@ def test_extra_block_types_closed_form(qtype):
     np.testing.assert_array_equal(gguf.dequantize_rows(raw, qtype, width), expected)
 
 
+@pytest.mark.parametrize("qtype", ["Q4_0", "Q4_1", "Q5_0"])
+def test_legacy_block_types_closed_form(qtype):
+    # Per-value scalar restatement of the GGML block definitions the reference's
+    # decoder follows (kaggle/qwen38_tpu/quant.py:15-55): FP16 d [, FP16 m]
+    # [, 32-bit high word], 16 nibble bytes (position i: byte i % 16, nibble
+    # i // 16); value d * (q - 8), d * q + m, d * (q - 16). Random FP16 d and m,
+    # expected values formed in float64 (exact here) and rounded once.
+    size = {"Q4_0": 18, "Q4_1": 20, "Q5_0": 22}[qtype]
+    rng = np.random.default_rng(75)
+    raw = rng.integers(0, 256, (3, 4, size), dtype=np.uint8)
+    d = rng.uniform(-0.5, 0.5, (3, 4)).astype(np.float16)
+    m = rng.uniform(-0.5, 0.5, (3, 4)).astype(np.float16)
+    raw[..., 0:2] = d.astype("<f2").view(np.uint8).reshape(3, 4, 2)
+    if qtype == "Q4_1":
+        raw[..., 2:4] = m.astype("<f2").view(np.uint8).reshape(3, 4, 2)
+    expected = np.zeros((3, 128), np.float64)
+    for r in range(3):
+        for b in range(4):
+            blk = raw[r, b]
+            for i in range(32):
+                if qtype == "Q5_0":
+                    high = int.from_bytes(blk[2:6].tobytes(), "little")
+                    q = ((int(blk[6 + i % 16]) >> (4 * (i // 16))) & 15) | (((high >> i) & 1) << 4)
+                    v = float(d[r, b]) * (q - 16)
+                elif qtype == "Q4_1":
+                    q = (int(blk[4 + i % 16]) >> (4 * (i // 16))) & 15
+                    v = float(d[r, b]) * q + float(m[r, b])
+                else:
+                    q = (int(blk[2 + i % 16]) >> (4 * (i // 16))) & 15
+                    v = float(d[r, b]) * (q - 8)
+                expected[r, 32 * b + i] = v
+    got = gguf.dequantize_rows(raw, qtype, 128 - 7)
+    np.testing.assert_array_equal(got, expected[:, : 128 - 7].astype(np.float32))
+
+
 def test_sigmoid_and_silu_against_fp64():
     x = np.concatenate([np.linspace(-30, 30, 20001), [0.0, -0.0, 1e-30, -1e-30]]).astype(np.float32)
     exact = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
