@@ -199,25 +199,34 @@ def clone_tables(tabs):
     return [type(t)(t.qtype, t.data.clone(), None, t.rows, t.width) for t in tabs]
 
 
-def cpu_oracle_moe(L, rows, types, hidden, inter, shared=None, reps=1):
+def cpu_repeat(fn, min_seconds, min_runs=1):
+    """Runs fn until ``min_runs`` runs and ``min_seconds`` of CPU time have
+    passed; returns (last result, median seconds per run, runs)."""
+    times, out = [], None
+    while len(times) < min_runs or sum(times) < min_seconds:
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return out, times[len(times) // 2], len(times)
+
+
+def cpu_oracle_moe(L, rows, types, hidden, inter, shared=None, min_seconds=0.0):
     """CPU baseline leg: the NumPy oracle on ``rows`` tokens of L with
-    cpu_threads() threads (a pool over experts, one BLAS thread each);
-    returns (output, seconds per run, threads)."""
+    cpu_threads() threads (a pool over experts, one BLAS thread each), repeated
+    for at least ``min_seconds``; returns (output, median seconds per run,
+    threads, runs)."""
     from threadpoolctl import threadpool_limits
 
     from oracle import moe as oracle_moe
 
     n = cpu_threads()
-    times, out = [], None
     with threadpool_limits(1):
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            out = oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"][rows], L["ids"][rows],
-                                        L["weights"][rows], types=types, hidden=hidden, intermediate=inter,
-                                        shared=shared, workers=n)
-            times.append(time.perf_counter() - t0)
-    times.sort()
-    return out, times[len(times) // 2], n
+        out, secs, runs = cpu_repeat(
+            lambda: oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"][rows], L["ids"][rows],
+                                          L["weights"][rows], types=types, hidden=hidden, intermediate=inter,
+                                          shared=shared, workers=n), min_seconds)
+    return out, secs, n, runs
 
 
 class MoeGemmBaselines:
@@ -307,19 +316,15 @@ def measure_projection(dev, with_cpu):
         from oracle import packed_q6
 
         n = cpu_threads()
-        times = []
+        xf = x.float().cpu().numpy()
         with threadpool_limits(n):
-            for _ in range(20):
-                t0 = time.perf_counter()
-                want = packed_q6.projection_reference(x.float().cpu().numpy(), w["raw"])
-                times.append(time.perf_counter() - t0)
+            want, secs, runs = cpu_repeat(lambda: packed_q6.projection_reference(xf, w["raw"]), 3.0, 20)
         np.testing.assert_allclose(y32, want, rtol=2e-5, atol=2e-4)
         err = y32.astype(np.float64) - want
         res["check"] = {"passed": True, "rtol": 2e-5, "atol": 2e-4, "max_abs_error": float(np.abs(err).max())}
-        secs = float(np.median(times))
         res["cpu_baseline"] = {"value": round(8 / secs, 1), "unit": "tokens/s", "cores": n, "kind": "port",
                                "sample": f"the whole projection (decode of W, FP64 product) by the NumPy oracle, "
-                                         f"median of 20 runs: {secs * 1e3:.2f} ms"}
+                                         f"median of {runs} runs: {secs * 1e3:.2f} ms"}
     lib = _lib.load()
     yb = torch.empty((8, 768), dtype=torch.bfloat16, device=dev)
     stream = lambda: _lib.stream_handle(dev)  # noqa: E731
@@ -410,15 +415,15 @@ def measure_prefill(dev, steps, warmup, with_cpu):
     if not np.isfinite(got).all():
         raise CheckFailed("prefill: nonfinite output rejected before timing")
     if with_cpu:
-        rows = np.random.default_rng(7).choice(PREFILL_TOKENS, 128, replace=False)
+        rows = np.random.default_rng(7).choice(PREFILL_TOKENS, 1024, replace=False)
         rows.sort()
-        want, secs, n = cpu_oracle_moe(L, rows, ("Q6_K",) * 3, HIDDEN, INTER)
+        want, secs, n, runs = cpu_oracle_moe(L, rows, ("Q6_K",) * 3, HIDDEN, INTER, min_seconds=8.0)
         res["check"] = dict(check_close("prefill", got[rows], want), sample_tokens=int(rows.size))
         flops = 2 * rows.size * TOP_K * 3 * HIDDEN * INTER
         res["cpu_baseline"] = {"value": round(flops / secs / 1e12, 6), "unit": "TFLOP/s", "cores": n,
                                "kind": "port", "tokens_per_s": round(rows.size / secs, 1),
-                               "sample": f"128 of the 4096 tokens (all their routes) by the NumPy oracle: "
-                                         f"{secs:.2f} s"}
+                               "sample": f"1024 of the 4096 tokens (all their routes) by the NumPy oracle, "
+                                         f"median of {runs} runs: {secs:.2f} s"}
     for _ in range(warmup):
         fn(*tabs, x, ids, w, workspace=ws, out=out)
     t = timed_reps({"fused": lambda i: fn(*tabs, x, ids, w, workspace=ws, out=out)}, inner=max(1, steps // 5))
@@ -491,11 +496,13 @@ def measure_q4_shared(dev, with_cpu):
         if not np.isfinite(got).all():
             raise CheckFailed(f"q4k_shared B={b}: nonfinite output rejected before timing")
         if with_cpu:
-            want, secs, n = cpu_oracle_moe(L, slice(0, b), ("Q4_K",) * 3, H4, I4, shared=shared_dec)
+            want, secs, n, runs = cpu_oracle_moe(L, slice(0, b), ("Q4_K",) * 3, H4, I4, shared=shared_dec,
+                                                 min_seconds=3.0)
             row["check"] = check_close(f"q4k_shared B={b}", got, want)
             row["cpu_baseline"] = {"value": round(nbytes / secs / 1e9, 4), "unit": "GB/s", "cores": n,
                                    "kind": "port", "tokens_per_s": round(b / secs, 2),
-                                   "sample": f"the whole {b}-token step by the NumPy oracle: {secs:.2f} s"}
+                                   "sample": f"the whole {b}-token step by the NumPy oracle, median of {runs} "
+                                             f"runs: {secs:.2f} s"}
         t = timed_reps({"fused": call}, inner=20)
         us = t["fused"]["median"]
         ph = phase_means(call, 50)
@@ -586,10 +593,8 @@ def measure_kv(dev, with_cpu):
             idx = c[None, :].astype(np.int32)
             return oracle_kv.read_paged(K["k"], K["k_scale"], K["page_table"][:1], P, H, D, D, idx)
 
-        t0 = time.perf_counter()
         with ThreadPoolExecutor(n) as pool:
-            want = np.concatenate(list(pool.map(part, chunks)), axis=1)
-        secs = time.perf_counter() - t0
+            want, secs, runs = cpu_repeat(lambda: np.concatenate(list(pool.map(part, chunks)), axis=1), 3.0)
         got = ok[:1].view(torch.int16).cpu().numpy().view(np.uint16)
         if not np.array_equal(got, bf16_bits(want)):
             raise CheckFailed("kv_gather: sequence 0 of K differs from the oracle")
@@ -598,7 +603,7 @@ def measure_kv(dev, with_cpu):
         res["cpu_baseline"] = {"value": round(per_seq / secs / 1e9, 3), "unit": "GB/s", "cores": n, "kind": "port",
                                "context_tokens_per_s": round(T / secs, 1),
                                "sample": f"one sequence of K (32768 tokens) by the NumPy oracle, tokens split "
-                                         f"over {n} threads: {secs:.2f} s"}
+                                         f"over {n} threads, median of {runs} runs: {secs:.3f} s"}
 
     def call(i):
         p = pools[i % 3]
@@ -731,7 +736,7 @@ def run(args):
     cpu = None
     if with_cpu:
         log("CPU oracle leg: one decode step ...")
-        want, secs, n = cpu_oracle_moe(L, slice(None), ("Q6_K",) * 3, HIDDEN, INTER, reps=3)
+        want, secs, n, runs = cpu_oracle_moe(L, slice(None), ("Q6_K",) * 3, HIDDEN, INTER, min_seconds=10.0)
         check = check_close("decode", got, want)
         for name, o in base_out.items():
             check[name] = check_close(f"decode {name}", o.float().cpu().numpy(), want, exact_frac=0.0)
@@ -798,7 +803,8 @@ def run(args):
             "value": round(nbytes / secs / 1e9, 4), "unit": "GB/s", "cores": n, "kind": "port",
             "tokens_per_s": round(TOKENS / secs, 2),
             "sample": f"one full decode step of the same workload ({active} active experts decoded, SwiGLU FFN, "
-                      f"combine) by the NumPy oracle with {n} threads, median of 3 runs: {secs:.3f} s",
+                      f"combine) by the NumPy oracle with {n} threads, median of {runs} runs "
+                      f"(about 10 s of CPU work): {secs:.3f} s per step",
         }
     configs = {}
     if not args.no_prefill:

@@ -109,21 +109,22 @@ int q6moe_gguf_decode(const uint8_t* raw, int qtype, int64_t rows, int64_t width
 
 /*
  * Expert tables of the routed FFN are unit-major, packed once from the GGUF
- * tables the reference keeps per expert ([E, bytes_per_expert], raw Q6_K,
- * Q4_K or Q8_0 rows; kaggle/qwen38_tpu/parallel.py:40-87). A unit is 16 output
- * rows x one 256-wide K block (Q6_K 3360 bytes, Q4_K 2304, Q8_0 4352; rows and
- * missing Q8_0 blocks padded with zeros); an expert's units run [row group][K
- * block]. Q4_K units hold the rows' block bytes in 16-byte chunks. Q6_K units
- * are bit-planar: the same 6-bit codes, sub-scales and FP16 scales, rearranged
- * per decoding lane; Q8_0 units hold each lane's 16 codes per 64-column chunk
- * and then the rows' FP16 block scales (maps in csrc/moe_common.h and
- * csrc/q6moe_device.h). The repack is lossless, so decoded values are those of
- * the GGUF rows.
+ * tables the reference keeps per expert ([E, bytes_per_expert] of raw GGUF
+ * rows; kaggle/qwen38_tpu/parallel.py:40-87). Formats: Q6_K, Q5_K, Q4_K and
+ * Q8_0 for gate/up; those or Q5_1 for down, in any pair. A unit is 16 output
+ * rows x one 256-wide K block (Q6_K 3360 bytes, Q5_K 2816, Q4_K 2304, Q8_0
+ * 4352, Q5_1 3072; rows and missing 32-value blocks padded with zeros); an
+ * expert's units run [row group][K block]. K-quant units hold the rows' block
+ * bytes in 16-byte chunks (Q6_K bit-planar: the same 6-bit codes, sub-scales
+ * and FP16 scales, rearranged per decoding lane); Q8_0 and Q5_1 units hold each
+ * lane's codes per 64-column chunk and then the rows' block scales (maps in
+ * csrc/moe_common.h and csrc/q6moe_device.h). The repack is lossless, so
+ * decoded values are those of the GGUF rows.
  */
 size_t q6moe_moe_table_bytes(int qtype, int64_t rows, int64_t width); /* per expert; 0 if invalid */
 
-/* raw [experts][rows][ceil(width/256)][210 or 144] (Q6_K, Q4_K) or
-   [experts][rows][width/32][34] (Q8_0) -> dst [experts][table bytes]
+/* raw [experts][rows][ceil(width/256)][210, 176 or 144] (Q6_K, Q5_K, Q4_K) or
+   [experts][rows][ceil(width/32)][34 or 24] (Q8_0, Q5_1) -> dst [experts][table bytes]
    (dst 16-byte aligned). No counterpart call in the reference, whose matmul
    reads GGUF bytes directly; this is its one-time load-side preparation. */
 int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, int64_t rows, int64_t width,
@@ -145,7 +146,7 @@ int q6moe_moe_unpack(const uint8_t* table, int qtype, int64_t experts, int64_t r
 
 /* Weight tables of one projection for all experts. */
 typedef struct q6moe_table {
-  int qtype;                /* gate/up: Q6MOE_Q6_K or Q6MOE_Q4_K; down: the same or Q6MOE_Q8_0 */
+  int qtype;                /* gate/up: Q6MOE_Q6_K, _Q5_K, _Q4_K or _Q8_0; down: those or Q6MOE_Q5_1 */
   const uint8_t* data;      /* unit-major table of expert e at data + e * data_stride */
   int64_t data_stride;      /* bytes between experts (>= q6moe_moe_table_bytes, multiple of 16) */
   const uint8_t* scales;    /* unused (NULL): the scales live in the units */
