@@ -837,9 +837,15 @@ __global__ void __launch_bounds__(64)
   *reinterpret_cast<u32x2*>(out + (int64_t)b * hidden + h) = o;
 }
 
-// Waves per workgroup (K split) for a launch of ``items`` workgroups at most:
-// enough to give every SIMD of the device about two waves, at most 4.
-static int split_for(int64_t items) {
+// Waves per workgroup (K split) for a launch of ``items`` workgroups at most.
+// A launch with few items gets up to 4 waves per item, until it has about 2.5
+// waves per SIMD (streams of a few units per wave then keep enough bytes in
+// flight). ``split_long`` asks for 2 waves per item when the launch is not
+// short of items but each item is long: the down items' K blocks (kDownRows
+// units each) split evenly in two. Measured on the decode steps of the
+// 128-expert Q6_K layer (1 wave best for both kernels) and the 64-expert Q4_K
+// layer (1 token: 4 and 4; 8 tokens: down 2; 16 tokens and more: 1).
+static int split_for(int64_t items, bool split_long) {
   static int simds = 0;
   if (!simds) {
     int dev = 0, cus = 0;
@@ -849,7 +855,8 @@ static int split_for(int64_t items) {
     simds = 4 * cus;
   }
   int ns = 1;
-  while (ns < 4 && items * ns * 2 <= 2 * (int64_t)simds) ns *= 2;
+  while (ns < 4 && items * ns * 2 * 4 <= 10 * (int64_t)simds) ns *= 2;
+  if (ns == 1 && split_long) ns = 2;
   return ns;
 }
 
@@ -871,7 +878,12 @@ static int launch(const DecArgs& A, hipStream_t s) {
   const int sh_gu = A.S.is ? (int)cdiv(A.S.is, 16) * passes : 0;
   const int sh_dn = A.S.is ? (int)cdiv(groups_h, kShRows) * passes : 0;
   const int64_t items_gu = (int64_t)groups_i * A.max_slots + sh_gu, items_dn = (int64_t)dn_x * A.max_slots + sh_dn;
-  const int ns_gu = split_for(items_gu), ns_dn = split_for(items_dn);
+  // long down items: an even number of K blocks, at least 4 (so 2 waves each
+  // stream 2 or more K blocks of kDownRows units), and the routing of at most
+  // 64 entries that every wave repeats cheaply
+  const int kb_i = (int)cdiv(A.I, kQK);
+  const bool long_dn = kb_i % 2 == 0 && kb_i >= 4 && A.R.B * A.R.K <= 64;
+  const int ns_gu = split_for(items_gu, false), ns_dn = split_for(items_dn, long_dn);
   hipLaunchKernelGGL((moe_dec_gate_up_kernel<FG, kFullK>), dim3((unsigned)items_gu), dim3(64 * ns_gu),
                      ns_gu * lds_gu, s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I, A.S);
   if (A.after_gate_up) (void)hipEventRecord((hipEvent_t)A.after_gate_up, s);
