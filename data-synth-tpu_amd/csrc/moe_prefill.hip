@@ -2,8 +2,9 @@
 //
 // The routing kernel (moe.hip) groups the routes by expert (ascending id,
 // tokens ascending) and splits each expert's routes into tiles of 128. One
-// workgroup (4 waves, one per SIMD; two workgroups per CU) computes a
-// 128-route tile against a block of output rows:
+// workgroup (4 waves, one per SIMD; two workgroups per CU) computes a tile
+// against a block of output rows; an expert's last, partial tile runs only the
+// 16-route column groups it needs, rounded up to 32 routes:
 //
 //   moe_pf_gate_up_kernel  64 intermediate rows (gate and up) per workgroup;
 //        g = RNE(x Wg^T), u = RNE(x Wu^T), a = RNE(RNE(g*sigmoid(g))*u)
@@ -32,17 +33,18 @@ namespace pf {
 
 constexpr int kWaves = 4;
 constexpr int kM = 128;            // routes per tile (MFMA column groups of 16)
-constexpr int kTG = kM / 16;       // token groups
 constexpr int kUnits = 2;          // units per wave per K block
 constexpr int kHalfBytes = kM * 128 * 2;  // one K half of the token tile (32 KB)
-constexpr int kXDma = kHalfBytes / 1024 / kWaves;  // token DMA instructions per wave per half
 constexpr int kAhead = 1;          // K halves in flight beyond the one being multiplied
 constexpr int kXStages = kAhead + 1;
 constexpr int kWLoads = 5;         // weight loads per unit per K block (3 code chunks, sub-scales, d)
+// A tile of NCG (2, 4, 6 or 8) 16-route column groups: the token rows of a K
+// half take NCG KB per wave, i.e. NCG DMA instructions of 1 KB per wave.
 // Vector-memory instructions per wave of the step before a first half (the
 // most of any step). The waits below need exact counts only for steps still in
 // flight behind the one awaited, and with one step ahead there are none.
-constexpr int kStepOps = kUnits * kWLoads + kXDma;
+template <int NCG>
+constexpr int step_ops() { return kUnits * kWLoads + NCG; }
 static_assert(kAhead == 1, "per-step wait counts assume one step in flight");
 constexpr int kLds = kXStages * kHalfBytes;
 
@@ -164,10 +166,10 @@ __device__ __forceinline__ void tile_info(const MoeWs& ws, int tile, Tile& T) {
 // a second-half step, which needs no weights, the DMA halves come first), so
 // that the four waves of a workgroup do not all queue their vector-memory
 // instructions at once right after the barrier.
-template <typename RowFn>
+template <int NCG, typename RowFn>
 __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
-                                          const uint16_t* x, const uint32_t (&xoff)[kXDma], int K,
-                                          int64_t expert, f32x4 (&acc)[kUnits][kTG]) {
+                                          const uint16_t* x, const uint32_t (&xoff)[NCG], int K,
+                                          int64_t expert, f32x4 (&acc)[kUnits][NCG]) {
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int j = lane & 15, jA = lane >> 4;
   const int kbs = K / kQK;
@@ -197,8 +199,9 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
       load_block(units[part], kbs, rgs[part], kb, lane, wr[part]);  // s even: h == 0
     } else if constexpr (slot == 0 || part < 4 - kUnits) {
       // second-half steps load no weights: their token DMA goes out in the first parts
-      constexpr int np = 4 - kUnits, per = kXDma / np, i0 = (slot == 0 ? part - kUnits : part) * per;
-      uint8_t* xs = smem + slot * kHalfBytes + wave * kXDma * 1024;
+      constexpr int np = 4 - kUnits, per = NCG / np, i0 = (slot == 0 ? part - kUnits : part) * per;
+      static_assert(NCG % np == 0, "the token DMA splits evenly over the parts");
+      uint8_t* xs = smem + slot * kHalfBytes + wave * NCG * 1024;
 #pragma unroll
       for (int i = i0; i < i0 + per; ++i) dma16(xb + (int64_t)(kb * kQK + h * 128) * 2, xoff[i], xs + i * 1024);
     }
@@ -212,7 +215,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     const int younger = S - 1 - s < kAhead - 1 ? S - 1 - s : kAhead - 1;
     static_for<0, kAhead>([&](auto yc) {
       constexpr int y = decltype(yc)::value;
-      if (younger == y) wait_vm<y * kStepOps>();
+      if (younger == y) wait_vm<y * step_ops<NCG>()>();
     });
     wg_barrier();  // every wave's share of this step's tile is in LDS; the oldest stage is free
     // The wait above covered this step's weight registers. Re-define them here
@@ -232,7 +235,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
       constexpr int f = decltype(fc)::value;
       const int c = xfrag_gran(f, jA);
 #pragma unroll
-      for (int tg = 0; tg < kTG; ++tg) {
+      for (int tg = 0; tg < NCG; ++tg) {
         const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + xgran(tg * 16 + j, c));
 #pragma unroll
         for (int u = 0; u < kUnits; ++u) acc[u][tg] = mfma16(a[u][f], xv, acc[u][tg]);
@@ -253,15 +256,28 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
 }
 
 // Per-lane token-tile DMA offsets: instruction i of this wave fills granules
-// (wave*kXDma + i)*64 + lane, i.e. token t = that/16, swizzled granule l%16.
-template <typename RowOf>
-__device__ __forceinline__ void x_offsets(uint32_t (&xoff)[kXDma], int K, RowOf row_of) {
+// (wave*NCG + i)*64 + lane, i.e. token t = that/16, swizzled granule l%16.
+template <int NCG, typename RowOf>
+__device__ __forceinline__ void x_offsets(uint32_t (&xoff)[NCG], int K, RowOf row_of) {
   const int wave = wave_id(), lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < kXDma; ++i) {
-    const int p = (wave * kXDma + i) * 64 + lane;
+  for (int i = 0; i < NCG; ++i) {
+    const int p = (wave * NCG + i) * 64 + lane;
     const int t = p >> 4, c = (p & 15) ^ (t & 15);
     xoff[i] = opaque((uint32_t)((row_of(t) * K + c * 8) * 2));
+  }
+}
+
+// Calls f(std::integral_constant<int, NCG>) for the tile's column groups: its
+// valid routes rounded up to 32 (2, 4, 6 or 8 groups of 16), so a partial tile
+// issues only the MFMAs and token DMA of the routes it holds.
+template <typename F>
+__device__ __forceinline__ void with_column_groups(int nv, F&& f) {
+  switch ((nv + 31) >> 5) {
+    case 1: f(std::integral_constant<int, 2>{}); break;
+    case 2: f(std::integral_constant<int, 4>{}); break;
+    case 3: f(std::integral_constant<int, 6>{}); break;
+    default: f(std::integral_constant<int, 8>{}); break;
   }
 }
 
@@ -279,34 +295,37 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
   const int rgb = col * kWaves + wave;  // this wave's row group (gate and up)
-  uint32_t xoff[kXDma];
-  x_offsets(xoff, hidden, [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; });
-  const Proj projs[2] = {gate, up};
-  const int unit_proj[kUnits] = {0, 1};
-  f32x4 acc[kUnits][kTG];
+  with_column_groups(T.nv, [&](auto ncg_c) {
+    constexpr int NCG = decltype(ncg_c)::value;
+    uint32_t xoff[NCG];
+    x_offsets(xoff, hidden, [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; });
+    const Proj projs[2] = {gate, up};
+    const int unit_proj[kUnits] = {0, 1};
+    f32x4 acc[kUnits][NCG];
 #pragma unroll
-  for (int u = 0; u < kUnits; ++u)
+    for (int u = 0; u < kUnits; ++u)
 #pragma unroll
-    for (int t = 0; t < kTG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  pf_stream(smem, projs, unit_proj, [&](int) { return rgb; }, x, xoff, hidden, T.expert, acc);
-  const int row = rgb * 16 + 4 * jA;
+      for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    pf_stream<NCG>(smem, projs, unit_proj, [&](int) { return rgb; }, x, xoff, hidden, T.expert, acc);
+    const int row = rgb * 16 + 4 * jA;
 #pragma unroll
-  for (int tg = 0; tg < kTG; ++tg) {
-    const int q = tg * 16 + j;
-    if (q < T.nv) {
-      float v[4];
+    for (int tg = 0; tg < NCG; ++tg) {
+      const int q = tg * 16 + j;
+      if (q < T.nv) {
+        float v[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float g = bf16_round(acc[0][tg][i]);
-        const float u = bf16_round(acc[1][tg][i]);
-        v[i] = bf16_round(g * sigmoid_acc(g)) * u;
+        for (int i = 0; i < 4; ++i) {
+          const float g = bf16_round(acc[0][tg][i]);
+          const float u = bf16_round(acc[1][tg][i]);
+          v[i] = bf16_round(g * sigmoid_acc(g)) * u;
+        }
+        u32x2 o;
+        o[0] = pack_bf16x2(v[0], v[1]);
+        o[1] = pack_bf16x2(v[2], v[3]);
+        *reinterpret_cast<u32x2*>(act + (int64_t)(T.r0 + q) * inter + row) = o;
       }
-      u32x2 o;
-      o[0] = pack_bf16x2(v[0], v[1]);
-      o[1] = pack_bf16x2(v[2], v[3]);
-      *reinterpret_cast<u32x2*>(act + (int64_t)(T.r0 + q) * inter + row) = o;
     }
-  }
+  });
 }
 
 __global__ void __launch_bounds__(64 * pf::kWaves, 2)
@@ -321,30 +340,33 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int jA = lane >> 4, j = lane & 15;
   const int rgb = col * 2 * kWaves + 2 * wave;  // this wave's two row groups
-  uint32_t xoff[kXDma];
-  x_offsets(xoff, inter, [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); });
-  const Proj projs[1] = {down};
-  const int unit_proj[kUnits] = {0, 0};
-  f32x4 acc[kUnits][kTG];
+  with_column_groups(T.nv, [&](auto ncg_c) {
+    constexpr int NCG = decltype(ncg_c)::value;
+    uint32_t xoff[NCG];
+    x_offsets(xoff, inter, [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); });
+    const Proj projs[1] = {down};
+    const int unit_proj[kUnits] = {0, 0};
+    f32x4 acc[kUnits][NCG];
 #pragma unroll
-  for (int u = 0; u < kUnits; ++u)
+    for (int u = 0; u < kUnits; ++u)
 #pragma unroll
-    for (int t = 0; t < kTG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  pf_stream(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, xoff, inter, T.expert, acc);
+      for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    pf_stream<NCG>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, xoff, inter, T.expert, acc);
 #pragma unroll
-  for (int u = 0; u < kUnits; ++u) {
-    const int row = (rgb + u) * 16 + 4 * jA;
+    for (int u = 0; u < kUnits; ++u) {
+      const int row = (rgb + u) * 16 + 4 * jA;
 #pragma unroll
-    for (int tg = 0; tg < kTG; ++tg) {
-      const int q = tg * 16 + j;
-      if (q < T.nv) {
-        u32x2 o;
-        o[0] = pack_bf16x2(acc[u][tg][0], acc[u][tg][1]);
-        o[1] = pack_bf16x2(acc[u][tg][2], acc[u][tg][3]);
-        *reinterpret_cast<u32x2*>(y + (int64_t)(T.r0 + q) * hidden + row) = o;
+      for (int tg = 0; tg < NCG; ++tg) {
+        const int q = tg * 16 + j;
+        if (q < T.nv) {
+          u32x2 o;
+          o[0] = pack_bf16x2(acc[u][tg][0], acc[u][tg][1]);
+          o[1] = pack_bf16x2(acc[u][tg][2], acc[u][tg][3]);
+          *reinterpret_cast<u32x2*>(y + (int64_t)(T.r0 + q) * hidden + row) = o;
+        }
       }
     }
-  }
+  });
 }
 
 bool pf_supported(int fmt, int64_t H, int64_t I) {
