@@ -31,6 +31,21 @@ def test_prefill_matches_oracle(device, tokens, experts, top_k, hidden, inter):
     assert_moe_close(got, _oracle(L))
 
 
+def test_prefill_partial_tiles_of_every_width(device):
+    # Top-1 routes assigned so that expert e holds counts[e] routes: partial
+    # tiles of 1-32, 33-64, 65-96 and 97-128 routes (2, 4, 6 and 8 column
+    # groups), exact multiples of 128 and a full tile plus a 1-route tail.
+    counts = [1, 17, 32, 33, 50, 64, 65, 90, 96, 97, 113, 127, 128, 129, 256, 200]
+    experts = len(counts)
+    tokens = sum(counts)
+    L = moe_layer(seed=23, experts=experts, top_k=1, hidden=256, intermediate=256, tokens=tokens, pack=False)
+    ids = np.repeat(np.arange(experts, dtype=np.int32), counts)
+    ids = np.random.default_rng(23).permutation(ids).reshape(tokens, 1)
+    w = np.ones((tokens, 1), np.float32)
+    got, _ = _run(L, device, mode=2, ids=ids, weights=w)
+    assert_moe_close(got, _oracle(L, ids=ids, weights=w))
+
+
 def test_prefill_and_decode_paths_agree(device):
     # Both paths are checked against the oracle; they share the routing and
     # the rounding boundaries, so they must also agree with each other.
