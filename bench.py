@@ -42,6 +42,9 @@ HBM traffic per launch from the committed rocprofv3 counter summaries
 The CPU baseline is the NumPy oracle (``kind: port``) on this host with the
 stated number of threads (the host's CPU affinity, at most 16), on a bounded
 sample of each workload; it is reported beside the GPU numbers, not targeted.
+
+By default the measurement runs in a child process that a watchdog kills
+after ``--watchdog`` seconds (900); ``--watchdog 0`` runs it in this process.
 """
 
 import argparse
@@ -670,21 +673,56 @@ def main():
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="first copy a buffer of this many MiB device-to-device 5 times (a known-size "
                          "kernel for scaling hardware byte counters)")
+    ap.add_argument("--watchdog", type=int, default=900,
+                    help="run the measurement in a child process and kill it after this many seconds "
+                         "(exit status 124), as the reference harness supervises its worker; 0 runs it in "
+                         "this process (used under rocprofv3)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         log("bench.py measures one GPU: the packed-expert path runs on a single MI355X here "
-            "(sharding is by expert, see the design notes); run with --gpus 1")
+            "(it would shard by expert across GPUs); run with --gpus 1")
         return 2
     if not (1 <= args.steps <= 100000 and 0 <= args.warmup <= 10000 and 1 <= args.layers <= 16):
         log("steps must be 1..100000, warmup 0..10000, layers 1..16")
         return 2
+    if args.watchdog > 0 and not os.environ.get(WORKER_ENV):
+        return supervise(args.watchdog)
     try:
         return run(args)
     except CheckFailed as exc:
         log(f"check failed: {exc}")
         print(json.dumps({"metric": METRIC, "error": str(exc)}), flush=True)
         return 1
+
+
+WORKER_ENV = "Q6MOE_BENCH_WORKER"
+
+
+def supervise(timeout_s):
+    """Watchdog (kaggle/packed_q6/benchmark.py:206-247): runs this script again
+    as a child in its own process group, with the same arguments, and kills the
+    group if it has not finished after ``timeout_s`` seconds. The child writes
+    the JSON line and its progress itself; this process touches no GPU and
+    returns the child's exit status (124 on a timeout)."""
+    import signal
+    import subprocess
+
+    env = dict(os.environ, **{WORKER_ENV: "1"})
+    child = subprocess.Popen([sys.executable, str(Path(__file__).resolve())] + sys.argv[1:], env=env,
+                             start_new_session=True)
+    try:
+        return child.wait(timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        log(f"watchdog: the measurement did not finish in {timeout_s} s; killing it")
+        os.killpg(child.pid, signal.SIGKILL)
+        child.wait()
+        print(json.dumps({"metric": METRIC, "error": f"timed out after {timeout_s} s"}), flush=True)
+        return 124
+    except KeyboardInterrupt:
+        os.killpg(child.pid, signal.SIGKILL)
+        child.wait()
+        return 130
 
 
 def run(args):
