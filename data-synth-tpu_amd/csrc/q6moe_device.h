@@ -71,7 +71,11 @@ __device__ __forceinline__ uint32_t q6_codes_hi(uint32_t ql, uint32_t hs) {
 // ds*32 are exact in FP32, so the value is exact; only the sign of an exact
 // zero can differ from ds * (c - 32) (+0 instead of -0), which no sum of
 // products can observe. q6_frag_exact keeps the reference's signed zeros.
+// The code words are made opaque first: callers pass masked words (K-quant and
+// Q5_1 nibbles), and the compiler would otherwise fold each byte's mask into a
+// v_bfe_u32 before its conversion instead of one v_cvt_f32_ubyteN per byte.
 __device__ __forceinline__ u32x4 q6_frag(uint32_t c0, uint32_t c1, float ds, float nds) {
+  asm("" : "+v"(c0), "+v"(c1));
   u32x4 r;
   r[0] = pack_bf16x2(__builtin_fmaf(ubyte_f(c0, 0), ds, nds), __builtin_fmaf(ubyte_f(c0, 1), ds, nds));
   r[1] = pack_bf16x2(__builtin_fmaf(ubyte_f(c0, 2), ds, nds), __builtin_fmaf(ubyte_f(c0, 3), ds, nds));
