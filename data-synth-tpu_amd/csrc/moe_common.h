@@ -284,7 +284,7 @@ struct Unit<FMT_Q8> {
     for (int g = 0; g < 4; ++g) c[g] = ld16_stream(u + 1024 * g + 16 * lane);
     d = *reinterpret_cast<const u32x2*>(u + 4096 + 8 * (2 * (lane & 15) + (lane >> 5)));
   }
-  __device__ __forceinline__ void decode(u32x4 a[8], int) const { q8_decode(c, d, a); }
+  __device__ __forceinline__ void decode(u32x4 a[8], int) const { q8_decode<true>(c, d, a); }
   static __device__ __forceinline__ int xoff(int f, int jA) { return q6_xfrag_offset(f, jA); }
 };
 

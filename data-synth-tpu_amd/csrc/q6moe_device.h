@@ -250,12 +250,16 @@ __device__ __forceinline__ void q6_decode_unit(const Q6Raw& r, int jA, u32x4 a[8
   }
 }
 
-// Element offset, inside one 256-wide K block, of the 8 x values that pair
-// with fragment f of a lane in k-group jA.
 // Q8_0: 8 int8 codes (two words, lowest byte first) times the block scale d;
 // each product is exact in FP32 (11-bit d times an 8-bit code), then RNE to
-// BF16 (kaggle/glm53_offload/gguf_quant.py:111-114).
+// BF16 (kaggle/glm53_offload/gguf_quant.py:111-114). kOpaque hides the words
+// from the compiler, which keeps each code's conversion one v_cvt_f32_i32 with
+// a sign-extended byte select where it would otherwise extract byte 0 with a
+// separate v_bfe_i32 (the generic kernels' register path); the LDS-staged
+// decode-step path selects the one-instruction form by itself.
+template <bool kOpaque = false>
 __device__ __forceinline__ u32x4 q8_frag(uint32_t w0, uint32_t w1, float d) {
+  if constexpr (kOpaque) asm("" : "+v"(w0), "+v"(w1));
   u32x4 r;
   r[0] = pack_bf16x2(d * (float)(int8_t)w0, d * (float)(int8_t)(w0 >> 8));
   r[1] = pack_bf16x2(d * (float)(int8_t)(w0 >> 16), d * (float)(int8_t)(w0 >> 24));
@@ -266,15 +270,18 @@ __device__ __forceinline__ u32x4 q8_frag(uint32_t w0, uint32_t w1, float d) {
 
 // The 8 A fragments of a Q8_0 unit from the lane's 4 code chunks and its 4
 // FP16 block scales (chunk g: fragments 2g and 2g+1, scale g).
+template <bool kOpaque = false>
 __device__ __forceinline__ void q8_decode(const u32x4 (&c)[4], u32x2 dw, u32x4 a[8]) {
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const float d = half_bits_to_float((dw[g >> 1] >> (16 * (g & 1))) & 0xffffu);
-    a[2 * g] = q8_frag(c[g][0], c[g][1], d);
-    a[2 * g + 1] = q8_frag(c[g][2], c[g][3], d);
+    a[2 * g] = q8_frag<kOpaque>(c[g][0], c[g][1], d);
+    a[2 * g + 1] = q8_frag<kOpaque>(c[g][2], c[g][3], d);
   }
 }
 
+// Element offset, inside one 256-wide K block, of the 8 x values that pair
+// with fragment f of a lane in k-group jA.
 __device__ __forceinline__ int q6_xfrag_offset(int f, int jA) {
   const int g = f >> 1, e = f & 1;
   return 128 * (g >> 1) + 32 * ((jA >> 1) + 2 * (g & 1)) + 16 * (jA & 1) + 8 * e;
