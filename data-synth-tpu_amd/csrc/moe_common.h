@@ -250,19 +250,17 @@ struct Unit<FMT_Q4K> {
       ds[h] = d * (float)sc;
       dm[h] = -(dmin * (float)mn);
     }
+    // Codes as FP16 subnormals (sub_frag): the low nibbles of bytes 0 and 2
+    // of a word sit at bits 0-3 of its halves (q * 2^-24), the high nibbles at
+    // bits 4-7 (q * 2^-20); bytes 1 and 3 the same after a shift by 8.
+    const float s_lo = ds[0] * 16777216.f, s_hi = ds[1] * 1048576.f;
 #pragma unroll
     for (int f = 0; f < 8; ++f) {
       const int hn = f >> 2, bg = f & 3;
       const u32x4& src = bg < 2 ? qa : qb;
-      uint32_t c0 = src[2 * (bg & 1)], c1 = src[2 * (bg & 1) + 1];
-      if (hn) {
-        c0 = (c0 >> 4) & 0x0f0f0f0fu;
-        c1 = (c1 >> 4) & 0x0f0f0f0fu;
-      } else {
-        c0 &= 0x0f0f0f0fu;
-        c1 &= 0x0f0f0f0fu;
-      }
-      a[f] = q6_frag(c0, c1, ds[hn], dm[hn]);
+      const uint32_t w0 = src[2 * (bg & 1)], w1 = src[2 * (bg & 1) + 1];
+      const uint32_t m = hn ? 0x00F000F0u : 0x000F000Fu;
+      a[f] = sub_frag(w0 & m, (w0 >> 8) & m, w1 & m, (w1 >> 8) & m, hn ? s_hi : s_lo, dm[hn]);
     }
   }
   static __device__ __forceinline__ int xoff(int f, int jA) {

@@ -250,6 +250,24 @@ __device__ __forceinline__ void q6_decode_unit(const Q6Raw& r, int jA, u32x4 a[8
   }
 }
 
+// Eight weights w = RNE_bf16(fma(q, a, n)) of small unsigned codes q held as
+// FP16 subnormals: a 16-bit half whose bits are q << b (q << b < 1024) is the
+// FP16 value q * 2^(b-24), exactly. v_fma_mix_f32 takes it as is with the
+// scale s = a * 2^(24-b) (a power-of-two multiple of a, exact; no overflow
+// for FP16-derived scales), so h * s = q * a exactly and the single rounding
+// is that of fma(q, a, n): the values are bit-identical to q6_frag's, with no
+// per-code integer-to-float conversion. ``e`` words hold K positions 0 and 2
+// of a four-code group in their low and high halves, ``o`` words positions 1
+// and 3.
+__device__ __forceinline__ u32x4 sub_frag(uint32_t e0, uint32_t o0, uint32_t e1, uint32_t o1, float s, float n) {
+  u32x4 r;
+  r[0] = pack_bf16x2(__builtin_fmaf(h16_lo(e0), s, n), __builtin_fmaf(h16_lo(o0), s, n));
+  r[1] = pack_bf16x2(__builtin_fmaf(h16_hi(e0), s, n), __builtin_fmaf(h16_hi(o0), s, n));
+  r[2] = pack_bf16x2(__builtin_fmaf(h16_lo(e1), s, n), __builtin_fmaf(h16_lo(o1), s, n));
+  r[3] = pack_bf16x2(__builtin_fmaf(h16_hi(e1), s, n), __builtin_fmaf(h16_hi(o1), s, n));
+  return r;
+}
+
 // Q8_0: 8 int8 codes (two words, lowest byte first) times the block scale d;
 // each product is exact in FP32 (11-bit d times an 8-bit code), then RNE to
 // BF16 (kaggle/glm53_offload/gguf_quant.py:111-114). kOpaque hides the words
