@@ -41,15 +41,30 @@ constexpr int kStages = 3;
 constexpr int kDownRows = 4;  // 16-row groups of down per wave
 constexpr int kPassTokens = 16;  // routes per weight pass (MFMA columns)
 
-// One ring stage holds a unit as it lies in the table (Q6_K 3360 B, Q4_K
-// 2304 B, Q5_K 2816 B, Q5_1 3072 B, Q8_0 4352 B), the Q6_K FP16 scales
-// repeated up to the stage's end.
+// One ring stage holds a unit as its DMA writes it (Q4_K 2304 B, Q5_K
+// 2816 B, Q5_1 3072 B, Q8_0 4352 B; Q6_K 3360 B with its FP16 scales repeated
+// up to 3584 B).
 template <int FMT>
-constexpr int stage_bytes() { return FMT == FMT_Q8 ? 4352 : 3584; }
+constexpr int stage_bytes() {
+  return FMT == FMT_Q8 ? 4352 : FMT == FMT_Q4K ? 2304 : FMT == FMT_Q5K ? 2816 : FMT == FMT_Q51 ? 3072 : 3584;
+}
+template <int FMT>
+constexpr int ring_bytes() { return kStages * stage_bytes<FMT>(); }
 constexpr int kXLoads = 8;   // token-operand loads per K block (one per MFMA)
 
-static_assert(kStages * stage_bytes<FMT_Q6>() >= 8 * kDecMaxEntries + 4 * kDecMaxExperts,
-              "routing scratch overlays the ring");
+// Per-wave LDS of the gate/up kernel: the weight ring, which the routing
+// scratch overlays before the ring fills (for more than 64 entries: ids,
+// merged weights and per-expert counts, 8 bytes per entry plus 4 per
+// expert), then the slot's token list. Sized per launch, so that a layer with
+// small units and few routes keeps more waves per CU.
+__host__ __device__ constexpr int route_scratch_bytes(int n) {
+  return n > 64 ? 8 * ((n + 3) & ~3) + 4 * kDecMaxExperts : 64;
+}
+template <int FMT>
+__host__ __device__ constexpr int gu_wave_lds(int n) {
+  const int r = ring_bytes<FMT>(), sc = route_scratch_bytes(n);
+  return (((r > sc ? r : sc) + 255) & ~255) + 4 * kDecMaxTokens;
+}
 
 template <int I, int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
@@ -483,8 +498,9 @@ __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTa
   const int n = R.B * R.K;
   if (n <= 64) return dec_route_small(R, slot, publish, T, scratch, tok, out);
   int* s_ids = reinterpret_cast<int*>(scratch);
-  float* s_r = reinterpret_cast<float*>(scratch + 4 * kDecMaxEntries);
-  int* s_cnt = reinterpret_cast<int*>(scratch + 8 * kDecMaxEntries);
+  const int n4 = (n + 3) & ~3;  // route_scratch_bytes(n) bytes: ids, weights, counts
+  float* s_r = reinterpret_cast<float*>(scratch + 4 * n4);
+  int* s_cnt = reinterpret_cast<int*>(scratch + 8 * n4);
 #pragma unroll
   for (int q = 0; q < kDecMaxExperts / 64; ++q) s_cnt[q * 64 + lane] = 0;
   for (int i = lane; i < n; i += 64) {
@@ -610,28 +626,27 @@ __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTa
 // w streams K blocks [w*kbs/NS, (w+1)*kbs/NS) through its own ring and the
 // partial sums meet in LDS, added in wave order by wave 0. NS > 1 when the
 // items alone would leave SIMDs idle (few tokens or experts).
-template <int FMT>
-constexpr int wave_lds() { return kStages * stage_bytes<FMT>() + 4 * kDecMaxTokens; }  // ring + token list
 
 __device__ __forceinline__ int split_waves() { return __builtin_amdgcn_readfirstlane(blockDim.x >> 6); }
 __device__ __forceinline__ int split_wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Sums the P accumulators of all waves into wave 0's (wave order); every wave
-// passes its barriers. The other waves' rings are free when this is called.
-template <int P, int kWaveLds>
-__device__ __forceinline__ void split_reduce(uint8_t* smem, int ns, int wave, f32x4 (&acc)[P]) {
+// passes its barriers. The other waves' rings (``wave_lds`` bytes apart) are
+// free when this is called.
+template <int P>
+__device__ __forceinline__ void split_reduce(uint8_t* smem, int ns, int wave, f32x4 (&acc)[P], int wave_lds) {
   if (ns == 1) return;
   const int lane = threadIdx.x & 63;
   __syncthreads();
   if (wave > 0) {
-    float* red = reinterpret_cast<float*>(smem + wave * kWaveLds);
+    float* red = reinterpret_cast<float*>(smem + wave * wave_lds);
 #pragma unroll
     for (int p = 0; p < P; ++p) *reinterpret_cast<f32x4*>(red + (p * 64 + lane) * 4) = acc[p];
   }
   __syncthreads();
   if (wave == 0) {
     for (int w = 1; w < ns; ++w) {
-      const float* red = reinterpret_cast<const float*>(smem + w * kWaveLds);
+      const float* red = reinterpret_cast<const float*>(smem + w * wave_lds);
 #pragma unroll
       for (int p = 0; p < P; ++p) acc[p] += *reinterpret_cast<const f32x4*>(red + (p * 64 + lane) * 4);
     }
@@ -643,9 +658,9 @@ __device__ __forceinline__ void split_reduce(uint8_t* smem, int ns, int wave, f3
 // tok[0..cnt) in passes of 16; a = RNE(RNE(g*sig(g)) * u) into act rows
 // t0 + q (row stride ``inter``).
 template <int FMT, bool kFullK>
-__device__ __forceinline__ void dec_gate_up_item(uint8_t* smem, uint8_t* ring, const Proj& gate, const Proj& up,
-                                                 int64_t expert, int rg, int t0, int cnt, const int* tok,
-                                                 const uint16_t* __restrict__ x, int nx, int hidden,
+__device__ __forceinline__ void dec_gate_up_item(uint8_t* smem, uint8_t* ring, int wave_lds, const Proj& gate,
+                                                 const Proj& up, int64_t expert, int rg, int t0, int cnt,
+                                                 const int* tok, const uint16_t* __restrict__ x, int nx, int hidden,
                                                  uint16_t* __restrict__ act, int inter) {
   const int ns = split_waves(), wave = split_wave();
   const int lane = threadIdx.x & 63, jA = lane >> 4, j = lane & 15;
@@ -659,7 +674,7 @@ __device__ __forceinline__ void dec_gate_up_item(uint8_t* smem, uint8_t* ring, c
     if (kb1 > kb0)
       stream_units<FMT, kFullK, 2>(
           ring, kb0, kb1 - kb0, xs, [&](int p, int kb, uint8_t* st) { (p ? wu : wg).issue(rg, kb, st); }, acc);
-    split_reduce<2, wave_lds<FMT>()>(smem, ns, wave, acc);
+    split_reduce<2>(smem, ns, wave, acc, wave_lds);
     // lane holds rows 4*(lane/16)+q, token column lane%16 of both accumulators
     if (wave == 0 && j < nt) {
 #pragma unroll
@@ -684,8 +699,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
                            int hidden, uint16_t* __restrict__ act, int inter, DecShared sh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int wave = split_wave();
-  uint8_t* ring = smem + wave * wave_lds<FMT>();
-  int* tok = reinterpret_cast<int*>(ring + kStages * stage_bytes<FMT>());
+  const int wl = gu_wave_lds<FMT>(R.B * R.K);
+  uint8_t* ring = smem + wave * wl;
+  int* tok = reinterpret_cast<int*>(ring + wl - 4 * kDecMaxTokens);
   const int sh_groups = (sh.is + 15) / 16, passes = (R.B + kPassTokens - 1) / kPassTokens;
   const int sh_items = sh.is ? sh_groups * passes : 0;
   const int item = blockIdx.x;
@@ -696,14 +712,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
     const int cnt = R.B - t0 < kPassTokens ? R.B - t0 : kPassTokens;
     if (lane < cnt) tok[lane] = t0 + lane;
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the list is in LDS before the ring fills
-    dec_gate_up_item<FMT, kFullK>(smem, ring, sh.gate, sh.up, 0, rg, t0, cnt, tok, x, R.B, hidden, sh.act, sh.is);
+    dec_gate_up_item<FMT, kFullK>(smem, ring, wl, sh.gate, sh.up, 0, rg, t0, cnt, tok, x, R.B, hidden, sh.act,
+                                  sh.is);
     return;
   }
   const int groups_i = (inter + 15) / 16;
   const int rg = (item - sh_items) % groups_i, slot = (item - sh_items) / groups_i;
   SlotRoute sr;
   if (!dec_route(R, slot, rg == 0 && wave == 0, T, ring, tok, sr)) return;
-  dec_gate_up_item<FMT, kFullK>(smem, ring, gate, up, sr.expert, rg, sr.t0, sr.cnt, tok, x, R.B, hidden, act, inter);
+  dec_gate_up_item<FMT, kFullK>(smem, ring, wl, gate, up, sr.expert, rg, sr.t0, sr.cnt, tok, x, R.B, hidden, act,
+                                inter);
 }
 
 // Items: the shared expert's down (kShRows row groups and 16 tokens each,
@@ -718,7 +736,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
                         float* __restrict__ contrib, int hidden, DecShared sh, int tokens) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int ns = split_waves(), wave = split_wave();
-  uint8_t* ring = smem + wave * wave_lds<FMT>();
+  uint8_t* ring = smem + wave * ring_bytes<FMT>();
   const int lane = threadIdx.x & 63, jA = lane >> 4, j = lane & 15;
   const int groups = (hidden + 15) / 16;
   const int sh_blocks = (groups + kShRows - 1) / kShRows, passes = (tokens + kPassTokens - 1) / kPassTokens;
@@ -738,7 +756,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
       stream_units<FMT, kFullK, kShRows>(
           ring, kb0, kb1 - kb0, xs,
           [&](int p, int kb, uint8_t* st) { wd.issue(rg0 + p < groups ? rg0 + p : groups - 1, kb, st); }, acc);
-    split_reduce<kShRows, wave_lds<FMT>()>(smem, ns, wave, acc);
+    split_reduce<kShRows>(smem, ns, wave, acc, ring_bytes<FMT>());
     if (wave == 0 && j < nt) {
 #pragma unroll
       for (int r = 0; r < kShRows; ++r)
@@ -775,7 +793,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
             wd.issue(rg, kb, st);
           },
           acc);
-    split_reduce<kDownRows, wave_lds<FMT>()>(smem, ns, wave, acc);
+    split_reduce<kDownRows>(smem, ns, wave, acc, ring_bytes<FMT>());
     if (wave == 0 && j < nt) {
 #pragma unroll
       for (int r = 0; r < kDownRows; ++r) {
@@ -864,11 +882,13 @@ static int split_for(int64_t items, bool split_long) {
 template <int FG, int FD, bool kFullK>
 static int launch(const DecArgs& A, hipStream_t s) {
   const int groups_i = (int)cdiv(A.I, 16), groups_h = (int)cdiv(A.H, 16);
-  constexpr int lds_gu = wave_lds<FG>(), lds_dn = wave_lds<FD>();
+  // per-wave LDS: the gate/up ring sized for this launch's routing entries
+  const int lds_gu = gu_wave_lds<FG>((int)(A.R.B * A.R.K));
+  constexpr int lds_dn = ring_bytes<FD>();
   static bool attr_done = false;
-  if (!attr_done) {
+  if (!attr_done) {  // the most any launch asks for
     (void)hipFuncSetAttribute((const void*)moe_dec_gate_up_kernel<FG, kFullK>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 4 * lds_gu);
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 4 * gu_wave_lds<FG>(kDecMaxEntries));
     (void)hipFuncSetAttribute((const void*)moe_dec_down_kernel<FD, kFullK>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, 4 * lds_dn);
     attr_done = true;
