@@ -1293,14 +1293,13 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   }
   mark(0);
   {
-    static bool attr_done = false;
-    if (!attr_done) {  // top_k <= 32: at most 64 KB and 96 KB of staged rows
+    static std::atomic<uint64_t> attr_done{0};
+    once_per_device(attr_done, [] {  // top_k <= 32: at most 64 KB and 96 KB of staged rows
       (void)hipFuncSetAttribute((const void*)moe_route_count_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          kChunk * 32 * 8);
+                                kChunk * 32 * 8);
       (void)hipFuncSetAttribute((const void*)moe_route_scatter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          kChunk * 32 * 12);
-      attr_done = true;
-    }
+                                kChunk * 32 * 12);
+    });
     const int nchunks = (int)cdiv(B, kChunk);
     int* chunk_cnt = reinterpret_cast<int*>(w + L.chunk_cnt);
     hipLaunchKernelGGL(moe_route_count_kernel, dim3(nchunks), dim3(kChunk), (size_t)kChunk * K * 8, s, a->ids,

@@ -885,14 +885,13 @@ static int launch(const DecArgs& A, hipStream_t s) {
   // per-wave LDS: the gate/up ring sized for this launch's routing entries
   const int lds_gu = gu_wave_lds<FG>((int)(A.R.B * A.R.K));
   constexpr int lds_dn = ring_bytes<FD>();
-  static bool attr_done = false;
-  if (!attr_done) {  // the most any launch asks for
+  static std::atomic<uint64_t> attr_done{0};
+  once_per_device(attr_done, [] {  // the most any launch asks for
     (void)hipFuncSetAttribute((const void*)moe_dec_gate_up_kernel<FG, kFullK>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, 4 * gu_wave_lds<FG>(kDecMaxEntries));
     (void)hipFuncSetAttribute((const void*)moe_dec_down_kernel<FD, kFullK>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 4 * lds_dn);
-    attr_done = true;
-  }
+                              hipFuncAttributeMaxDynamicSharedMemorySize, 4 * ring_bytes<FD>());
+  });
   const int dn_x = (int)cdiv(groups_h, kDownRows);
   const int passes = (int)cdiv(A.R.B, kPassTokens);
   const int sh_gu = A.S.is ? (int)cdiv(A.S.is, 16) * passes : 0;

@@ -377,12 +377,11 @@ int64_t pf_tile_routes() { return pf::kM; }
 
 int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
                        const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up, bool with_down) {
-  static bool attr_done = false;
-  if (!attr_done) {
+  static std::atomic<uint64_t> attr_done{0};
+  once_per_device(attr_done, [] {
     (void)hipFuncSetAttribute((const void*)moe_pf_gate_up_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
     (void)hipFuncSetAttribute((const void*)moe_pf_down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
-    attr_done = true;
-  }
+  });
   const auto grid = [&](int ncol) { return dim3((unsigned)(((int64_t)ncol * max_tiles + 7) / 8 * 8)); };
   hipLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds,
                      s, g, u, ws, x, H, ws.act, I);
