@@ -15,6 +15,7 @@
 //                        optional always-on shared expert RNE(routed + shared).
 //
 // No atomics touch floating-point data, so results are bitwise reproducible.
+#include <algorithm>
 #include <mutex>
 
 #include "moe_common.h"
@@ -1101,7 +1102,8 @@ extern "C" size_t q6moe_moe_workspace_size(int64_t tokens, int64_t top_k, int64_
     return 0;
   const size_t pf = ws_layout(tokens, top_k, experts, hidden, intermediate, shared_intermediate, kPrefillTile,
                               false).total;
-  if (!dec_supported(tokens, top_k, experts)) return pf;
+  const int64_t width = std::max(hidden, std::max(intermediate, shared_intermediate));
+  if (!dec_supported(tokens, top_k, experts, width)) return pf;
   const size_t dec = ws_layout(tokens, top_k, experts, hidden, intermediate, shared_intermediate, kPrefillTile,
                                true).total;
   return pf > dec ? pf : dec;
@@ -1185,11 +1187,13 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   Q6MOE_REQUIRE(a->compute == 0 || a->compute == 1, "moe_forward: compute must be 0 (bf16) or 1 (int8_q8)");
   const bool w8 = a->compute == 1;
   Q6MOE_REQUIRE(!(w8 && a->mode == 1), "moe_forward: the int8_q8 policy runs on the grouped kernels (mode 0 or 2)");
-  if (a->mode == 1 && !dec_supported(B, K, E)) {
-    set_error("moe_forward: decode mode needs tokens*top_k <= 1024, top_k <= 32, experts <= 256");
+  const int64_t width = std::max(H, std::max(I, Is));
+  if (a->mode == 1 && !dec_supported(B, K, E, width)) {
+    set_error("moe_forward: decode mode needs tokens <= 256, tokens*top_k <= 1024, experts <= 256 and "
+              "tokens*top_k*max(hidden, intermediate, shared_intermediate) < 2^30");
     return Q6MOE_ERR_INVALID;
   }
-  const bool decode = !w8 && dec_supported(B, K, E) && (a->mode == 1 || (a->mode == 0 && B <= 64));
+  const bool decode = !w8 && dec_supported(B, K, E, width) && (a->mode == 1 || (a->mode == 0 && B <= 64));
   const WsLayout L = ws_layout(B, K, E, H, I, Is, kPrefillTile, decode);
   if (workspace_bytes < L.total) {
     if (static_ws)

@@ -175,7 +175,10 @@ struct DecArgs {
   void* after_down;     // optional hipEvent_t
 };
 
-bool dec_supported(int64_t B, int64_t K, int64_t E);
+// The decode-step kernels take the call: tokens, routes and experts within
+// their limits, and routes x width (the largest of hidden, intermediate and
+// shared intermediate) BF16 values within 32-bit byte offsets.
+bool dec_supported(int64_t B, int64_t K, int64_t E, int64_t width);
 constexpr int kDecSharedTokens = 64;  // the shared expert joins the decode launches up to this many tokens
 int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s);
 

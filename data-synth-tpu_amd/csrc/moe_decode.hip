@@ -914,8 +914,9 @@ static int launch(const DecArgs& A, hipStream_t s) {
   return Q6MOE_OK;
 }
 
-bool dec_supported(int64_t B, int64_t K, int64_t E) {
-  return B <= kDecMaxTokens && B * K <= kDecMaxEntries && E <= kDecMaxExperts;
+bool dec_supported(int64_t B, int64_t K, int64_t E, int64_t width) {
+  // the token streams address rows with 32-bit byte offsets (routes x width BF16)
+  return B <= kDecMaxTokens && B * K <= kDecMaxEntries && E <= kDecMaxExperts && B * K * width * 2 < (1ll << 31);
 }
 
 template <int FG, int FD>

@@ -136,3 +136,21 @@ def test_library_rejects_bad_arguments_without_a_device():
     assert b"null" in lib.q6moe_last_error()
     rc = lib.q6moe_gguf_decode(ctypes.c_void_p(16), 99, 1, 32, ctypes.c_void_p(16), 0, None)
     assert rc == -3
+
+
+def test_decode_mode_rejects_token_rows_past_32_bit_offsets_without_a_device():
+    # 1024 routes x hidden 2^20 BF16 values = 2^31 bytes: the decode-step
+    # kernels address token rows with 32-bit byte offsets, so mode 1 refuses
+    # the call (mode 0 takes the grouped kernels instead). The checks run
+    # before any device work; the pointers are never dereferenced.
+    lib = _lib.load()
+    fake = ctypes.c_void_p(1 << 20)
+    tab = _lib.Table(14, fake, 1 << 40, None, 0)
+    args = _lib.MoeArgs(gate=tab, up=tab, down=tab, experts=8, hidden=1 << 20, intermediate=256,
+                        x=fake, ids=fake, weights=fake, tokens=256, top_k=4, out=fake, workspace=fake,
+                        workspace_bytes=0, mode=1)
+    assert lib.q6moe_moe_forward(ctypes.byref(args), None) == -1
+    assert b"decode mode" in lib.q6moe_last_error()
+    args.hidden = (1 << 20) - 256  # just under the bound: decode mode passes validation (then the workspace check)
+    assert lib.q6moe_moe_forward(ctypes.byref(args), None) == -1
+    assert b"decode mode" not in lib.q6moe_last_error()
