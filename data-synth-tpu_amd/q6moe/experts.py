@@ -46,8 +46,8 @@ GATE_UP_TYPES = ("Q6_K", "Q5_K", "Q4_K", "Q8_0")       # gate/up types the kerne
 class ExpertTable:
     """One projection for all experts, resident on the GPU.
 
-    ``data`` [E, q6moe_moe_table_bytes] unit-major tables (Q6_K or Q4_K); the
-    scales live inside the units, so ``scales`` is None.
+    ``data`` [E, q6moe_moe_table_bytes] unit-major tables (Q6_K, Q5_K, Q4_K,
+    Q8_0 or Q5_1); the scales live inside the units, so ``scales`` is None.
     """
 
     qtype: str
@@ -222,16 +222,36 @@ def _check_workspace(workspace, need, device):
     return workspace
 
 
+MODES = (0, 1, 2)  # kernel family: by token count, decode-step kernels, grouped (prefill) kernels
+
+
 class ExpertFFN:
-    """Callable returned by ``expert_parallel``."""
+    """Callable returned by ``expert_parallel``.
+
+    ``expert_parallel`` caches its result, so one object serves every caller
+    with the same configuration; it holds no per-call state. ``mode`` picks the
+    kernel family: 0 (the default) the decode-step kernels up to 64 tokens and
+    the grouped ones above, 1 always the decode-step kernels, 2 always the
+    grouped kernels. ``with_mode`` returns a copy that runs another family.
+    """
 
     def __init__(self, qtype, hidden, intermediate, mode=0, down_qtype=None, compute="bf16"):
+        if mode not in MODES:
+            raise ValueError(f"mode must be one of {MODES}")
         self.qtype = qtype
         self.down_qtype = down_qtype or qtype
         self.hidden = hidden
         self.intermediate = intermediate
-        self.mode = mode
+        self._mode = mode
         self.compute = compute
+
+    @property
+    def mode(self):
+        return self._mode
+
+    def with_mode(self, mode):
+        """This FFN with the kernel family ``mode`` (0, 1 or 2)."""
+        return ExpertFFN(self.qtype, self.hidden, self.intermediate, mode, self.down_qtype, self.compute)
 
     def workspace_bytes(self, tokens, top_k, experts, shared_intermediate=0):
         return int(_lib.load().q6moe_moe_workspace_size(

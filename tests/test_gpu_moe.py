@@ -55,11 +55,8 @@ def _run(L, device, mode=0, shared=None, weights=None, ids=None):
         sh = dict(gate=pack_experts(shared["gate"][None], q, Is, H, device),
                   up=pack_experts(shared["up"][None], q, Is, H, device),
                   down=pack_experts(shared["down"][None], qd, H, Is, device))
-    fn.mode = mode
-    try:
-        out = fn(*tabs, x, ids, w, shared=sh)
-    finally:
-        fn.mode = 0
+    fn = fn.with_mode(mode)
+    out = fn(*tabs, x, ids, w, shared=sh)
     return out.float().cpu().numpy(), (fn, tabs, x, ids, w, sh)
 
 
@@ -154,12 +151,8 @@ def test_shared_expert_repeated_calls(device, qtype, tokens, mode):
     want = _oracle(L, shared=L["shared"])
     got, ctx = _run(L, device, mode=mode, shared=L["shared"])
     assert_moe_close(got, want)
-    fn, tabs, x, ids, w, sh = ctx
-    fn.mode = mode
-    try:
-        outs = [fn(*tabs, x, ids, w, shared=sh) for _ in range(3)]
-    finally:
-        fn.mode = 0
+    fn, tabs, x, ids, w, sh = ctx  # fn runs ``mode``
+    outs = [fn(*tabs, x, ids, w, shared=sh) for _ in range(3)]
     for o in outs:
         np.testing.assert_array_equal(o.float().cpu().numpy(), got)
 
@@ -360,13 +353,10 @@ def test_shared_expert_router_gate_on_device(device):
         x = torch.from_numpy(L["x"]).to(device).to(torch.bfloat16)
         ids = torch.from_numpy(L["ids"]).to(device)
         w = torch.from_numpy(L["weights"]).to(device).to(torch.bfloat16)
-        fn.mode = mode
-        try:
-            got = fn(*tabs, x, ids, w, shared=shared).float().cpu().numpy()
-            scale = torch.from_numpy(oracle_moe.shared_gate(L["x"], router)).to(device).to(torch.bfloat16)
-            got2 = fn(*tabs, x, ids, w, shared=dict(shared, router=None, scale=scale)).float().cpu().numpy()
-        finally:
-            fn.mode = 0
+        fm = fn.with_mode(mode)
+        got = fm(*tabs, x, ids, w, shared=shared).float().cpu().numpy()
+        scale = torch.from_numpy(oracle_moe.shared_gate(L["x"], router)).to(device).to(torch.bfloat16)
+        got2 = fm(*tabs, x, ids, w, shared=dict(shared, router=None, scale=scale)).float().cpu().numpy()
         from oracle.gguf import dequantize_rows
 
         dec = dict(gate=bf16_round_np(dequantize_rows(sh["gate"], "Q6_K", 512)),

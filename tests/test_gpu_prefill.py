@@ -82,11 +82,7 @@ def test_prefill_workload_full_size_sampled(device):
                                  L["weights"][rows], types=("Q6_K",) * 3, hidden=2048, intermediate=768)
     assert_moe_close(got[rows], want)
     fn, tabs, x, ids, w, _ = ctx
-    fn.mode = 2
-    try:
-        again = fn(*tabs, x, ids, w).float().cpu().numpy()
-    finally:
-        fn.mode = 0
+    again = fn.with_mode(2)(*tabs, x, ids, w).float().cpu().numpy()
     np.testing.assert_array_equal(got, again)
     assert torch.isfinite(torch.from_numpy(got)).all()
 

@@ -93,12 +93,9 @@ def test_reference_routing_validation_gate_int8_q8(device, batch, mode):
     x = torch.from_numpy(source).to(device).to(torch.bfloat16)
     i = torch.from_numpy(ids).to(device)
     w = torch.from_numpy(weights).to(device).to(torch.bfloat16)
-    fn.mode = mode
-    try:
-        got = fn(*tabs, x, i, w).float().cpu().numpy()
-        zeros = fn(*tabs, x, i, torch.zeros_like(w)).float().cpu().numpy()
-    finally:
-        fn.mode = 0
+    fm = fn.with_mode(mode)
+    got = fm(*tabs, x, i, w).float().cpu().numpy()
+    zeros = fm(*tabs, x, i, torch.zeros_like(w)).float().cpu().numpy()
     np.testing.assert_allclose(got, want, atol=3e-3, rtol=3e-3)
     np.testing.assert_array_equal(got[np.all(weights == 0, axis=-1)], 0)
     np.testing.assert_array_equal(zeros, 0)
@@ -117,11 +114,7 @@ def test_int8_q8_policy_matches_oracle(device, qtype, tokens, mode):
     x = torch.from_numpy(L["x"]).to(device).to(torch.bfloat16)
     ids = torch.from_numpy(L["ids"]).to(device)
     w = torch.from_numpy(L["weights"]).to(device).to(torch.bfloat16)
-    fn.mode = mode
-    try:
-        got = fn(*tabs, x, ids, w).float().cpu().numpy()
-    finally:
-        fn.mode = 0
+    got = fn.with_mode(mode)(*tabs, x, ids, w).float().cpu().numpy()
     want = oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"], L["ids"], L["weights"],
                                  types=(qtype, qtype, "Q8_0"), hidden=512, intermediate=256, policy="int8_q8")
     assert_moe_close(got, want)

@@ -183,12 +183,9 @@ def test_reference_routing_validation_gate(device, batch, mode):
     x = torch.from_numpy(source).to(device).to(torch.bfloat16)
     i = torch.from_numpy(ids).to(device)
     w = torch.from_numpy(weights).to(device).to(torch.bfloat16)
-    fn.mode = mode
-    try:
-        got = fn(*tabs, x, i, w).float().cpu().numpy()
-        zeros = fn(*tabs, x, i, torch.zeros_like(w)).float().cpu().numpy()
-    finally:
-        fn.mode = 0
+    fm = fn.with_mode(mode)
+    got = fm(*tabs, x, i, w).float().cpu().numpy()
+    zeros = fm(*tabs, x, i, torch.zeros_like(w)).float().cpu().numpy()
     np.testing.assert_allclose(got, want, atol=3e-3, rtol=3e-3)
     np.testing.assert_array_equal(got[np.all(weights == 0, axis=-1)], 0)
     np.testing.assert_array_equal(zeros, 0)

@@ -154,3 +154,18 @@ def test_decode_mode_rejects_token_rows_past_32_bit_offsets_without_a_device():
     args.hidden = (1 << 20) - 256  # just under the bound: decode mode passes validation (then the workspace check)
     assert lib.q6moe_moe_forward(ctypes.byref(args), None) == -1
     assert b"decode mode" not in lib.q6moe_last_error()
+
+
+def test_expert_ffn_mode_copies_leave_the_cached_callable_alone():
+    from q6moe.experts import expert_parallel
+
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q6_K", hidden=512, intermediate=256)
+    assert fn is expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q6_K", hidden=512,
+                                 intermediate=256)
+    pre = fn.with_mode(2)
+    assert (fn.mode, pre.mode) == (0, 2) and pre is not fn
+    assert (pre.qtype, pre.down_qtype, pre.hidden, pre.intermediate, pre.compute) == ("Q6_K", "Q6_K", 512, 256, "bf16")
+    with pytest.raises(AttributeError):
+        fn.mode = 1
+    with pytest.raises(ValueError):
+        fn.with_mode(3)

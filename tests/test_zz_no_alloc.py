@@ -36,17 +36,14 @@ def _inputs(L, device, tokens):
 
 
 def _both(fn, tabs, device, x, ids, w, mode, shared=None):
-    fn.mode = mode
-    try:
-        want = fn(*tabs, x, ids, w, shared=shared)
-        args, out, keep = fn.args(*tabs, x, ids, w, shared=shared, with_workspace=False)
-        with torch.cuda.device(device):
-            rc = _noalloc()(ctypes.byref(args), _lib.stream_handle(device))
-        _lib.check(rc, "moe_forward_noalloc")
-        torch.cuda.synchronize()
-        del keep
-    finally:
-        fn.mode = 0
+    fn = fn.with_mode(mode)
+    want = fn(*tabs, x, ids, w, shared=shared)
+    args, out, keep = fn.args(*tabs, x, ids, w, shared=shared, with_workspace=False)
+    with torch.cuda.device(device):
+        rc = _noalloc()(ctypes.byref(args), _lib.stream_handle(device))
+    _lib.check(rc, "moe_forward_noalloc")
+    torch.cuda.synchronize()
+    del keep
     return want.view(torch.int16).cpu().numpy(), out.view(torch.int16).cpu().numpy()
 
 
