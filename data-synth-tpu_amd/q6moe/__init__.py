@@ -1,15 +1,18 @@
-"""q6moe: MI355X-native packed-weight (Q6_K / Q4_K) expert matmul and Q8 KV gather.
+"""q6moe: MI355X-native packed-weight expert matmul and INT8 KV cache.
 
-Host surface mirrors the reference operators of AhmadSaeedZaidi/data-synth-tpu:
+GGUF expert tables (Q6_K, Q5_K, Q4_K, Q8_0 gate/up; those or Q5_1 down) are
+decoded inside the matmul kernels. Host surface mirrors the reference
+operators of AhmadSaeedZaidi/data-synth-tpu:
 
 * ``pack_q6`` / ``unpack_q6`` / ``PackedQ6``   (kaggle/packed_q6/layout.py)
 * ``q6_matmul``                                (kaggle/packed_q6/kernel.py)
 * ``block_layout`` / ``dequantize_rows``       (kaggle/glm53_offload/gguf_quant.py)
 * ``expert_parallel`` / ``grouped_expert_parallel`` (kaggle/qwen38_tpu/experts.py,
-  grouped_experts.py)
+  grouped_experts.py); ``routes`` (math.py:277-281)
 * ``q8_matmul`` / ``bf16_q8_matmul`` / ``pack_q8`` (kaggle/qwen38_tpu/compute.py)
-* ``quantize`` / ``gather_scale_plane`` / ``read_quantized``
-  (kaggle/qwen38_tpu/attention_cache.py)
+* ``quantize`` / ``write_quantized`` / ``gather_scale_plane`` /
+  ``read_quantized`` (kaggle/qwen38_tpu/attention_cache.py), with the paged
+  forms ``write_paged`` / ``read_paged`` and ``paged_decode_attention``
 
 All device work runs in hand-written HIP kernels (libq6moe.so, gfx950).
 """
@@ -38,8 +41,13 @@ def __getattr__(name):
         from . import compute
 
         return getattr(compute, name)
-    if name in ("quantize", "gather_scale_plane", "read_quantized", "read_paged"):
+    if name in ("quantize", "write_quantized", "gather_scale_plane", "read_quantized", "write_paged", "read_paged",
+                "paged_decode_attention"):
         from . import attention_cache
 
         return getattr(attention_cache, name)
+    if name == "routes":
+        from . import router
+
+        return router.routes
     raise AttributeError(name)
