@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY. Nothing in the product package imports this
 package. Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
-leg of ``bench.py`` may import it, and only as the checker (or, in the bench,
+leg of ``bench.py`` may import it, and only to check results (or, in the bench,
 as the timed CPU baseline), never as the thing that is measured or shipped.
 
 Every function restates the algorithm of a reference file in plain NumPy and
