@@ -97,3 +97,33 @@ def test_decode_attention_c5_shape_sampled(device):
     got, qv = _run(device, pools, scales, table, q, lengths, P, KVH)
     rows = [2, 7]
     _check(got[rows], _want(pools, scales, table, qv, lengths, P, KVH, rows=rows))
+
+
+def _sweep_case(seed):
+    """A seeded attention shape: batch, KV heads, query heads per KV head, page
+    size, pages per sequence, ragged lengths and a few unmapped table entries."""
+    rng = np.random.default_rng(500 + seed)
+    batch = int(rng.integers(1, 6))
+    kvh = int(rng.choice([1, 2, 4]))
+    r = int(rng.integers(1, 9))
+    page_size = int(rng.choice([64, 128, 256]))
+    pps = int(rng.integers(1, 13))
+    lengths = [int(rng.integers(1, pps * page_size + 1)) for _ in range(batch)]
+    unmapped = int(rng.integers(0, 3)) if pps > 1 else 0
+    return batch, kvh, r, page_size, pps, lengths, unmapped
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_decode_attention_seeded_sweep(device, seed):
+    batch, kvh, r, page_size, pps, lengths, unmapped = _sweep_case(seed)
+    pages = batch * pps + 2
+    pools, scales, table, q = _case(900 + seed, batch, kvh, r, pages=pages, page_size=page_size, pps=pps)
+    rng = np.random.default_rng(seed)
+    for _ in range(unmapped):  # -1 or past the pool: read as zero codes and scales
+        table[rng.integers(batch), rng.integers(pps)] = -1 if rng.random() < 0.5 else pages + 5
+    print(f"[sweep] batch {batch} kvh {kvh} r {r} page {page_size} pps {pps} lengths {lengths}", flush=True)
+    got, qv = _run(device, pools, scales, table, q, lengths, page_size, kvh)
+    pz = [np.concatenate([p, np.zeros((1,) + p.shape[1:], p.dtype)]) for p in pools]
+    sz = [np.concatenate([s, np.zeros((1,) + s.shape[1:], s.dtype)]) for s in scales]
+    tz = np.where((table < 0) | (table >= pages), pages, table).astype(np.int32)
+    _check(got, _want(pz, sz, tz, qv, lengths, page_size, kvh))
