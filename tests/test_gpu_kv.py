@@ -124,3 +124,44 @@ def test_decode_attention_output_for_a_permuted_query(device):
     with pytest.raises(ValueError, match="out must be"):
         paged_decode_attention(q, *args[:2], *args[2:4], args[4], lengths, page_size=256, kv_heads=4,
                                out=torch.empty((2, 8, 64), dtype=torch.bfloat16, device=device))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_paged_read_seeded_sweep(device, seed):
+    # Seeded shapes: page size, pages per sequence, KV heads, head_dim (vector
+    # path when its rows split into 16-byte groups, scalar path otherwise),
+    # scale group, FP32 or BF16 scales, BF16 or FP32 output, and explicit
+    # indices (negative and past-the-end ones normalized as the reference does).
+    rng = np.random.default_rng(300 + seed)
+    B = int(rng.integers(1, 5))
+    P = int(rng.choice([1, 3, 16, 64, 256]))
+    pps = int(rng.integers(1, 6))
+    H = int(rng.integers(1, 5))
+    D = int(rng.choice([16, 32, 64, 128, 10, 48]))
+    group = int(rng.choice([g for g in (D, 16, 32, 8) if D % g == 0]))
+    pages = B * pps + int(rng.integers(0, 3))
+    pool = rng.integers(-127, 128, (pages, P, H, D), dtype=np.int8)
+    scales = rng.uniform(0, 0.05, (pages, P, H * D // group)).astype(np.float32)
+    sdt = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+    if sdt == torch.bfloat16:
+        scales = bf16_round(scales)
+    odt = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+    table = rng.permutation(pages)[: B * pps].astype(np.int32).reshape(B, pps)
+    idx = None
+    if rng.random() < 0.6:
+        idx = rng.integers(-pps * P - 3, pps * P + 3, (B, int(rng.integers(1, 40)))).astype(np.int32)
+    print(f"[sweep] B {B} P {P} pps {pps} H {H} D {D} group {group} scales {sdt} out {odt} "
+          f"indices {None if idx is None else idx.shape}", flush=True)
+    got = read_paged(torch.from_numpy(pool).to(device), torch.from_numpy(scales).to(device).to(sdt),
+                     torch.from_numpy(table).to(device), page_size=P, kv_heads=H, head_dim=D, group=group,
+                     indices=None if idx is None else torch.from_numpy(idx).to(device), dtype=odt)
+    want = oracle_kv.read_paged(pool, scales, table, P, H, D, group, idx)  # BF16 values as FP32
+    if odt == torch.bfloat16:
+        np.testing.assert_array_equal(_bits(got), bf16_bits(want))
+    else:
+        t = oracle_kv.normalize_index(np.broadcast_to(np.arange(pps * P), (B, pps * P)) if idx is None else idx,
+                                      pps * P)
+        page = table[np.arange(B)[:, None], t // P]
+        exact = (pool[page, t % P].astype(np.float32).reshape(B, t.shape[1], -1, group)
+                 * scales[page, t % P][..., None]).reshape(want.shape)
+        np.testing.assert_array_equal(got.cpu().numpy(), exact)
