@@ -170,7 +170,11 @@ typedef struct q6moe_moe_args {
   uint16_t* out;               /* BF16 [B, H] */
   void* workspace;             /* >= q6moe_moe_workspace_size(...) bytes, 256-byte aligned */
   size_t workspace_bytes;
-  int mode;                    /* 0 auto, 1 decode kernels, 2 grouped-GEMM (prefill) kernels */
+  /* kernel family: 0 the decode-step kernels up to 64 tokens where they apply, else the
+     grouped ones; 1 the decode-step kernels (B <= 256, B*top_k <= 1024, E <= 256 and
+     B*top_k*max(H, I, Is) < 2^30, else Q6MOE_ERR_INVALID); 2 the grouped-GEMM (prefill)
+     kernels, tiled on the matrix cores for Q6_K with H and I multiples of 256 */
+  int mode;
   /* optional profiling: NULL, or Q6MOE_MOE_EVENTS hipEvent_t handles recorded on ``stream``
      before routing, after routing, after gate/up, after down, after the combine */
   void* const* events;
