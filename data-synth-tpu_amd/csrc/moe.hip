@@ -1340,7 +1340,8 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
     }
     const int max_tiles = (int)(E + B * K / kPrefillTile + 1);
     down_done = fmt_dn == FMT_Q6 && !w8_dn;  // a Q6_K down runs tiled in the same call
-    launch_moe_prefill(g, u, d, ws, max_tiles, a->x, (int)H, (int)I, s, a->events ? a->events[2] : nullptr,
+    launch_moe_prefill(g, u, d, ws, max_tiles, a->x, (int)B, (int)(B * K), (int)H, (int)I, s,
+                       a->events ? a->events[2] : nullptr,
                        down_done);
   } else {
     dispatch_format(fmt, [&](auto fg) {

@@ -17,7 +17,7 @@
 // half, and decodes each half straight into MFMA A operands; decoded weights never leave registers. The 128 token
 // rows of the current K half sit in LDS (double-buffered, XOR-swizzled so the
 // 16 token columns of an MFMA read hit distinct banks), filled by direct
-// global->LDS DMA, and every wave multiplies them against its own rows. The
+// buffer->LDS DMA, and every wave multiplies them against its own rows. The
 // two workgroups of a CU run out of step, so one's decode (VALU) overlaps the
 // other's MFMAs.
 #include <type_traits>
@@ -66,17 +66,11 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   asm volatile("" : "+v"(v));
   return v;
 }
-__device__ __forceinline__ const uint8_t* sgpr_ptr(const uint8_t* p) {
-  const uint64_t v = (uint64_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const uint8_t*)(((uint64_t)hi << 32) | lo);
-}
-__device__ __forceinline__ void dma16(const uint8_t* base, uint32_t voff, void* lds) {
-  __builtin_amdgcn_global_load_lds(sgpr_ptr(base) + voff, LDS_PTR(lds), 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const uint8_t* base, uint32_t voff, void* lds) {
-  __builtin_amdgcn_global_load_lds(sgpr_ptr(base) + voff, LDS_PTR(lds), 4, 0, 0);
+// Direct buffer->LDS DMA of 16 bytes per lane: byte offset voff (per lane)
+// plus soff (wave-uniform) into the buffer r, no address arithmetic in VGPRs;
+// an offset past the buffer's end reads zeros.
+__device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, LDS_PTR(lds), 16, voff, soff, 0, 0);
 }
 // Workgroup barrier without the memory fence of __syncthreads (whose release
 // would wait for every outstanding DMA, including the ones prefetching the
@@ -168,13 +162,14 @@ __device__ __forceinline__ void tile_info(const MoeWs& ws, int tile, Tile& T) {
 // instructions at once right after the barrier.
 template <int NCG, typename RowFn>
 __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
-                                          const uint16_t* x, const uint32_t (&xoff)[NCG], int K,
+                                          const uint16_t* x, int x_rows, const uint32_t (&xoff)[NCG], int K,
                                           int64_t expert, f32x4 (&acc)[kUnits][NCG]) {
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int j = lane & 15, jA = lane >> 4;
   const int kbs = K / kQK;
   const int S = 2 * kbs;
-  const uint8_t* xb = reinterpret_cast<const uint8_t*>(x);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(x), (short)0, (int)((uint32_t)x_rows * (uint32_t)K * 2u), 0x00020000);
   const uint8_t* units[kUnits];
   int rgs[kUnits];
 #pragma unroll
@@ -203,7 +198,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
       static_assert(NCG % np == 0, "the token DMA splits evenly over the parts");
       uint8_t* xs = smem + slot * kHalfBytes + wave * NCG * 1024;
 #pragma unroll
-      for (int i = i0; i < i0 + per; ++i) dma16(xb + (int64_t)(kb * kQK + h * 128) * 2, xoff[i], xs + i * 1024);
+      for (int i = i0; i < i0 + per; ++i) bdma16(xr, xoff[i], (uint32_t)(kb * kQK + h * 128) * 2u, xs + i * 1024);
     }
   };
   auto issue = [&](int s, auto slot_c) {
@@ -284,7 +279,7 @@ __device__ __forceinline__ void with_column_groups(int nv, F&& f) {
 }  // namespace pf
 
 __global__ void __launch_bounds__(64 * pf::kWaves, 2)
-    moe_pf_gate_up_kernel(Proj gate, Proj up, MoeWs ws, const uint16_t* __restrict__ x, int hidden,
+    moe_pf_gate_up_kernel(Proj gate, Proj up, MoeWs ws, const uint16_t* __restrict__ x, int tokens, int hidden,
                           uint16_t* __restrict__ act, int inter) {
   using namespace pf;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -306,7 +301,7 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
       for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pf_stream<NCG>(smem, projs, unit_proj, [&](int) { return rgb; }, x, xoff, hidden, T.expert, acc);
+    pf_stream<NCG>(smem, projs, unit_proj, [&](int) { return rgb; }, x, tokens, xoff, hidden, T.expert, acc);
     const int row = rgb * 16 + 4 * jA;
 #pragma unroll
     for (int tg = 0; tg < NCG; ++tg) {
@@ -329,7 +324,7 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
 }
 
 __global__ void __launch_bounds__(64 * pf::kWaves, 2)
-    moe_pf_down_kernel(Proj down, MoeWs ws, const uint16_t* __restrict__ act, int inter,
+    moe_pf_down_kernel(Proj down, MoeWs ws, const uint16_t* __restrict__ act, int routes, int inter,
                        uint16_t* __restrict__ y, int hidden) {
   using namespace pf;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -351,7 +346,8 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
       for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pf_stream<NCG>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, xoff, inter, T.expert, acc);
+    pf_stream<NCG>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, routes, xoff, inter, T.expert,
+                   acc);
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
       const int row = (rgb + u) * 16 + 4 * jA;
@@ -376,7 +372,8 @@ bool pf_supported(int fmt, int64_t H, int64_t I) {
 int64_t pf_tile_routes() { return pf::kM; }
 
 int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
-                       const uint16_t* x, int H, int I, hipStream_t s, void* after_gate_up, bool with_down) {
+                       const uint16_t* x, int B, int routes, int H, int I, hipStream_t s, void* after_gate_up,
+                       bool with_down) {
   static std::atomic<uint64_t> attr_done{0};
   once_per_device(attr_done, [] {
     (void)hipFuncSetAttribute((const void*)moe_pf_gate_up_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
@@ -384,11 +381,11 @@ int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs&
   });
   const auto grid = [&](int ncol) { return dim3((unsigned)(((int64_t)ncol * max_tiles + 7) / 8 * 8)); };
   hipLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds,
-                     s, g, u, ws, x, H, ws.act, I);
+                     s, g, u, ws, x, B, H, ws.act, I);
   if (after_gate_up) (void)hipEventRecord((hipEvent_t)after_gate_up, s);
   if (with_down)
     hipLaunchKernelGGL(moe_pf_down_kernel, grid(H / (32 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds, s,
-                       d, ws, ws.act, I, ws.y, H);
+                       d, ws, ws.act, routes, I, ws.y, H);
   return Q6MOE_OK;
 }
 
