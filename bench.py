@@ -11,7 +11,9 @@ HBM addresses (default 4: about 0.8 GB of active expert bytes per rotation,
 over 3x the 256 MB Infinity Cache), so the weights stream from HBM. ``value``
 is algorithmic bytes per step (active experts' packed weights + activations +
 routing inputs + output, each byte once) over the mean time of ``--steps``
-back-to-back steps.
+back-to-back steps, after ``--warmup`` untimed steps (default 5000, about
+0.3 s: the CPU legs leave the GPU idle for seconds, and the first tens of
+milliseconds of steps after that run at a lower clock).
 
 Every workload is checked before it is timed (finite outputs, and, in the CPU
 baseline leg, the CPU oracle's values within tolerance: max relative error
@@ -145,18 +147,20 @@ def check_finite(name, t):
         raise CheckFailed(f"{name}: nonfinite output rejected before timing")
 
 
-def timed_reps(methods, reps=REPS, inner=10, warmup=2, seed=42):
+def timed_reps(methods, reps=REPS, inner=10, warmup=2, seed=42, warm_s=0.2):
     """Per-call device time (us) of each method: ``reps`` repetitions of
     ``inner`` back-to-back calls bracketed by HIP events on the current stream,
     the methods interleaved in a seeded random order per repetition
-    (kaggle/packed_q6/benchmark.py:127-149). Returns median/min/max per method."""
+    (kaggle/packed_q6/benchmark.py:127-149). Returns median/min/max per method.
+    Each method first runs untimed for ``warmup`` calls and at least ``warm_s``
+    seconds, so that the GPU clock has left its idle state (the CPU legs
+    before a measurement leave the GPU idle for seconds)."""
     import numpy as np
     import torch
 
     names = list(methods)
     for name in names:
-        for i in range(warmup):
-            methods[name](i)
+        warm_up(methods[name], warmup, warm_s)
     torch.cuda.synchronize()
     rng = np.random.default_rng(seed)
     samples = {n: [] for n in names}
@@ -174,6 +178,21 @@ def timed_reps(methods, reps=REPS, inner=10, warmup=2, seed=42):
             samples[name].append(a.elapsed_time(b) * 1e3 / inner)
             i += inner
     return {n: stats(v) for n, v in samples.items()}
+
+
+def warm_up(fn, calls, seconds):
+    """Untimed calls of fn(i): at least ``calls`` of them and at least ``seconds`` of wall time."""
+    import torch
+
+    t0 = time.perf_counter()
+    i = 0
+    while i < calls or time.perf_counter() - t0 < seconds:
+        fn(i)
+        i += 1
+        if i % 64 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return i
 
 
 def phase_means(fn, steps, n_events=5):
@@ -429,7 +448,7 @@ def measure_prefill(dev, steps, warmup, with_cpu):
                                          f"median of {runs} runs: {secs:.2f} s"}
     for _ in range(warmup):
         fn(*tabs, x, ids, w, workspace=ws, out=out)
-    t = timed_reps({"fused": lambda i: fn(*tabs, x, ids, w, workspace=ws, out=out)}, inner=max(1, steps // 5))
+    t = timed_reps({"fused": lambda i: fn(*tabs, x, ids, w, workspace=ws, out=out)}, inner=steps)
     step_us = t["fused"]["median"]
     ph = phase_means(lambda i, ev: fn(*tabs, x, ids, w, workspace=ws, out=out, events=ev), steps)
     tflops = PREFILL_FLOPS / (step_us * 1e-6) / 1e12
@@ -613,7 +632,7 @@ def measure_kv(dev, with_cpu):
         read_paged(p["k"], p["k_scale"], table, page_size=P, kv_heads=H, head_dim=D, out=ok)
         read_paged(p["v"], p["v_scale"], table, page_size=P, kv_heads=H, head_dim=D, out=ov)
 
-    t = timed_reps({"fused": call}, inner=5)
+    t = timed_reps({"fused": call}, inner=20)
     us = t["fused"]["median"]
     # one launch per read_paged: events around each K and V launch
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(61)]
@@ -648,7 +667,7 @@ def measure_kv(dev, with_cpu):
 
     attn(0)
     check_finite("kv_attention", oq)
-    ta = timed_reps({"fused": attn}, inner=5)
+    ta = timed_reps({"fused": attn}, inner=20)
     aus = ta["fused"]["median"]
     abytes = sum(pools[0][n].numel() * pools[0][n].element_size() for n in pools[0]) + table.numel() * 4 + \
         2 * q.numel() * 2
@@ -663,7 +682,9 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5000,
+                    help="untimed steps before the timed ones (the default, about 0.3 s of steps, brings the "
+                         "GPU clock out of its idle state after the CPU legs)")
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true",
                     help="skip the CPU oracle leg (and with it the oracle value checks; finiteness is still checked)")
@@ -683,8 +704,8 @@ def main():
         log("bench.py measures one GPU: the packed-expert path runs on a single MI355X here "
             "(it would shard by expert across GPUs); run with --gpus 1")
         return 2
-    if not (1 <= args.steps <= 100000 and 0 <= args.warmup <= 10000 and 1 <= args.layers <= 16):
-        log("steps must be 1..100000, warmup 0..10000, layers 1..16")
+    if not (1 <= args.steps <= 100000 and 0 <= args.warmup <= 100000 and 1 <= args.layers <= 16):
+        log("steps must be 1..100000, warmup 0..100000, layers 1..16")
         return 2
     if args.watchdog > 0 and not os.environ.get(WORKER_ENV):
         return supervise(args.watchdog)
