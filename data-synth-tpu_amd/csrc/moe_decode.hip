@@ -864,13 +864,17 @@ __global__ void __launch_bounds__(64)
 // 128-expert Q6_K layer (1 wave best for both kernels) and the 64-expert Q4_K
 // layer (1 token: 4 and 4; 8 tokens: down 2; 16 tokens and more: 1).
 static int split_for(int64_t items, bool split_long) {
-  static int simds = 0;
+  // SIMDs of the current device (4 per CU), looked up once per device id
+  static std::atomic<int> simds_of[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::atomic<int>& slot = simds_of[dev & 63];
+  int simds = slot.load(std::memory_order_relaxed);
   if (!simds) {
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     simds = 4 * cus;
+    slot.store(simds, std::memory_order_relaxed);
   }
   int ns = 1;
   while (ns < 4 && items * ns * 2 * 4 <= 10 * (int64_t)simds) ns *= 2;
