@@ -1257,7 +1257,6 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
       phases(sg, su, sd, dense, 1, (int)B, (int)Is, ws.sh_act, ws.sh_y, [](int) {});
       if ((rc = check_launch("moe shared expert kernels"))) return rc;
     }
-    mark(1);
     DecArgs D;
     D.gate = make_proj(a->gate, (int)I, (int)H);
     D.up = make_proj(a->up, (int)I, (int)H);
@@ -1288,6 +1287,8 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
       D.S.act = ws.sh_act;
       D.S.y = ws.sh_y;
     }
+    // events[1] and [2] take the gate/up kernel's own start and end timestamps
+    D.gate_up_start = a->events ? a->events[1] : nullptr;
     D.after_gate_up = a->events ? a->events[2] : nullptr;
     D.after_down = a->events ? a->events[3] : nullptr;
     if ((rc = launch_moe_decode(fmt, fmt_dn, D, s))) return rc;
@@ -1314,7 +1315,6 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
                        (int)B, (int)K, (int)E, nchunks, ws, chunk_cnt);
     if ((rc = check_launch("moe routing kernels"))) return rc;
   }
-  mark(1);
 
   TokenSrc routed{0, (int)B, ws.hdr, ws.active, ws.act_off, ws.route_tok};
   const int slots = (int)(E < B * K ? E : B * K);
@@ -1328,6 +1328,7 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   // gate/up + SwiGLU
   bool down_done = false;
   if (w8_gu) {
+    mark(1);
     int8_t* xq = reinterpret_cast<int8_t*>(w + L.xq);
     float* xq_s = reinterpret_cast<float*>(w + L.xq_s);
     launch_act_q8(a->x, B, (int)H, nullptr, xq, xq_s, s);
@@ -1340,10 +1341,11 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
     }
     const int max_tiles = (int)(E + B * K / kPrefillTile + 1);
     down_done = fmt_dn == FMT_Q6 && !w8_dn;  // a Q6_K down runs tiled in the same call
+    // events[1] and [2] take the gate/up kernel's own start and end timestamps
     launch_moe_prefill(g, u, d, ws, max_tiles, a->x, (int)B, (int)(B * K), (int)H, (int)I, s,
-                       a->events ? a->events[2] : nullptr,
-                       down_done);
+                       a->events ? a->events[1] : nullptr, a->events ? a->events[2] : nullptr, down_done);
   } else {
+    mark(1);
     dispatch_format(fmt, [&](auto fg) {
       launch_gate_up<decltype(fg)::value>(g, u, routed, slots, max_tokens, a->x, (int)H, (int)I, ws.act, s);
     });

@@ -171,6 +171,7 @@ struct DecArgs {
   const uint16_t* sh_y;
   const uint16_t* sh_scale;
   uint16_t* out;
+  void* gate_up_start;  // optional hipEvent_t: the gate/up kernel's start (with after_gate_up, its end)
   void* after_gate_up;  // optional hipEvent_t
   void* after_down;     // optional hipEvent_t
 };
@@ -191,8 +192,8 @@ int launch_pf_unpack(const Proj& p, int experts, uint16_t* out, hipStream_t s);
 bool pf_supported(int fmt, int64_t H, int64_t I);
 int64_t pf_tile_routes();
 int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
-                       const uint16_t* x, int B, int routes, int H, int I, hipStream_t s, void* after_gate_up,
-                       bool with_down);
+                       const uint16_t* x, int B, int routes, int H, int I, hipStream_t s, void* gate_up_start,
+                       void* after_gate_up, bool with_down);
 
 // ---------------------------------------------------------------------------
 // Unit decoders: 16 output rows x one 256-wide K block -> 8 MFMA A operands.

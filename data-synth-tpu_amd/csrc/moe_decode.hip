@@ -24,6 +24,8 @@
 // compile-time constant of the unit's position in its K block. One-wave
 // workgroups spread the waves evenly over the SIMDs. Weights are read once
 // per 16 routes of an expert.
+#include <hip/hip_ext.h>
+
 #include <type_traits>
 
 #include "moe_common.h"
@@ -907,9 +909,16 @@ static int launch(const DecArgs& A, hipStream_t s) {
   const int kb_i = (int)cdiv(A.I, kQK);
   const bool long_dn = kb_i % 2 == 0 && kb_i >= 4 && A.R.B * A.R.K <= 64;
   const int ns_gu = split_for(items_gu, false), ns_dn = split_for(items_dn, long_dn);
-  hipLaunchKernelGGL((moe_dec_gate_up_kernel<FG, kFullK>), dim3((unsigned)items_gu), dim3(64 * ns_gu),
-                     ns_gu * lds_gu, s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I, A.S);
-  if (A.after_gate_up) (void)hipEventRecord((hipEvent_t)A.after_gate_up, s);
+  if (A.gate_up_start && A.after_gate_up) {
+    // the events take the kernel's own start and end timestamps
+    hipExtLaunchKernelGGL((moe_dec_gate_up_kernel<FG, kFullK>), dim3((unsigned)items_gu), dim3(64 * ns_gu),
+                          ns_gu * lds_gu, s, (hipEvent_t)A.gate_up_start, (hipEvent_t)A.after_gate_up, 0, A.gate,
+                          A.up, A.R, A.T, A.x, A.H, A.act, A.I, A.S);
+  } else {
+    hipLaunchKernelGGL((moe_dec_gate_up_kernel<FG, kFullK>), dim3((unsigned)items_gu), dim3(64 * ns_gu),
+                       ns_gu * lds_gu, s, A.gate, A.up, A.R, A.T, A.x, A.H, A.act, A.I, A.S);
+    if (A.after_gate_up) (void)hipEventRecord((hipEvent_t)A.after_gate_up, s);
+  }
   hipLaunchKernelGGL((moe_dec_down_kernel<FD, kFullK>), dim3((unsigned)items_dn), dim3(64 * ns_dn),
                      ns_dn * lds_dn, s, A.down, A.T, A.act, A.I, A.contrib, A.H, A.S, A.R.B);
   if (A.after_down) (void)hipEventRecord((hipEvent_t)A.after_down, s);

@@ -20,6 +20,8 @@
 // buffer->LDS DMA, and every wave multiplies them against its own rows. The
 // two workgroups of a CU run out of step, so one's decode (VALU) overlaps the
 // other's MFMAs.
+#include <hip/hip_ext.h>
+
 #include <type_traits>
 
 #include "moe_common.h"
@@ -372,17 +374,23 @@ bool pf_supported(int fmt, int64_t H, int64_t I) {
 int64_t pf_tile_routes() { return pf::kM; }
 
 int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
-                       const uint16_t* x, int B, int routes, int H, int I, hipStream_t s, void* after_gate_up,
-                       bool with_down) {
+                       const uint16_t* x, int B, int routes, int H, int I, hipStream_t s, void* gate_up_start,
+                       void* after_gate_up, bool with_down) {
   static std::atomic<uint64_t> attr_done{0};
   once_per_device(attr_done, [] {
     (void)hipFuncSetAttribute((const void*)moe_pf_gate_up_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
     (void)hipFuncSetAttribute((const void*)moe_pf_down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
   });
   const auto grid = [&](int ncol) { return dim3((unsigned)(((int64_t)ncol * max_tiles + 7) / 8 * 8)); };
-  hipLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds,
-                     s, g, u, ws, x, B, H, ws.act, I);
-  if (after_gate_up) (void)hipEventRecord((hipEvent_t)after_gate_up, s);
+  if (gate_up_start && after_gate_up) {
+    // the events take the kernel's own start and end timestamps
+    hipExtLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds, s,
+                          (hipEvent_t)gate_up_start, (hipEvent_t)after_gate_up, 0, g, u, ws, x, B, H, ws.act, I);
+  } else {
+    hipLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds,
+                       s, g, u, ws, x, B, H, ws.act, I);
+    if (after_gate_up) (void)hipEventRecord((hipEvent_t)after_gate_up, s);
+  }
   if (with_down)
     hipLaunchKernelGGL(moe_pf_down_kernel, grid(H / (32 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds, s,
                        d, ws, ws.act, routes, I, ws.y, H);

@@ -176,7 +176,9 @@ typedef struct q6moe_moe_args {
      kernels, tiled on the matrix cores for Q6_K with H and I multiples of 256 */
   int mode;
   /* optional profiling: NULL, or Q6MOE_MOE_EVENTS hipEvent_t handles recorded on ``stream``
-     before routing, after routing, after gate/up, after down, after the combine */
+     before routing, after routing, after gate/up, after down, after the combine; on the
+     decode-step and tiled prefill paths the second and third take the gate/up kernel's own
+     start and end timestamps (hipExtLaunchKernel), so that their difference is its duration */
   void* const* events;
   /* optional BF16 [H] shared-expert router (kaggle/qwen38_tpu/math.py:283): the shared
      output is scaled per token by RNE(sigmoid(RNE(x . shared_router))), computed on the

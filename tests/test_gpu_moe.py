@@ -405,3 +405,24 @@ def test_checkpoint_format_mixes_match_oracle(device, qtype, down, tokens, mode)
     sh = L.get("shared")
     got, _ = _run(L, device, mode=mode, shared=sh)
     assert_moe_close(got, _oracle(L, shared=sh))
+
+
+@pytest.mark.parametrize("tokens,mode", [(8, 1), (300, 2)])
+def test_profiling_events_leave_results_and_bracket_gate_up(device, tokens, mode):
+    """The optional profiling events: the output is bitwise the one without
+    them, the five events are ordered, and the second and third (the gate/up
+    kernel's own start and end on the decode-step and tiled prefill paths)
+    span a positive part of the call."""
+    L = moe_layer(seed=5, experts=16, top_k=4, hidden=512, intermediate=256, tokens=tokens, pack=False)
+    plain, (fn, tabs, x, ids, w, _) = _run(L, device, mode=mode)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+    for ev in evs:
+        ev.record()
+    torch.cuda.synchronize()
+    for _ in range(3):
+        got = fn(*tabs, x, ids, w, events=evs)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.float().cpu().numpy().view(np.uint32), plain.view(np.uint32))
+        ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(4)]
+        assert all(m >= 0.0 for m in ms), ms
+        assert 0.0 < ms[1] <= evs[0].elapsed_time(evs[4]), ms
