@@ -13,8 +13,9 @@
 //        (experts.py:108). The combine kernel in moe.hip sums f32(y)*f32(r).
 //
 // Each wave owns 2 units (16 weight rows x one 256-wide K block) per K block,
-// loads a unit's bytes into registers in the step before the block's first K
-// half, and decodes each half straight into MFMA A operands; decoded weights never leave registers. The 128 token
+// loads a unit's bytes into one of two register sets during the previous
+// block's first K half, and decodes each half straight into MFMA A operands;
+// decoded weights never leave registers. The 128 token
 // rows of the current K half sit in LDS (double-buffered, XOR-swizzled so the
 // 16 token columns of an MFMA read hit distinct banks), filled by direct
 // buffer->LDS DMA, and every wave multiplies them against its own rows. The
@@ -37,17 +38,10 @@ constexpr int kWaves = 4;
 constexpr int kM = 128;            // routes per tile (MFMA column groups of 16)
 constexpr int kUnits = 2;          // units per wave per K block
 constexpr int kHalfBytes = kM * 128 * 2;  // one K half of the token tile (32 KB)
-constexpr int kAhead = 1;          // K halves in flight beyond the one being multiplied
-constexpr int kXStages = kAhead + 1;
+constexpr int kXStages = 2;        // token-tile stages in LDS: the K half being multiplied and the next
 constexpr int kWLoads = 5;         // weight loads per unit per K block (3 code chunks, sub-scales, d)
 // A tile of NCG (2, 4, 6 or 8) 16-route column groups: the token rows of a K
 // half take NCG KB per wave, i.e. NCG DMA instructions of 1 KB per wave.
-// Vector-memory instructions per wave of the step before a first half (the
-// most of any step). The waits below need exact counts only for steps still in
-// flight behind the one awaited, and with one step ahead there are none.
-template <int NCG>
-constexpr int step_ops() { return kUnits * kWLoads + NCG; }
-static_assert(kAhead == 1, "per-step wait counts assume one step in flight");
 constexpr int kLds = kXStages * kHalfBytes;
 
 static_assert(kLds <= 160 * 1024, "LDS budget");
@@ -153,14 +147,14 @@ __device__ __forceinline__ void tile_info(const MoeWs& ws, int tile, Tile& T) {
 
 // The streaming core shared by both kernels. ``rg_of(u)`` gives unit u's row
 // group; the token tile's rows come in by DMA at the per-lane offsets xoff.
-// K half s (block s/2, half s%2) is step s. Each wave loads its own weights
-// into registers and DMAs its share of the token tile into LDS stage
-// s % kXStages, kAhead steps before it is multiplied; one workgroup barrier
-// per step makes every wave's share visible and frees the stage read in the
-// step before. The next step's loads go out in four parts, one after each
-// fragment's MFMAs (unit 0, unit 1, then the two halves of the token DMA; for
-// a second-half step, which needs no weights, the DMA halves come first), so
-// that the four waves of a workgroup do not all queue their vector-memory
+// K half s (block s/2, half s%2) is step s. Each wave DMAs its share of the
+// token tile into LDS stage s % kXStages one step before it is multiplied,
+// and loads its own weights into registers a step and a half ahead; one
+// workgroup barrier per step makes every wave's share visible and frees the
+// stage read in the step before. The next step's loads go out in four parts,
+// one after each fragment's MFMAs (the two halves of the token DMA, then, in a
+// first-half step, the next block's weights for unit 0 and unit 1), so that
+// the four waves of a workgroup do not all queue their vector-memory
 // instructions at once right after the barrier.
 template <int NCG, typename RowFn>
 __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
@@ -180,54 +174,53 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     units[u] = p.data + expert * p.dstride;
     rgs[u] = rg_of(u);
   }
-  // One register set per unit: a K block's weights arrive during the step
-  // before its first half (once the previous block's second half is decoded)
-  // and serve both of its halves.
-  static_assert(kXStages == 2, "a K block's weights serve the steps of slots 0 and 1");
-  BlockRegs wr[kUnits];
-  // For a first-half step, part p < kUnits loads unit p's weights and the
-  // remaining parts split the token DMA; a second-half step only DMAs, in the
-  // first parts
-  auto issue_part = [&](int s, auto slot_c, auto part_c) {
+  // Two register sets per unit, one per K block parity: block b+1's weights
+  // are loaded during the first half of block b (after that step's token
+  // DMA), so they have a step and a half to arrive; the second-half step that
+  // follows waits only for its token DMA.
+  static_assert(kXStages == 2, "two K halves per block");
+  BlockRegs wr[2][kUnits];
+  // Issued step s (the step after the current one): token DMA in parts 0 and
+  // 1; for a second-half s (block b = s/2), block b+1's weights in parts 2
+  // and 3 (unit part-2) into register set ``wset``.
+  auto issue_part = [&](int s, auto slot_c, auto part_c, auto wset_c) {
     constexpr int slot = decltype(slot_c)::value;
     constexpr int part = decltype(part_c)::value;
+    constexpr int wset = decltype(wset_c)::value;
     const int kb = s >> 1, h = s & 1;
-    if constexpr (slot == 0 && part < kUnits) {
-      load_block(units[part], kbs, rgs[part], kb, lane, wr[part]);  // s even: h == 0
-    } else if constexpr (slot == 0 || part < 4 - kUnits) {
-      // second-half steps load no weights: their token DMA goes out in the first parts
-      constexpr int np = 4 - kUnits, per = NCG / np, i0 = (slot == 0 ? part - kUnits : part) * per;
-      static_assert(NCG % np == 0, "the token DMA splits evenly over the parts");
+    if constexpr (part < 2) {
+      static_assert(NCG % 2 == 0, "the token DMA splits evenly over two parts");
+      constexpr int per = NCG / 2, i0 = part * per;
       uint8_t* xs = smem + slot * kHalfBytes + wave * NCG * 1024;
 #pragma unroll
       for (int i = i0; i < i0 + per; ++i) bdma16(xr, xoff[i], (uint32_t)(kb * kQK + h * 128) * 2u, xs + i * 1024);
+    } else if constexpr (slot == 1 && part - 2 < kUnits) {
+      if (kb + 1 < kbs) load_block(units[part - 2], kbs, rgs[part - 2], kb + 1, lane, wr[wset][part - 2]);
     }
   };
-  auto issue = [&](int s, auto slot_c) {
-    static_for<0, 4>([&](auto pc) { issue_part(s, slot_c, pc); });
-  };
-  auto step = [&](int s, auto slot_c) {
+  auto step = [&](int s, auto slot_c, auto set_c) {
     constexpr int slot = decltype(slot_c)::value;
-    // this step's loads have landed once at most the younger steps' remain
-    const int younger = S - 1 - s < kAhead - 1 ? S - 1 - s : kAhead - 1;
-    static_for<0, kAhead>([&](auto yc) {
-      constexpr int y = decltype(yc)::value;
-      if (younger == y) wait_vm<y * step_ops<NCG>()>();
-    });
+    constexpr int set = decltype(set_c)::value;
+    // this step's token DMA has landed once at most the next block's weight
+    // loads (issued after it, in a first-half step) remain
+    if (slot == 1 && (s >> 1) + 1 < kbs)
+      wait_vm<kUnits * kWLoads>();
+    else
+      wait_vm<0>();
     wg_barrier();  // every wave's share of this step's tile is in LDS; the oldest stage is free
-    // The wait above covered this step's weight registers. Re-define them here
-    // so that the compiler does not also wait, after the next step's loads are
-    // issued, for everything in flight before decoding them.
+    // The wait above covered this block's weight registers. Re-define them
+    // here so that the compiler does not also wait, after the next step's
+    // loads are issued, for everything in flight before decoding them.
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
-      BlockRegs& w = wr[u];
+      BlockRegs& w = wr[set][u];
       asm volatile("" : "+v"(w.c0), "+v"(w.c1), "+v"(w.c2), "+v"(w.sc), "+v"(w.d));
     }
-    const bool more = s + kAhead < S;
+    const bool more = s + 1 < S;
     const uint8_t* xs = smem + slot * kHalfBytes;
     u32x4 a[kUnits][4];
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) decode_half(wr[u], slot, lane, a[u]);  // slot == s % 2 == h
+    for (int u = 0; u < kUnits; ++u) decode_half(wr[set][u], slot, lane, a[u]);  // slot == s % 2 == h
     static_for<0, 4>([&](auto fc) {
       constexpr int f = decltype(fc)::value;
       const int c = xfrag_gran(f, jA);
@@ -238,17 +231,24 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
         for (int u = 0; u < kUnits; ++u) acc[u][tg] = mfma16(a[u][f], xv, acc[u][tg]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if (more) issue_part(s + kAhead, std::integral_constant<int, (slot + kAhead) % kXStages>{}, fc);
+      if (more)
+        issue_part(s + 1, std::integral_constant<int, 1 - slot>{}, fc, std::integral_constant<int, 1 - set>{});
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  static_for<0, kAhead>([&](auto ic) {
-    if (decltype(ic)::value < S) issue(decltype(ic)::value, ic);
+  // prologue: block 0's weights and step 0's token DMA
+#pragma unroll
+  for (int u = 0; u < kUnits; ++u) load_block(units[u], kbs, rgs[u], 0, lane, wr[0][u]);
+  static_for<0, 2>([&](auto pc) {
+    issue_part(0, std::integral_constant<int, 0>{}, pc, std::integral_constant<int, 1>{});
   });
-  for (int s0 = 0; s0 < S; s0 += kXStages) {
-    static_for<0, kXStages>([&](auto ic) {
-      if (s0 + decltype(ic)::value < S) step(s0 + decltype(ic)::value, ic);
-    });
+  for (int s0 = 0; s0 < S; s0 += 4) {
+    step(s0, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+    step(s0 + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+    if (s0 + 2 < S) {
+      step(s0 + 2, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+      step(s0 + 3, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    }
   }
 }
 
