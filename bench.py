@@ -12,10 +12,12 @@ over 3x the 256 MB Infinity Cache), so the weights stream from HBM. ``value``
 is algorithmic bytes per step (active experts' packed weights + activations +
 routing inputs + output, each byte once) over the mean time of ``--steps``
 back-to-back steps, after ``--warmup`` untimed steps (default 5000, about
-0.3 s). The per-phase timing and the interleaved repetitions of the headline
-workload run before its timed steps: the CPU legs leave the GPU idle for
-seconds, and the first tens of milliseconds of steps after that run at a
-lower clock.
+0.3 s). The interleaved repetitions of the headline workload, then its
+per-phase event timing, run before its timed steps: the CPU legs leave the GPU
+idle for seconds, and the first tens of milliseconds of steps after that run
+at a lower clock. ``extras.hbm_copy`` is a plain 1 GiB device-to-device copy
+timed in the same run, the practical streaming ceiling beside the 8 TB/s spec
+that the rooflines use as their peak.
 
 Every workload is checked before it is timed (finite outputs, and, in the CPU
 baseline leg, the CPU oracle's values within tolerance: max relative error
@@ -212,6 +214,32 @@ def phase_means(fn, steps, n_events=5):
         fn(i, evs[i])
     torch.cuda.synchronize()
     return np.array([[row[j].elapsed_time(row[j + 1]) for j in range(n_events - 1)] for row in evs]).mean(0) * 1e3
+
+
+def copy_ceiling(dev, mib=1024, reps=REPS):
+    """A plain device-to-device copy of ``mib`` MiB (torch's copy kernel): the
+    read + write bytes over its median time, as the practical HBM rate beside
+    the 8 TB/s spec peak."""
+    import numpy as np
+    import torch
+
+    src = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    us = []
+    for _ in range(reps):
+        a.record()
+        dst.copy_(src)
+        b.record()
+        torch.cuda.synchronize()
+        us.append(a.elapsed_time(b) * 1e3)
+    del src, dst
+    med = float(np.median(us))
+    return {"value": round(2 * (mib << 20) / (med * 1e-6) / 1e9, 1), "unit": "GB/s",
+            "note": f"device-to-device copy of {mib} MiB (read + write bytes), median of {reps}: {med:.1f} us"}
 
 
 def copies_for(nbytes, lo=2, hi=16):
@@ -805,14 +833,15 @@ def run(args):
         for name, o in base_out.items():
             check_finite(name, o)
 
-    # Per-kernel durations with HIP events recorded between the launches, and
-    # interleaved repetitions of the fused step against the decode-then-GEMM
-    # baselines. They run before the headline timing, so that the GPU has left
-    # the idle clock of the CPU leg above when the timed steps start.
-    ph = phase_means(step, args.steps)
-    gu_bytes = active * 2 * Q6_PROJ_BYTES + TOKENS * HIDDEN * 2 + routes * INTER * 2
+    # Interleaved repetitions of the fused step against the decode-then-GEMM
+    # baselines (each method warmed up first), then per-kernel durations from
+    # HIP events stamped at the launches. They run before the headline timing,
+    # so that the GPU has left the idle clock of the CPU leg above when the
+    # timed steps start.
     reps = timed_reps({"fused": step, "decode_then_bf16_gemm": baselines.decode_then_gemm,
                        "predecoded_bf16_gemm": baselines.predecoded}, inner=20)
+    ph = phase_means(step, max(args.steps, 50))
+    gu_bytes = active * 2 * Q6_PROJ_BYTES + TOKENS * HIDDEN * 2 + routes * INTER * 2
 
     for i in range(args.warmup):
         step(i)
@@ -886,7 +915,8 @@ def run(args):
         log("timing the paged KV gather and the fused decode attention (seed 4) ...")
         configs["kv_gather"], kv_attention = measure_kv(dev, with_cpu)
         log("timing the Q6_K gate/up + Q8_0 down step ...")
-        result["extras"] = {"q8_0_down": measure_q8_down(dev), "kv_attention": kv_attention}
+        result["extras"] = {"q8_0_down": measure_q8_down(dev), "kv_attention": kv_attention,
+                            "hbm_copy": copy_ceiling(dev)}
     if "prefill" in configs:
         result["prefill"] = configs["prefill"]
     result["configs"] = configs
