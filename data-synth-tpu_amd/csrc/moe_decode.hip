@@ -772,9 +772,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
   }
   const int dn_x = (groups + kDownRows - 1) / kDownRows;
   const int slot = (item - sh_items) / dn_x;
+  // The slot's tables are read together with the active-slot count (every
+  // slot below max_slots <= E is in bounds; an inactive one's values are
+  // never used), so the weight stream's expert is known one load latency
+  // after the start rather than two.
+  const int t0 = T.slot_t0[slot], cnt = T.slot_cnt[slot], expert = T.slot_e[slot];
+  asm volatile("" ::: "memory");  // keeps the loads above issued here, not sunk below the branches
   if (slot >= T.hdr[0]) return;
-  const int t0 = T.slot_t0[slot], cnt = T.slot_cnt[slot];
-  const WStream<FMT> wd(down, T.slot_e[slot], lane);
+  const WStream<FMT> wd(down, expert, lane);
   const int rg0 = ((item - sh_items) % dn_x) * kDownRows;
   const int kb0 = wave * down.kb / ns, kb1 = (wave + 1) * down.kb / ns;
   for (int tc = 0; tc < cnt; tc += kPassTokens) {
@@ -825,10 +830,22 @@ __global__ void __launch_bounds__(64)
   const int b = blockIdx.x;
   const int h = (blockIdx.y * 64 + threadIdx.x) * 4;
   if (h >= hidden) return;
-  const int m = T.tok_n[b];
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const float* base = contrib + (int64_t)b * K * hidden + h;
-  for (int r0 = 0; r0 < m; r0 += 8) {
+  // The first 8 rank rows are loaded together with the token's route count,
+  // without waiting for it (rows past K repeat row K-1, so every load is in
+  // bounds), then only its m routes are summed; later rows, for top-k above
+  // 8, after it.
+  f32x4 v0[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    v0[i] = *reinterpret_cast<const f32x4*>(base + (int64_t)(i < K ? i : K - 1) * hidden);
+  asm volatile("" ::: "memory");  // keeps the loads above issued here, not sunk into the sum's branches
+  const int m = T.tok_n[b];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (i < m) acc += v0[i];
+  for (int r0 = 8; r0 < m; r0 += 8) {
     f32x4 v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
