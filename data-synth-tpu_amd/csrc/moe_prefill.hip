@@ -145,8 +145,32 @@ __device__ __forceinline__ void tile_info(const MoeWs& ws, int tile, Tile& T) {
   T.nv = d.nv;
 }
 
+// Token rows of this wave's token-tile DMA: instruction i fills granules
+// (wave*NCG + i)*64 + lane, i.e. token t = that/16. All rows are read before
+// any is used, so a row table's loads are in flight together.
+template <int NCG, typename RowOf>
+__device__ __forceinline__ void tile_rows(int (&rows)[NCG], RowOf row_of) {
+  const int wave = wave_id(), lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < NCG; ++i) rows[i] = row_of(((wave * NCG + i) * 64 + lane) >> 4);
+}
+
+// Per-lane byte offsets of those DMA instructions: row rows[i], swizzled
+// granule (p % 16) ^ (t % 16) of p = (wave*NCG + i)*64 + lane, t = p/16.
+template <int NCG>
+__device__ __forceinline__ void x_offsets(uint32_t (&xoff)[NCG], const int (&rows)[NCG], int K) {
+  const int wave = wave_id(), lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < NCG; ++i) {
+    const int p = (wave * NCG + i) * 64 + lane;
+    const int t = p >> 4, c = (p & 15) ^ (t & 15);
+    xoff[i] = opaque((uint32_t)((rows[i] * K + c * 8) * 2));
+  }
+}
+
 // The streaming core shared by both kernels. ``rg_of(u)`` gives unit u's row
-// group; the token tile's rows come in by DMA at the per-lane offsets xoff.
+// group and ``row_of(t)`` the x row of the tile's token t; the token rows come
+// in by DMA at per-lane offsets computed in the prologue.
 // K half s (block s/2, half s%2) is step s. Each wave DMAs its share of the
 // token tile into LDS stage s % kXStages one step before it is multiplied,
 // and loads its own weights into registers a step and a half ahead; one
@@ -156,10 +180,10 @@ __device__ __forceinline__ void tile_info(const MoeWs& ws, int tile, Tile& T) {
 // first-half step, the next block's weights for unit 0 and unit 1), so that
 // the four waves of a workgroup do not all queue their vector-memory
 // instructions at once right after the barrier.
-template <int NCG, typename RowFn>
+template <int NCG, typename RowFn, typename RowOf>
 __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
-                                          const uint16_t* x, int x_rows, const uint32_t (&xoff)[NCG], int K,
-                                          int64_t expert, f32x4 (&acc)[kUnits][NCG]) {
+                                          const uint16_t* x, int x_rows, RowOf row_of, int K, int64_t expert,
+                                          f32x4 (&acc)[kUnits][NCG]) {
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int j = lane & 15, jA = lane >> 4;
   const int kbs = K / kQK;
@@ -180,6 +204,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
   // follows waits only for its token DMA.
   static_assert(kXStages == 2, "two K halves per block");
   BlockRegs wr[2][kUnits];
+  uint32_t xoff[NCG];  // per-lane byte offsets of the token rows, set in the prologue
   // Issued step s (the step after the current one): token DMA in parts 0 and
   // 1; for a second-half s (block b = s/2), block b+1's weights in parts 2
   // and 3 (unit part-2) into register set ``wset``.
@@ -236,9 +261,17 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
       __builtin_amdgcn_sched_barrier(0);
     });
   };
-  // prologue: block 0's weights and step 0's token DMA
+  // prologue: the tile's token rows (a table read, for gate/up), block 0's
+  // weights, then step 0's token DMA once the rows have arrived; the weights
+  // are in flight meanwhile
+  {
+    int rows[NCG];
+    tile_rows(rows, row_of);
 #pragma unroll
-  for (int u = 0; u < kUnits; ++u) load_block(units[u], kbs, rgs[u], 0, lane, wr[0][u]);
+    for (int u = 0; u < kUnits; ++u) load_block(units[u], kbs, rgs[u], 0, lane, wr[0][u]);
+    asm volatile("" ::: "memory");  // every load above issues before the offsets wait on the rows
+    x_offsets(xoff, rows, K);
+  }
   static_for<0, 2>([&](auto pc) {
     issue_part(0, std::integral_constant<int, 0>{}, pc, std::integral_constant<int, 1>{});
   });
@@ -249,19 +282,6 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
       step(s0 + 2, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
       step(s0 + 3, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
     }
-  }
-}
-
-// Per-lane token-tile DMA offsets: instruction i of this wave fills granules
-// (wave*NCG + i)*64 + lane, i.e. token t = that/16, swizzled granule l%16.
-template <int NCG, typename RowOf>
-__device__ __forceinline__ void x_offsets(uint32_t (&xoff)[NCG], int K, RowOf row_of) {
-  const int wave = wave_id(), lane = threadIdx.x & 63;
-#pragma unroll
-  for (int i = 0; i < NCG; ++i) {
-    const int p = (wave * NCG + i) * 64 + lane;
-    const int t = p >> 4, c = (p & 15) ^ (t & 15);
-    xoff[i] = opaque((uint32_t)((row_of(t) * K + c * 8) * 2));
   }
 }
 
@@ -294,8 +314,6 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
   const int rgb = col * kWaves + wave;  // this wave's row group (gate and up)
   with_column_groups(T.nv, [&](auto ncg_c) {
     constexpr int NCG = decltype(ncg_c)::value;
-    uint32_t xoff[NCG];
-    x_offsets(xoff, hidden, [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; });
     const Proj projs[2] = {gate, up};
     const int unit_proj[kUnits] = {0, 1};
     f32x4 acc[kUnits][NCG];
@@ -303,7 +321,8 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
       for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pf_stream<NCG>(smem, projs, unit_proj, [&](int) { return rgb; }, x, tokens, xoff, hidden, T.expert, acc);
+    pf_stream<NCG>(smem, projs, unit_proj, [&](int) { return rgb; }, x, tokens,
+                   [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; }, hidden, T.expert, acc);
     const int row = rgb * 16 + 4 * jA;
 #pragma unroll
     for (int tg = 0; tg < NCG; ++tg) {
@@ -339,8 +358,6 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
   const int rgb = col * 2 * kWaves + 2 * wave;  // this wave's two row groups
   with_column_groups(T.nv, [&](auto ncg_c) {
     constexpr int NCG = decltype(ncg_c)::value;
-    uint32_t xoff[NCG];
-    x_offsets(xoff, inter, [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); });
     const Proj projs[1] = {down};
     const int unit_proj[kUnits] = {0, 0};
     f32x4 acc[kUnits][NCG];
@@ -348,8 +365,8 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
       for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pf_stream<NCG>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, routes, xoff, inter, T.expert,
-                   acc);
+    pf_stream<NCG>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, routes,
+                   [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); }, inter, T.expert, acc);
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
       const int row = (rgb + u) * 16 + 4 * jA;
