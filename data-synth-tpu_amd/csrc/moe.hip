@@ -29,21 +29,31 @@ constexpr int kChunkWords = kChunk / 32;
 
 __device__ __forceinline__ bool is_route(float r) { return r != 0.f || r != r; }
 
-// Copies n (>= 1) consecutive values of src into LDS, converted by cv. Eight
-// loads per lane are in flight at once (clamped in-range addresses, stores
-// masked), so a chunk's rows arrive in one or two memory round trips.
-template <typename D, typename S, typename Cv>
-__device__ __forceinline__ void stage_chunk(D* dst, const S* __restrict__ src, int n, Cv cv) {
+// Copies n (>= 1) consecutive values of two arrays into LDS, converted by
+// cva and cvb. Every lane's loads of both (eight of each per pass) are issued
+// before its first store, so a chunk's rows arrive in one memory round trip
+// per 8 * kChunk values. Indexes past n are clamped to n - 1 for the load and
+// the store alike (a repeat store of element n-1's own value), so no load or
+// store sits behind a branch.
+template <typename DA, typename SA, typename CvA, typename DB, typename SB, typename CvB>
+__device__ __forceinline__ void stage_chunk2(DA* da, const SA* __restrict__ sa, CvA cva, DB* db,
+                                             const SB* __restrict__ sb, CvB cvb, int n) {
   for (int i0 = threadIdx.x; i0 < n; i0 += 8 * kChunk) {
-    S v[8];
+    SA va[8];
+    SB vb[8];
+    int ix[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int i = i0 + u * kChunk;
-      v[u] = src[i < n ? i : n - 1];
+      ix[u] = i0 + u * kChunk < n ? i0 + u * kChunk : n - 1;
+      va[u] = sa[ix[u]];
+      vb[u] = sb[ix[u]];
     }
+    asm volatile("" ::: "memory");  // the loads above stay ahead of the stores below
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (i0 + u * kChunk < n) dst[i0 + u * kChunk] = cv(v[u]);
+    for (int u = 0; u < 8; ++u) {
+      da[ix[u]] = cva(va[u]);
+      db[ix[u]] = cvb(vb[u]);
+    }
   }
 }
 
@@ -62,8 +72,8 @@ __global__ void __launch_bounds__(kChunk)
   const int nb = B - b0 < kChunk ? B - b0 : kChunk;
   const int64_t e0 = (int64_t)b0 * K;
   for (int e = tid; e < E; e += kChunk) cnt[e] = 0;
-  stage_chunk(s_ids, ids + e0, nb * K, [](int v) { return v; });
-  stage_chunk(s_w, wts + e0, nb * K, [](uint16_t v) { return bf16_to_float(v); });
+  stage_chunk2(s_ids, ids + e0, [](int v) { return v; }, s_w, wts + e0, [](uint16_t v) { return bf16_to_float(v); },
+               nb * K);
   __syncthreads();
   if (tid < nb && K <= 8) {
     // top_k <= 8: the token's entries in registers, every loop unrolled (the
@@ -196,10 +206,13 @@ __global__ void __launch_bounds__(kChunk)
   const int nb = B - b0 < kChunk ? B - b0 : kChunk;
   const int64_t e0 = (int64_t)b0 * K;
   for (int i = tid; i < E * kChunkWords; i += kChunk) bits[i / kChunkWords][i % kChunkWords] = 0u;
-  for (int e = tid; e < E; e += kChunk)
-    s_pos[e] = chunk_pos[(int64_t)nchunks * E + e] + chunk_pos[(int64_t)blockIdx.x * E + e];
-  stage_chunk(s_ids, ids + e0, nb * K, [](int v) { return v; });
-  stage_chunk(s_r, ws.ent_r + e0, nb * K, [](float v) { return v; });
+  // one expert per lane (E <= kChunk): its first position and this chunk's
+  // offset within it, loaded together with the chunk's entries
+  static_assert(kRouteMaxExperts <= kChunk, "one lane per expert");
+  const int ec = tid < E ? tid : E - 1;
+  const int pe0 = chunk_pos[(int64_t)nchunks * E + ec], pe1 = chunk_pos[(int64_t)blockIdx.x * E + ec];
+  stage_chunk2(s_ids, ids + e0, [](int v) { return v; }, s_r, ws.ent_r + e0, [](float v) { return v; }, nb * K);
+  if (tid < E) s_pos[tid] = pe0 + pe1;
   __syncthreads();
   if (tid < nb)
     for (int kk = 0; kk < K; ++kk)
