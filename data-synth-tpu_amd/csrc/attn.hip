@@ -59,11 +59,18 @@ __device__ __forceinline__ int attn_len(const AttnParams& p, int b) {
   return n < 1 ? 1 : (n > p.cap ? p.cap : n);
 }
 
-// Pool row of token t0 of sequence b, or -1 for an unmapped page (read as 0).
-// A wave's 64 tokens t0 + [0, 64) (t0 a multiple of 64) lie in one page,
-// since page_size is a multiple of 64: one table lookup per wave.
-__device__ __forceinline__ int64_t attn_base_row(const AttnParams& p, int b, int t0) {
-  const int64_t pg = p.table[(int64_t)b * p.pps + t0 / p.page];
+// Page-table entry of token t0 of sequence b. The page index is clamped into
+// the sequence's row, so the load is in bounds for any t0 and can be issued
+// before the sequence length is known. A wave's 64 tokens t0 + [0, 64) (t0 a
+// multiple of 64) lie in one page, since page_size is a multiple of 64: one
+// table lookup per wave.
+__device__ __forceinline__ int64_t attn_page(const AttnParams& p, int b, int t0) {
+  const int pi = t0 / p.page;
+  return p.table[(int64_t)b * p.pps + (pi < p.pps ? pi : p.pps - 1)];
+}
+
+// Pool row of token t0 on page pg, or -1 for an unmapped page (read as 0).
+__device__ __forceinline__ int64_t attn_row(const AttnParams& p, int64_t pg, int t0) {
   return pg < 0 || pg >= p.pool_pages ? -1 : pg * p.page + t0 % p.page;
 }
 
@@ -87,7 +94,7 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnParams p) {
   }
   const float kDiv = static_cast<float>(11.313708498984761);  // float32(128 ** 0.5) (attention_cache.py:163)
   const int64_t rowbytes = (int64_t)p.kvh * kAttnD;
-  const int64_t base = attn_base_row(p, b, t0);
+  const int64_t base = attn_row(p, attn_page(p, b, t0), t0);
   // the wave's rows start at pool row base (wave-uniform); the lane adds its
   // token row col and channel group 32-bit offsets, row block rb adds 16 rows
   const int8_t* kw = p.kc + (base < 0 ? 0 : base) * rowbytes + kh * kAttnD;
@@ -196,16 +203,39 @@ __global__ void __launch_bounds__(256) attn_pv_kernel(AttnParams p) {
   __shared__ float red[4][kAttnR][kAttnD];                              // per-wave partial sums
   const int chunk = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int n = attn_len(p, b);
   const int c0 = chunk * kAttnChunk;
+  const int r16 = lane & 15, kg = lane >> 4;
+  // The wave's page entry and the heads' softmax statistics (scalar loads;
+  // the head index is clamped into the group's r, and what it stands in for
+  // is never used) are read together with the length.
+  const int64_t pg = attn_page(p, b, c0 + 64 * wave);
+  float sm[kAttnR], sl[kAttnR];
+#pragma unroll
+  for (int h = 0; h < kAttnR; ++h) {
+    const int64_t hh = (int64_t)b * p.hq + kh * p.r + (h < p.r ? h : 0);
+    sm[h] = p.stats[hh * 2];
+    sl[h] = p.stats[hh * 2 + 1];
+  }
+  const int n = attn_len(p, b);
+  asm volatile("" ::: "memory");  // the loads above issue before the length is waited for
   if (c0 >= n) return;  // uniform over the workgroup
   const int nv = n - c0 < kAttnChunk ? n - c0 : kAttnChunk;
-  const int r16 = lane & 15, kg = lane >> 4;
-  // V codes first (their loads overlap the probability pass): lane (r16, kg)
+  // For the probability pass (thread t = token c0 + t): the chunk's scores of
+  // every head, loaded before the V codes so that the pass waits for them
+  // only (token clamped into the sequence's length).
+  const int t = threadIdx.x;
+  uint16_t sc[kAttnR];
+  {
+    const int tc = c0 + (t < nv ? t : nv - 1);
+#pragma unroll
+    for (int h = 0; h < kAttnR; ++h) sc[h] = p.s[((int64_t)b * p.hq + kh * p.r + (h < p.r ? h : 0)) * p.cap + tc];
+  }
+  // V codes next (their loads overlap the probability pass): lane (r16, kg)
   // reads channels 8*r16 + [0, 8) of the wave's tokens 32s + 8kg + j (s = 0, 1;
-  // j = 0..7); tokens from nv on and unmapped pages read as 0.
+  // j = 0..7), all in the wave's page (row 0 of the pool for an unmapped one);
+  // tokens from nv on and unmapped pages are zeroed after the loads.
   const int64_t rowbytes = (int64_t)p.kvh * kAttnD;
-  const int64_t base = 64 * wave < nv ? attn_base_row(p, b, c0 + 64 * wave) : -1;
+  const int64_t base = attn_row(p, pg, c0 + 64 * wave);
   const int8_t* vw = p.vc + (base < 0 ? 0 : base) * rowbytes + kh * kAttnD;
   const float* sw = p.vs + ((base < 0 ? 0 : base) + 8 * kg) * p.kvh + kh;
   const uint32_t lane_off = (uint32_t)(8 * kg) * (uint32_t)rowbytes + 8u * r16;
@@ -215,28 +245,26 @@ __global__ void __launch_bounds__(256) attn_pv_kernel(AttnParams p) {
   for (int st = 0; st < 2; ++st)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      wv[st][j] = u32x2{0u, 0u};
-      sv[st][j] = 0.f;
-      if (base >= 0 && 64 * wave + 32 * st + 8 * kg + j < nv) {
-        wv[st][j] = *reinterpret_cast<const u32x2*>(vw + lane_off + (uint32_t)(32 * st + j) * (uint32_t)rowbytes);
-        sv[st][j] = sw[(32 * st + j) * p.kvh];
-      }
+      wv[st][j] = *reinterpret_cast<const u32x2*>(vw + lane_off + (uint32_t)(32 * st + j) * (uint32_t)rowbytes);
+      sv[st][j] = sw[(32 * st + j) * p.kvh];
     }
   // 1. RNE_bf16(prob) of every (head, token) of the chunk, once; heads from r
   //    on are 0 (MFMA columns 8-15 take zero operands below)
-  {
-    const int t = threadIdx.x;
 #pragma unroll
-    for (int h = 0; h < kAttnR; ++h) {
-      float q = 0.f;
-      if (t < nv && h < p.r) {
-        const int64_t hh = (int64_t)b * p.hq + kh * p.r + h;
-        const float m = p.stats[hh * 2], l = p.stats[hh * 2 + 1];
-        q = bf16_round(expf(bf16_to_float(p.s[hh * p.cap + c0 + t]) - m) / l);
-      }
-      pr[h][t] = bf16_bits(q);
-    }
+  for (int h = 0; h < kAttnR; ++h) {
+    float q = 0.f;
+    if (t < nv && h < p.r) q = bf16_round(expf(bf16_to_float(sc[h]) - sm[h]) / sl[h]);
+    pr[h][t] = bf16_bits(q);
   }
+  // the V operands of tokens from nv on, and of an unmapped page, are zero
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool ok = base >= 0 && 64 * wave + 32 * st + 8 * kg + j < nv;
+      wv[st][j] = ok ? wv[st][j] : u32x2{0u, 0u};
+      sv[st][j] = ok ? sv[st][j] : 0.f;
+    }
   __syncthreads();
   // 2. out[h][d] over the wave's 64 tokens as 8 tiles of v_mfma_f32_16x16x32_bf16:
   //    tile T has A[row r][k] = v[token 32s + k][channel 8r + T] (lane (r16, kg)
