@@ -88,6 +88,18 @@ def test_small_layers_match_oracle(device, qtype, tokens, experts, top_k):
     assert_moe_close(got, _oracle(L))
 
 
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("tokens,top_k", [(3, 12), (5, 16), (40, 10)])
+def test_top_k_above_eight_matches_oracle(device, mode, tokens, top_k):
+    # More than 8 routes per token: the decode-step combine sums the rank rows
+    # past the first eight in a second loop, and the routing kernels of every
+    # path take their general (non-register) branches.
+    L = moe_layer(seed=60 + tokens + top_k, experts=20, top_k=top_k, hidden=512, intermediate=256,
+                  tokens=tokens, pack=False)
+    got, _ = _run(L, device, mode=mode)
+    assert_moe_close(got, _oracle(L))
+
+
 def test_decode_workload_full_size(device):
     # 128 experts, top-8, hidden 2048, intermediate 768, Q6_K, 8 tokens, seed 1.
     L = moe_layer(seed=1, pack=False)
