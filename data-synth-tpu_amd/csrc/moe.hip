@@ -1072,6 +1072,26 @@ extern "C" int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, in
   return check_launch("moe_pack_kernel");
 }
 
+// e[i] = exp(-|x[i]|) and s[i] = sigmoid_acc(x[i]) for BF16 x: the values the
+// SwiGLU epilogues and the shared-expert gate compute.
+__global__ void __launch_bounds__(256) sigmoid_probe_kernel(const uint16_t* __restrict__ x, int64_t n,
+                                                            float* __restrict__ e, float* __restrict__ s) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float v = bf16_to_float(x[i]);
+  e[i] = expf(-fabsf(v));
+  s[i] = sigmoid_acc(v);
+}
+
+extern "C" int q6moe_sigmoid_probe(const uint16_t* x, int64_t n, float* e, float* s, void* stream) {
+  Q6MOE_REQUIRE(x && e && s, "sigmoid_probe: null pointer");
+  Q6MOE_REQUIRE(n >= 1 && n <= (int64_t)1 << 30, "sigmoid_probe: n must be in [1, 2^30]");
+  Q6MOE_REQUIRE(aligned(x, 2) && aligned(e, 4) && aligned(s, 4), "sigmoid_probe: misaligned pointer");
+  hipLaunchKernelGGL(sigmoid_probe_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, (hipStream_t)stream, x, n,
+                     e, s);
+  return check_launch("sigmoid_probe_kernel");
+}
+
 extern "C" int q6moe_moe_unpack(const uint8_t* table, int qtype, int64_t experts, int64_t rows, int64_t width,
                                 int64_t stride, int path, uint16_t* out, void* stream) {
   Q6MOE_REQUIRE(table && out, "moe_unpack: null pointer");

@@ -180,11 +180,22 @@ __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
 }
 
 // Accurate FP32 sigmoid: where(x >= 0, 1, e) / (1 + e), e = exp(-|x|)
-// (kaggle/qwen38_tpu/numerics.py:42-45), IEEE division.
+// (kaggle/qwen38_tpu/numerics.py:42-45), with the correctly rounded quotient.
+// The divisor d = 1 + e lies in (1, 2] and the numerator in [0, 1], so the
+// quotient is formed by the FMA method of Markstein (IBM J. Res. Dev. 34,
+// 1990): the hardware reciprocal refined by one Newton step, the product,
+// and one correction by the exact FMA residual, without the scaling steps a
+// general division needs for extreme exponents. For every BF16 input (the
+// only inputs its callers pass) it equals the IEEE quotient of the same e;
+// the sigmoid probe's test checks all of them.
 __device__ __forceinline__ float sigmoid_acc(float x) {
-  float e = expf(-fabsf(x));
-  float num = x >= 0.f ? 1.f : e;
-  return num / (1.f + e);
+  const float e = expf(-fabsf(x));
+  const float num = x >= 0.f ? 1.f : e;
+  const float d = 1.f + e;
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float r1 = __builtin_fmaf(__builtin_fmaf(-d, r, 1.f), r, r);
+  const float q = num * r1;
+  return __builtin_fmaf(__builtin_fmaf(-d, q, num), r1, q);
 }
 
 // ---------------------------------------------------------------------------

@@ -145,6 +145,7 @@ SIGNATURES = {
     "q6moe_moe_table_bytes": (_size, [_int, _i64, _i64]),
     "q6moe_moe_pack": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp]),
     "q6moe_moe_unpack": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _int, _vp, _vp]),
+    "q6moe_sigmoid_probe": (_int, [_vp, _i64, _vp, _vp, _vp]),
     "q6moe_moe_workspace_size": (_size, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "q6moe_moe_forward": (_int, [ctypes.POINTER(MoeArgs), _vp]),
     "q6moe_moe_forward_noalloc": (_int, [ctypes.POINTER(MoeArgs), _vp]),

@@ -144,6 +144,15 @@ int q6moe_moe_pack(const uint8_t* raw, int qtype, int64_t experts, int64_t rows,
 int q6moe_moe_unpack(const uint8_t* table, int qtype, int64_t experts, int64_t rows, int64_t width,
                      int64_t stride, int path, uint16_t* out, void* stream);
 
+/*
+ * Sigmoid probe: for n BF16 inputs x, e[i] = exp(-|x[i]|) and s[i] = the FP32
+ * sigmoid that the routed FFN's SwiGLU and the shared-expert gate compute,
+ * where(x >= 0, 1, e) / (1 + e) (kaggle/qwen38_tpu/numerics.py:42-45), on the
+ * given stream. No counterpart call in the reference: it is for tests of that
+ * formula (the quotient is the correctly rounded one of the same e).
+ */
+int q6moe_sigmoid_probe(const uint16_t* x, int64_t n, float* e, float* s, void* stream);
+
 /* Weight tables of one projection for all experts. */
 typedef struct q6moe_table {
   int qtype;                /* gate/up: Q6MOE_Q6_K, _Q5_K, _Q4_K or _Q8_0; down: those or Q6MOE_Q5_1 */
