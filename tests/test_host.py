@@ -136,6 +136,10 @@ def test_library_rejects_bad_arguments_without_a_device():
     assert b"null" in lib.q6moe_last_error()
     rc = lib.q6moe_gguf_decode(ctypes.c_void_p(16), 99, 1, 32, ctypes.c_void_p(16), 0, None)
     assert rc == -3
+    rc = lib.q6moe_sigmoid_probe(None, 4, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert rc == -1 and b"null" in lib.q6moe_last_error()
+    rc = lib.q6moe_sigmoid_probe(ctypes.c_void_p(16), 0, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert rc == -1 and b"n must be" in lib.q6moe_last_error()
 
 
 def test_decode_mode_rejects_token_rows_past_32_bit_offsets_without_a_device():
