@@ -610,6 +610,107 @@ def measure_q8_down(dev):
             "active_experts": active, "bytes_per_step": nbytes, "layer_copies": copies}
 
 
+WIDE_E, WIDE_K, WIDE_H, WIDE_I, WIDE_SEED, WIDE_TOKENS = 512, 10, 2560, 640, 5, 2048
+WIDE_GATE_BYTES = WIDE_I * (WIDE_H // 256) * 210   # Q6_K gate (or up) of one expert
+WIDE_DOWN_BYTES = WIDE_H * (WIDE_I // 32) * 34     # Q8_0 down of one expert
+
+
+def measure_wide_layer(dev, with_cpu):
+    """The reference model's MoE layer (kaggle/qwen38_tpu/config.py:13-19: 512
+    experts, top-10, hidden 2560, intermediate 640) in its Q6 checkpoint's formats
+    (checkpoints/q6.json: Q6_K gate/up, Q8_0 down), weights N(0, 0.02) per expert,
+    seed 5: decode steps of 1, 8 and 64 tokens (the first rows of the 2048-token
+    layer) and the 2048-token prefill step. Layer copies rotate so that one
+    rotation's active bytes exceed 3x the Infinity Cache."""
+    import numpy as np
+    import torch
+
+    from q6moe.experts import expert_parallel
+    from q6moe.synth import wide_moe_layer
+
+    L = wide_moe_layer(seed=WIDE_SEED, tokens=WIDE_TOKENS)
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q8_0", hidden=WIDE_H,
+                         intermediate=WIDE_I)
+    base = list(fn.prepare(L["gate"].reshape(WIDE_E, -1), L["up"].reshape(WIDE_E, -1),
+                           L["down"].reshape(WIDE_E, -1), dev))
+    per_expert = 2 * WIDE_GATE_BYTES + WIDE_DOWN_BYTES
+    types = ("Q6_K", "Q6_K", "Q8_0")
+    xa = torch.from_numpy(L["x"]).to(dev).to(torch.bfloat16)
+    ida = torch.from_numpy(L["ids"]).to(dev)
+    wa = torch.from_numpy(L["weights"]).to(dev).to(torch.bfloat16)
+    out = {"workload": "moe_q6k_gateup_q8_0_down_e512_top10_h2560_i640_seed5", "decode": {}}
+    layers = [base]
+    for b in (1, 8, 64):
+        active = len(np.unique(L["ids"][:b]))
+        routes = int(np.count_nonzero(L["weights"][:b]))
+        nbytes = active * per_expert + 2 * b * WIDE_H * 2 + b * WIDE_K * 6
+        copies = copies_for(nbytes, hi=4)
+        while len(layers) < copies:
+            layers.append(clone_tables(base))
+        x, ids, w = xa[:b].contiguous(), ida[:b].contiguous(), wa[:b].contiguous()
+        f = fn.with_mode(1)
+        ws = torch.empty(f.workspace_bytes(b, WIDE_K, WIDE_E), dtype=torch.uint8, device=dev)
+        o = torch.empty((b, WIDE_H), dtype=torch.bfloat16, device=dev)
+
+        def call(i, events=None):
+            f(*layers[i % copies], x, ids, w, workspace=ws, out=o, events=events)
+
+        call(0)
+        got = o.float().cpu().numpy()
+        row = {}
+        if not np.isfinite(got).all():
+            raise CheckFailed(f"wide layer B={b}: nonfinite output rejected before timing")
+        if with_cpu:
+            want, secs, n, runs = cpu_oracle_moe(L, slice(0, b), types, WIDE_H, WIDE_I, min_seconds=3.0)
+            row["check"] = check_close(f"wide layer B={b}", got, want)
+            row["cpu_baseline"] = {"value": round(nbytes / secs / 1e9, 4), "unit": "GB/s", "cores": n,
+                                   "kind": "port", "tokens_per_s": round(b / secs, 2),
+                                   "sample": f"the whole {b}-token step by the NumPy oracle, median of {runs} "
+                                             f"runs: {secs:.2f} s"}
+        t = timed_reps({"fused": call}, inner=20)
+        us = t["fused"]["median"]
+        ph = phase_means(call, 50)
+        gu_bytes = active * 2 * WIDE_GATE_BYTES + b * WIDE_H * 2 + routes * WIDE_I * 2
+        row.update({"us_per_step": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                    "tokens_per_s": round(b / (us * 1e-6), 1),
+                    "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "step_us": t["fused"],
+                    "phases_us": {k: round(float(v), 2) for k, v in zip(("pre", "gate_up", "down", "combine"), ph)},
+                    "active_experts": active, "bytes_per_step": nbytes, "layer_copies": copies,
+                    "roofline": roofline("q6moe::moe_dec_gate_up_kernel<0, false>", "hbm", gu_bytes, ph[1],
+                                         work_unit="bytes_per_launch", tag=f"wide {b} token")})
+        out["decode"][str(b)] = row
+    del layers[1:]
+    # prefill: all 2048 tokens on the grouped kernels
+    B = WIDE_TOKENS
+    flops = 2 * B * WIDE_K * 3 * WIDE_H * WIDE_I
+    ws = torch.empty(fn.workspace_bytes(B, WIDE_K, WIDE_E), dtype=torch.uint8, device=dev)
+    o = torch.empty((B, WIDE_H), dtype=torch.bfloat16, device=dev)
+    fn(*base, xa, ida, wa, workspace=ws, out=o)
+    got = o.float().cpu().numpy()
+    pf = {}
+    if not np.isfinite(got).all():
+        raise CheckFailed("wide layer prefill: nonfinite output rejected before timing")
+    if with_cpu:
+        rows = np.sort(np.random.default_rng(11).choice(B, 128, replace=False))
+        want, secs, n, runs = cpu_oracle_moe(L, rows, types, WIDE_H, WIDE_I, min_seconds=5.0)
+        pf["check"] = dict(check_close("wide layer prefill", got[rows], want), sample_tokens=int(rows.size))
+        sflops = 2 * rows.size * WIDE_K * 3 * WIDE_H * WIDE_I
+        pf["cpu_baseline"] = {"value": round(sflops / secs / 1e12, 6), "unit": "TFLOP/s", "cores": n,
+                              "kind": "port", "tokens_per_s": round(rows.size / secs, 1),
+                              "sample": f"128 of the {B} tokens (all their routes) by the NumPy oracle, median "
+                                        f"of {runs} runs: {secs:.2f} s"}
+    t = timed_reps({"fused": lambda i: fn(*base, xa, ida, wa, workspace=ws, out=o)}, inner=10)
+    us = t["fused"]["median"]
+    ph = phase_means(lambda i, ev: fn(*base, xa, ida, wa, workspace=ws, out=o, events=ev), 10)
+    tflops = flops / (us * 1e-6) / 1e12
+    pf.update({"tokens": B, "us_per_step": round(us, 1), "value": round(tflops, 1), "unit": "TFLOP/s",
+               "mfma_fraction": round(tflops / MFMA_PEAK_TFLOPS, 4), "flops_per_step": flops,
+               "tokens_per_s": round(B / (us * 1e-6), 1), "step_us": t["fused"],
+               "phases_us": {k: round(float(v), 1) for k, v in zip(("route", "gate_up", "down", "combine"), ph)}})
+    out["prefill"] = pf
+    return out
+
+
 def measure_kv(dev, with_cpu):
     """Paged INT8 KV gather + dequant of every cached token (batch 8, 4 KV heads x 128,
     32768 tokens per sequence in pages of 256, FP32 per-token-per-head scales, seed 4):
@@ -917,6 +1018,8 @@ def run(args):
         log("timing the Q6_K gate/up + Q8_0 down step ...")
         result["extras"] = {"q8_0_down": measure_q8_down(dev), "kv_attention": kv_attention,
                             "hbm_copy": copy_ceiling(dev)}
+        log("timing the 512-expert layer of the reference model (seed 5) ...")
+        configs["wide_layer"] = measure_wide_layer(dev, with_cpu)
     if "prefill" in configs:
         result["prefill"] = configs["prefill"]
     result["configs"] = configs

@@ -23,9 +23,9 @@
 
 namespace q6moe {
 
-constexpr int kRouteMaxExperts = 256;
 constexpr int kChunk = 256;  // tokens per routing workgroup
 constexpr int kChunkWords = kChunk / 32;
+constexpr int kExpertsPerLane = kMaxExperts / kChunk;  // experts per lane of a routing workgroup
 
 __device__ __forceinline__ bool is_route(float r) { return r != 0.f || r != r; }
 
@@ -67,7 +67,7 @@ __global__ void __launch_bounds__(kChunk)
   extern __shared__ int sm[];
   int* s_ids = sm;                                            // [kChunk * K]
   float* s_w = reinterpret_cast<float*>(sm + kChunk * K);     // [kChunk * K] weights, then merged weights
-  __shared__ int cnt[kRouteMaxExperts];
+  __shared__ int cnt[kMaxExperts];
   const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
   const int nb = B - b0 < kChunk ? B - b0 : kChunk;
   const int64_t e0 = (int64_t)b0 * K;
@@ -127,15 +127,16 @@ __global__ void __launch_bounds__(kChunk)
   for (int e = tid; e < E; e += kChunk) chunk_cnt[(int64_t)blockIdx.x * E + e] = cnt[e];
 }
 
-// Routing, pass 2 (one workgroup, one lane per expert): active experts in
-// ascending id (experts.py:74-76), each expert's first route position, the
-// 128-route prefill tiles, each chunk's first position per expert relative to
-// the expert's first (chunk_cnt is rewritten in place) and, in row nchunks of
-// chunk_cnt, each expert's first position.
-__global__ void __launch_bounds__(kRouteMaxExperts)
+// Routing, pass 2 (one workgroup of E lanes rounded up to whole waves, one
+// lane per expert): active experts in ascending id (experts.py:74-76), each
+// expert's first route position, the 128-route prefill tiles, each chunk's
+// first position per expert relative to the expert's first (chunk_cnt is
+// rewritten in place) and, in row nchunks of chunk_cnt, each expert's first
+// position.
+__global__ void __launch_bounds__(kMaxExperts)
     moe_route_scan_kernel(int E, int nchunks, int mtile, MoeWs ws, int* __restrict__ chunk_cnt) {
-  __shared__ int s_a[kRouteMaxExperts], s_c[kRouteMaxExperts], s_t[kRouteMaxExperts];
-  const int e = threadIdx.x;
+  __shared__ int s_wt[3][kMaxExperts / 64];  // per-wave totals of the three scans
+  const int e = threadIdx.x, lane = e & 63, wv = e >> 6;
   int total = 0;
   if (e < E) {
     for (int c0 = 0; c0 < nchunks; c0 += 8) {
@@ -154,20 +155,30 @@ __global__ void __launch_bounds__(kRouteMaxExperts)
     }
   }
   const int act = total > 0, nt = (total + mtile - 1) / mtile;
-  s_a[e] = act;
-  s_c[e] = total;
-  s_t[e] = nt;
-  __syncthreads();
-  // inclusive Hillis-Steele scans over the 256 lanes
-  for (int off = 1; off < kRouteMaxExperts; off <<= 1) {
-    const int va = e >= off ? s_a[e - off] : 0, vc = e >= off ? s_c[e - off] : 0, vt = e >= off ? s_t[e - off] : 0;
-    __syncthreads();
-    s_a[e] += va;
-    s_c[e] += vc;
-    s_t[e] += vt;
-    __syncthreads();
+  // inclusive scans of (active, routes, tiles) in expert order: within each
+  // wave by shuffles, then plus the totals of the earlier waves
+  int ia = act, ic = total, it = nt;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int ta = __shfl_up(ia, off), tc = __shfl_up(ic, off), tt = __shfl_up(it, off);
+    if (lane >= off) {
+      ia += ta;
+      ic += tc;
+      it += tt;
+    }
   }
-  const int slot = s_a[e] - act, base = s_c[e] - total, t0 = s_t[e] - nt;
+  if (lane == 63) {
+    s_wt[0][wv] = ia;
+    s_wt[1][wv] = ic;
+    s_wt[2][wv] = it;
+  }
+  __syncthreads();
+  for (int w = 0; w < wv; ++w) {
+    ia += s_wt[0][w];
+    ic += s_wt[1][w];
+    it += s_wt[2][w];
+  }
+  const int slot = ia - act, base = ic - total, t0 = it - nt;
   if (e < E) {
     chunk_cnt[(int64_t)nchunks * E + e] = base;
     if (act) {
@@ -179,12 +190,11 @@ __global__ void __launch_bounds__(kRouteMaxExperts)
       }
     }
   }
-  if (e == kRouteMaxExperts - 1) {
-    const int na = s_a[e];
-    ws.act_off[na] = s_c[e];
-    ws.hdr[0] = na;
-    ws.hdr[1] = s_c[e];
-    ws.hdr[2] = s_t[e];
+  if (e == (int)blockDim.x - 1) {  // lanes past E add nothing: the last one holds the totals
+    ws.act_off[ia] = ic;
+    ws.hdr[0] = ia;
+    ws.hdr[1] = ic;
+    ws.hdr[2] = it;
   }
 }
 
@@ -200,23 +210,34 @@ __global__ void __launch_bounds__(kChunk)
   int* s_ids = sm;                                          // [kChunk * K]
   float* s_r = reinterpret_cast<float*>(sm + kChunk * K);   // [kChunk * K]
   int* s_tp = sm + 2 * kChunk * K;                          // [kChunk * K]
-  __shared__ uint32_t bits[kRouteMaxExperts][kChunkWords];
-  __shared__ int s_pos[kRouteMaxExperts];
+  uint32_t* bits = reinterpret_cast<uint32_t*>(sm + 3 * kChunk * K);  // [E][kChunkWords] token bitmaps
+  int* s_pos = sm + 3 * kChunk * K + E * kChunkWords;       // [E]
   const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
   const int nb = B - b0 < kChunk ? B - b0 : kChunk;
   const int64_t e0 = (int64_t)b0 * K;
-  for (int i = tid; i < E * kChunkWords; i += kChunk) bits[i / kChunkWords][i % kChunkWords] = 0u;
-  // one expert per lane (E <= kChunk): its first position and this chunk's
-  // offset within it, loaded together with the chunk's entries
-  static_assert(kRouteMaxExperts <= kChunk, "one lane per expert");
-  const int ec = tid < E ? tid : E - 1;
-  const int pe0 = chunk_pos[(int64_t)nchunks * E + ec], pe1 = chunk_pos[(int64_t)blockIdx.x * E + ec];
+  for (int i = tid; i < E * kChunkWords; i += kChunk) bits[i] = 0u;
+  // experts tid + kChunk * q: their first positions and this chunk's offsets
+  // within them, loaded together with the chunk's entries (indexes past E
+  // repeat expert E - 1; the loads past the first kChunk experts are skipped
+  // for smaller layers)
+  int pe[kExpertsPerLane];
+#pragma unroll
+  for (int q = 0; q < kExpertsPerLane; ++q) {
+    pe[q] = 0;
+    if (q == 0 || q * kChunk < E) {
+      const int ec = tid + q * kChunk < E ? tid + q * kChunk : E - 1;
+      pe[q] = chunk_pos[(int64_t)nchunks * E + ec] + chunk_pos[(int64_t)blockIdx.x * E + ec];
+    }
+  }
   stage_chunk2(s_ids, ids + e0, [](int v) { return v; }, s_r, ws.ent_r + e0, [](float v) { return v; }, nb * K);
-  if (tid < E) s_pos[tid] = pe0 + pe1;
+#pragma unroll
+  for (int q = 0; q < kExpertsPerLane; ++q)
+    if (tid + q * kChunk < E) s_pos[tid + q * kChunk] = pe[q];
   __syncthreads();
   if (tid < nb)
     for (int kk = 0; kk < K; ++kk)
-      if (is_route(s_r[tid * K + kk])) atomicOr(&bits[s_ids[tid * K + kk]][tid >> 5], 1u << (tid & 31));
+      if (is_route(s_r[tid * K + kk]))
+        atomicOr(&bits[s_ids[tid * K + kk] * kChunkWords + (tid >> 5)], 1u << (tid & 31));
   __syncthreads();
   if (tid < nb && K <= 8) {
     // top_k <= 8: the token's entries and its position list in registers; the
@@ -228,10 +249,10 @@ __global__ void __launch_bounds__(kChunk)
       const float r = kk < K ? s_r[tid * K + kk] : 0.f;
       if (kk < K && is_route(r)) {
         const int e = s_ids[tid * K + kk];
-        int rank = __popc(bits[e][tid >> 5] & ((1u << (tid & 31)) - 1u));
+        int rank = __popc(bits[e * kChunkWords + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
 #pragma unroll
         for (int w = 0; w < kChunkWords - 1; ++w)
-          if (w < (tid >> 5)) rank += __popc(bits[e][w]);
+          if (w < (tid >> 5)) rank += __popc(bits[e * kChunkWords + w]);
         const int p = s_pos[e] + rank;
         ws.route_tok[p] = b0 + tid;
         ws.route_w[p] = r;
@@ -258,8 +279,8 @@ __global__ void __launch_bounds__(kChunk)
       const float r = s_r[tid * K + kk];
       if (is_route(r)) {
         const int e = s_ids[tid * K + kk];
-        int rank = __popc(bits[e][tid >> 5] & ((1u << (tid & 31)) - 1u));
-        for (int w = 0; w < (tid >> 5); ++w) rank += __popc(bits[e][w]);
+        int rank = __popc(bits[e * kChunkWords + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
+        for (int w = 0; w < (tid >> 5); ++w) rank += __popc(bits[e * kChunkWords + w]);
         const int pos = s_pos[e] + rank;
         ws.route_tok[pos] = b0 + tid;
         ws.route_w[pos] = r;
@@ -1191,7 +1212,7 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   Q6MOE_REQUIRE(a->x && a->ids && a->weights && a->out && workspace, "moe_forward: null pointer");
   const int64_t B = a->tokens, K = a->top_k, E = a->experts, H = a->hidden, I = a->intermediate;
   Q6MOE_REQUIRE(B >= 1 && K >= 1 && E >= 1 && H >= 1 && I >= 1, "moe_forward: sizes must be positive");
-  Q6MOE_REQUIRE(E <= kRouteMaxExperts, "moe_forward: at most 256 experts per call");
+  Q6MOE_REQUIRE(E <= kMaxExperts, "moe_forward: at most 1024 experts per call");
   Q6MOE_REQUIRE(K <= 32, "moe_forward: top_k must be at most 32");
   Q6MOE_REQUIRE(B * K <= (1 << 28) && H <= (1 << 24) && I <= (1 << 24), "moe_forward: problem too large");
   Q6MOE_REQUIRE(H % 8 == 0 && I % 8 == 0, "moe_forward: hidden and intermediate must be multiples of 8");
@@ -1222,7 +1243,7 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   Q6MOE_REQUIRE(!(w8 && a->mode == 1), "moe_forward: the int8_q8 policy runs on the grouped kernels (mode 0 or 2)");
   const int64_t width = std::max(H, std::max(I, Is));
   if (a->mode == 1 && !dec_supported(B, K, E, width)) {
-    set_error("moe_forward: decode mode needs tokens <= 256, tokens*top_k <= 1024, experts <= 256 and "
+    set_error("moe_forward: decode mode needs tokens <= 256, tokens*top_k <= 1024, experts <= 1024 and "
               "tokens*top_k*max(hidden, intermediate, shared_intermediate) < 2^30");
     return Q6MOE_ERR_INVALID;
   }
@@ -1332,19 +1353,22 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   mark(0);
   {
     static std::atomic<uint64_t> attr_done{0};
-    once_per_device(attr_done, [] {  // top_k <= 32: at most 64 KB and 96 KB of staged rows
+    // top_k <= 32, experts <= kMaxExperts: at most 64 KB of staged rows for
+    // the count, 132 KB of staged rows, bitmaps and positions for the scatter
+    const auto scatter_lds = [](int64_t k, int64_t e) { return (size_t)(3 * kChunk * k + e * (kChunkWords + 1)) * 4; };
+    once_per_device(attr_done, [&] {
       (void)hipFuncSetAttribute((const void*)moe_route_count_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 kChunk * 32 * 8);
       (void)hipFuncSetAttribute((const void*)moe_route_scatter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                kChunk * 32 * 12);
+                                (int)scatter_lds(32, kMaxExperts));
     });
     const int nchunks = (int)cdiv(B, kChunk);
     int* chunk_cnt = reinterpret_cast<int*>(w + L.chunk_cnt);
     hipLaunchKernelGGL(moe_route_count_kernel, dim3(nchunks), dim3(kChunk), (size_t)kChunk * K * 8, s, a->ids,
                        a->weights, (int)B, (int)K, (int)E, ws, chunk_cnt);
-    hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3(kRouteMaxExperts), 0, s, (int)E, nchunks,
+    hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3((unsigned)cdiv(E, 64) * 64), 0, s, (int)E, nchunks,
                        (int)kPrefillTile, ws, chunk_cnt);
-    hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nchunks), dim3(kChunk), (size_t)kChunk * K * 12, s, a->ids,
+    hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nchunks), dim3(kChunk), scatter_lds(K, E), s, a->ids,
                        (int)B, (int)K, (int)E, nchunks, ws, chunk_cnt);
     if ((rc = check_launch("moe routing kernels"))) return rc;
   }

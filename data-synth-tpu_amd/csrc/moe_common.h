@@ -9,6 +9,11 @@ namespace q6moe {
 
 enum { FMT_Q6 = 0, FMT_Q4K = 1, FMT_Q8 = 2, FMT_Q5K = 3, FMT_Q51 = 4 };
 
+// Experts of one layer (one call) that the routing of every path handles:
+// the decode kernels' expert bit mask and counts, the grouped routing's
+// per-expert counts, bitmaps and scans, and the device router.
+constexpr int kMaxExperts = 1024;
+
 // Expert tables of the routed-expert kernels are unit-major: a unit is 16
 // output rows x one 256-wide K block, stored exactly as a wave stages it in
 // LDS, and an expert's units are ordered [row group][K block] so that a wave

@@ -38,7 +38,7 @@ namespace q6moe {
 
 constexpr int kDecMaxEntries = 1024;  // tokens * top_k handled by the decode path
 constexpr int kDecMaxTokens = 256;    // tokens handled by the decode path
-constexpr int kDecMaxExperts = 256;
+constexpr int kMaskWords = kMaxExperts / 32;  // expert bit mask of the small-batch routing
 constexpr int kStages = 3;
 constexpr int kDownRows = 4;  // 16-row groups of down per wave
 constexpr int kPassTokens = 16;  // routes per weight pass (MFMA columns)
@@ -55,16 +55,17 @@ constexpr int ring_bytes() { return kStages * stage_bytes<FMT>(); }
 constexpr int kXLoads = 8;   // token-operand loads per K block (one per MFMA)
 
 // Per-wave LDS of the gate/up kernel: the weight ring, which the routing
-// scratch overlays before the ring fills (for more than 64 entries: ids,
-// merged weights and per-expert counts, 8 bytes per entry plus 4 per
-// expert), then the slot's token list. Sized per launch, so that a layer with
-// small units and few routes keeps more waves per CU.
-__host__ __device__ constexpr int route_scratch_bytes(int n) {
-  return n > 64 ? 8 * ((n + 3) & ~3) + 4 * kDecMaxExperts : 64;
+// scratch overlays before the ring fills (for up to 64 entries the expert bit
+// mask; for more: ids, merged weights and per-expert counts, 8 bytes per
+// entry plus 4 per expert rounded up to 256 experts), then the slot's token
+// list. Sized per launch, so that a layer with small units and few routes
+// keeps more waves per CU.
+__host__ __device__ constexpr int route_scratch_bytes(int n, int experts) {
+  return n > 64 ? 8 * ((n + 3) & ~3) + 4 * ((experts + 255) & ~255) : 4 * kMaskWords;
 }
 template <int FMT>
-__host__ __device__ constexpr int gu_wave_lds(int n) {
-  const int r = ring_bytes<FMT>(), sc = route_scratch_bytes(n);
+__host__ __device__ constexpr int gu_wave_lds(int n, int experts) {
+  const int r = ring_bytes<FMT>(), sc = route_scratch_bytes(n, experts);
   return (((r > sc ? r : sc) + 255) & ~255) + 4 * kDecMaxTokens;
 }
 
@@ -402,7 +403,10 @@ __device__ bool dec_route_small(const DecRoute& R, int slot, bool publish, const
   const int lane = threadIdx.x & 63;
   const int n = R.B * R.K;
   uint32_t* s_mask = reinterpret_cast<uint32_t*>(scratch);  // one bit per expert
-  if (lane < kDecMaxExperts / 32) s_mask[lane] = 0u;
+  // Up to 256 experts the mask is 8 words, read as two 16-byte words; a wider
+  // layer's further words are read in one more batch.
+  const bool wide = R.E > 256;
+  if (lane < (wide ? kMaskWords : 8)) s_mask[lane] = 0u;
   int id = -1;
   float rw = 0.f;
   if (lane < n) {
@@ -436,9 +440,8 @@ __device__ bool dec_route_small(const DecRoute& R, int slot, bool publish, const
   r = r != 0.f ? r : 0.f;
   const bool live = r != 0.f;
   if (live) atomicOr(&s_mask[id >> 5], 1u << (id & 31));
-  static_assert(kDecMaxExperts == 256, "mask read as two 16-byte words");
   const u32x4 mA = *reinterpret_cast<const u32x4*>(s_mask), mB = *reinterpret_cast<const u32x4*>(s_mask + 4);
-  uint32_t m[kDecMaxExperts / 32];
+  uint32_t m[kMaskWords];
   int total = 0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -446,7 +449,20 @@ __device__ bool dec_route_small(const DecRoute& R, int slot, bool publish, const
     m[q + 4] = __builtin_amdgcn_readfirstlane(mB[q]);
   }
 #pragma unroll
-  for (int q = 0; q < kDecMaxExperts / 32; ++q) total += __builtin_popcount(m[q]);
+  for (int q = 8; q < kMaskWords; ++q) m[q] = 0u;
+  if (wide) {
+    u32x4 mw[kMaskWords / 4 - 2];
+#pragma unroll
+    for (int c = 0; c < kMaskWords / 4 - 2; ++c) mw[c] = *reinterpret_cast<const u32x4*>(s_mask + 8 + 4 * c);
+#pragma unroll
+    for (int c = 0; c < kMaskWords / 4 - 2; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) m[8 + 4 * c + q] = __builtin_amdgcn_readfirstlane(mw[c][q]);
+#pragma unroll
+    for (int q = 8; q < kMaskWords; ++q) total += __builtin_popcount(m[q]);
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q) total += __builtin_popcount(m[q]);
   const uint64_t lm = __ballot(live);
   if (publish && slot == 0) {
     if (lane == 0) {
@@ -459,8 +475,7 @@ __device__ bool dec_route_small(const DecRoute& R, int slot, bool publish, const
   if (alive) {
     // the slot's expert: the slot-th set bit of the mask (ascending id)
     int e = 0, rem = slot;
-#pragma unroll
-    for (int q = 0; q < kDecMaxExperts / 32; ++q) {
+    const auto find = [&](auto q) {
       const int c = __builtin_popcount(m[q]);
       if (rem >= 0 && rem < c) {
         uint32_t w = m[q];
@@ -468,7 +483,9 @@ __device__ bool dec_route_small(const DecRoute& R, int slot, bool publish, const
         e = 32 * q + __builtin_ctz(w);
       }
       rem -= c;
-    }
+    };
+    static_for<0, 8>(find);
+    if (wide && rem >= 0) static_for<8, kMaskWords>(find);
     const uint64_t below = __ballot(live && id < e);
     const uint64_t mine = __ballot(live && id == e);
     const int t0 = __popcll(below), cnt = __popcll(mine);
@@ -503,8 +520,8 @@ __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTa
   const int n4 = (n + 3) & ~3;  // route_scratch_bytes(n) bytes: ids, weights, counts
   float* s_r = reinterpret_cast<float*>(scratch + 4 * n4);
   int* s_cnt = reinterpret_cast<int*>(scratch + 8 * n4);
-#pragma unroll
-  for (int q = 0; q < kDecMaxExperts / 64; ++q) s_cnt[q * 64 + lane] = 0;
+  const int e256 = (R.E + 255) & ~255;  // counts zeroed in whole chunks of 256 experts
+  for (int i = lane; i < e256; i += 64) s_cnt[i] = 0;
   for (int i = lane; i < n; i += 64) {
     s_ids[i] = R.ids[i];
     s_r[i] = bf16_to_float(R.wts[i]);
@@ -537,45 +554,50 @@ __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTa
     }
     __syncthreads();
   }
-  // exclusive scans over experts (4 per lane) of active flags and counts
-  int act[4], cnt[4], la = 0, lc = 0;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    cnt[q] = s_cnt[lane * 4 + q];
-    act[q] = cnt[q] > 0;
-    la += act[q];
-    lc += cnt[q];
-  }
-  int ia = la, ic = lc;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int ta = __shfl_up(ia, off), tc = __shfl_up(ic, off);
-    if (lane >= off) {
-      ia += ta;
-      ic += tc;
-    }
-  }
-  const int total = __builtin_amdgcn_readfirstlane(__shfl(ia, 63));
-  const int routes = __builtin_amdgcn_readfirstlane(__shfl(ic, 63));
+  // exclusive scans over experts of active flags and counts, in chunks of
+  // 256 experts (4 per lane), each chunk starting from the earlier chunks' totals
   const bool tables = publish && slot == 0;
-  int ea = ia - la, ec = ic - lc;
+  int total = 0, routes = 0;
   int my_e = -1, my_t0 = 0, my_c = 0;
+  for (int c0 = 0; c0 < R.E; c0 += 256) {
+    int act[4], cnt[4], la = 0, lc = 0;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    if (act[q]) {
-      if (ea == slot) {
-        my_e = lane * 4 + q;
-        my_t0 = ec;
-        my_c = cnt[q];
-      }
-      if (tables) {
-        T.slot_e[ea] = lane * 4 + q;
-        T.slot_t0[ea] = ec;
-        T.slot_cnt[ea] = cnt[q];
+    for (int q = 0; q < 4; ++q) {
+      cnt[q] = s_cnt[c0 + lane * 4 + q];
+      act[q] = cnt[q] > 0;
+      la += act[q];
+      lc += cnt[q];
+    }
+    int ia = la, ic = lc;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int ta = __shfl_up(ia, off), tc = __shfl_up(ic, off);
+      if (lane >= off) {
+        ia += ta;
+        ic += tc;
       }
     }
-    ea += act[q];
-    ec += cnt[q];
+    int ea = total + ia - la, ec = routes + ic - lc;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (act[q]) {
+        const int e = c0 + lane * 4 + q;
+        if (ea == slot) {
+          my_e = e;
+          my_t0 = ec;
+          my_c = cnt[q];
+        }
+        if (tables) {
+          T.slot_e[ea] = e;
+          T.slot_t0[ea] = ec;
+          T.slot_cnt[ea] = cnt[q];
+        }
+      }
+      ea += act[q];
+      ec += cnt[q];
+    }
+    total += __builtin_amdgcn_readfirstlane(__shfl(ia, 63));
+    routes += __builtin_amdgcn_readfirstlane(__shfl(ic, 63));
   }
   if (tables) {
     if (lane == 0) {
@@ -701,7 +723,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
                            int hidden, uint16_t* __restrict__ act, int inter, DecShared sh) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int wave = split_wave();
-  const int wl = gu_wave_lds<FMT>(R.B * R.K);
+  const int wl = gu_wave_lds<FMT>(R.B * R.K, R.E);
   uint8_t* ring = smem + wave * wl;
   int* tok = reinterpret_cast<int*>(ring + wl - 4 * kDecMaxTokens);
   const int sh_groups = (sh.is + 15) / 16, passes = (R.B + kPassTokens - 1) / kPassTokens;
@@ -906,12 +928,13 @@ template <int FG, int FD, bool kFullK>
 static int launch(const DecArgs& A, hipStream_t s) {
   const int groups_i = (int)cdiv(A.I, 16), groups_h = (int)cdiv(A.H, 16);
   // per-wave LDS: the gate/up ring sized for this launch's routing entries
-  const int lds_gu = gu_wave_lds<FG>((int)(A.R.B * A.R.K));
+  const int lds_gu = gu_wave_lds<FG>((int)(A.R.B * A.R.K), A.R.E);
   constexpr int lds_dn = ring_bytes<FD>();
   static std::atomic<uint64_t> attr_done{0};
   once_per_device(attr_done, [] {  // the most any launch asks for
     (void)hipFuncSetAttribute((const void*)moe_dec_gate_up_kernel<FG, kFullK>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 4 * gu_wave_lds<FG>(kDecMaxEntries));
+                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                              4 * gu_wave_lds<FG>(kDecMaxEntries, kMaxExperts));
     (void)hipFuncSetAttribute((const void*)moe_dec_down_kernel<FD, kFullK>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, 4 * ring_bytes<FD>());
   });
@@ -946,7 +969,7 @@ static int launch(const DecArgs& A, hipStream_t s) {
 
 bool dec_supported(int64_t B, int64_t K, int64_t E, int64_t width) {
   // the token streams address rows with 32-bit byte offsets (routes x width BF16)
-  return B <= kDecMaxTokens && B * K <= kDecMaxEntries && E <= kDecMaxExperts && B * K * width * 2 < (1ll << 31);
+  return B <= kDecMaxTokens && B * K <= kDecMaxEntries && E <= kMaxExperts && B * K * width * 2 < (1ll << 31);
 }
 
 template <int FG, int FD>

@@ -17,8 +17,8 @@ def routes(logits, top_k, active=None):
         raise ValueError("logits must be a GPU tensor [tokens, experts]")
     logits = logits.to(torch.float32).contiguous()
     B, E = logits.shape
-    if type(top_k) is not int or not 1 <= top_k <= min(E, 32) or E > 256:
-        raise ValueError("need 1 <= top_k <= min(experts, 32) and experts <= 256")
+    if type(top_k) is not int or not 1 <= top_k <= min(E, 32) or E > 1024:
+        raise ValueError("need 1 <= top_k <= min(experts, 32) and experts <= 1024")
     act = None
     if active is not None:
         act = active.to(device=logits.device, dtype=torch.uint8).contiguous()

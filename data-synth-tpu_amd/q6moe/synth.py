@@ -118,6 +118,66 @@ def moe_layer(
     return out
 
 
+def _expert_weights(seed, e, hidden, intermediate, sigma, quant, quant_d):
+    rng = np.random.default_rng([seed, e])
+    g = quant(_normal(rng, (intermediate, hidden), sigma))
+    u = quant(_normal(rng, (intermediate, hidden), sigma))
+    d = quant_d(_normal(rng, (hidden, intermediate), sigma))
+    return g, u, d
+
+
+def wide_moe_layer(
+    seed=5,
+    experts=512,
+    top_k=10,
+    hidden=2560,
+    intermediate=640,
+    tokens=8,
+    sigma=0.02,
+    qtype="Q6_K",
+    down_qtype="Q8_0",
+    bias_sigma=None,
+    workers=None,
+):
+    """A wide routed layer whose experts are drawn independently: by default
+    the MoE layer of the reference's model (kaggle/qwen38_tpu/config.py:13-19:
+    512 experts, top-10, hidden 2560, intermediate 640) in the formats of its
+    Q6 checkpoint (checkpoints/q6.json: Q6_K gate/up, Q8_0 down in every layer).
+
+    Draw order: ``default_rng(seed)``: x [B, H], logits [B, E], bias [E] (if
+    ``bias_sigma``); then expert e's gate [I, H], up [I, H] and down [H, I],
+    each N(0, sigma), from its own ``default_rng([seed, e])``, so the experts
+    are quantized on a thread pool (``workers``) with the same bytes for any
+    pool size. Returns the same keys as ``moe_layer`` (raw GGUF tables
+    [E, rows, blocks, bytes], no SoA planes).
+    """
+    from concurrent.futures import ThreadPoolExecutor
+    import os
+
+    rng = np.random.default_rng(seed)
+    x = _normal(rng, (tokens, hidden))
+    logits = _normal(rng, (tokens, experts))
+    if bias_sigma is not None:
+        logits = (logits + _normal(rng, (experts,), bias_sigma)[None, :]).astype(np.float32)
+    quant, quant_d = QUANTIZERS[qtype], QUANTIZERS[down_qtype]
+    first = _expert_weights(seed, 0, hidden, intermediate, sigma, quant, quant_d)
+    tables = {n: np.empty((experts,) + t.shape, np.uint8) for n, t in zip(("gate", "up", "down"), first)}
+
+    def one(e):
+        parts = first if e == 0 else _expert_weights(seed, e, hidden, intermediate, sigma, quant, quant_d)
+        for n, t in zip(("gate", "up", "down"), parts):
+            tables[n][e] = t
+
+    workers = workers or min(16, len(os.sched_getaffinity(0)))
+    with ThreadPoolExecutor(workers) as pool:
+        list(pool.map(one, range(experts)))
+    ids, weights = softmax_topk(logits, top_k)
+    out = dict(x=x, logits=logits, experts=experts, top_k=top_k, hidden=hidden, intermediate=intermediate,
+               qtype=qtype, down_qtype=down_qtype, ids=ids, weights=weights)
+    out.update(tables)
+    return out
+
+
 def kv_pages(seed=4, batch=8, context=32768, page_size=256, kv_heads=4, head_dim=128, q_heads=32):
     """Draw order: K [pages, P, KVH, D]; V (same); page-table permutation; q [B, Hq, D].
 

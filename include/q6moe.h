@@ -164,7 +164,7 @@ typedef struct q6moe_table {
 
 typedef struct q6moe_moe_args {
   q6moe_table gate, up, down;  /* gate/up: [I rows, H], down: [H rows, I] per expert */
-  int64_t experts;             /* E */
+  int64_t experts;             /* E, 1..1024 (the reference model's layer has 512) */
   int64_t hidden;              /* H */
   int64_t intermediate;        /* I */
   const uint16_t* x;           /* BF16 [B, H] */
@@ -180,7 +180,7 @@ typedef struct q6moe_moe_args {
   void* workspace;             /* >= q6moe_moe_workspace_size(...) bytes, 256-byte aligned */
   size_t workspace_bytes;
   /* kernel family: 0 the decode-step kernels up to 64 tokens where they apply, else the
-     grouped ones; 1 the decode-step kernels (B <= 256, B*top_k <= 1024, E <= 256 and
+     grouped ones; 1 the decode-step kernels (B <= 256, B*top_k <= 1024, E <= 1024 and
      B*top_k*max(H, I, Is) < 2^30, else Q6MOE_ERR_INVALID); 2 the grouped-GEMM (prefill)
      kernels, tiled on the matrix cores for Q6_K with H and I multiples of 256 */
   int mode;
@@ -203,7 +203,7 @@ typedef struct q6moe_moe_args {
 
 /*
  * Router (routes_and_shared's routing, kaggle/qwen38_tpu/math.py:277-281): FP32
- * softmax of logits [B, E] (E <= 256), top_k (k <= 32; larger probability
+ * softmax of logits [B, E] (E <= 1024), top_k (k <= 32; larger probability
  * first, lower expert id on ties), weights divided by their FP32 sum in
  * selection order, rows with active[b] == 0 zeroed (active NULL: all active),
  * RNE to BF16. Writes ids int32 [B, k] and weights BF16 [B, k]: the ids and

@@ -15,7 +15,10 @@ from q6moe.router import routes
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("tokens,experts,top_k", [(8, 128, 8), (300, 64, 6), (5, 256, 32), (3, 7, 7), (1, 1, 1)])
+@pytest.mark.parametrize("tokens,experts,top_k", [(8, 128, 8), (300, 64, 6), (5, 256, 32), (3, 7, 7), (1, 1, 1),
+                                                   # the reference model's router (config.py:17-18) and the
+                                                   # widest layer the kernels take
+                                                   (64, 512, 10), (2048, 512, 10), (9, 257, 3), (17, 1024, 32)])
 def test_router_matches_oracle(device, tokens, experts, top_k):
     rng = np.random.default_rng(tokens * experts + top_k)
     logits = rng.standard_normal((tokens, experts)).astype(np.float32)
@@ -36,3 +39,8 @@ def test_router_ties_pick_the_lower_id(device):
     ids, _ = routes(torch.from_numpy(logits).to(device), 4)
     want_ids, _ = oracle_routing.route(logits, 4)
     np.testing.assert_array_equal(ids.cpu().numpy(), want_ids)
+
+
+def test_router_rejects_more_than_1024_experts(device):
+    with pytest.raises(ValueError, match="experts <= 1024"):
+        routes(torch.zeros((2, 1025), device=device), 4)
