@@ -1121,7 +1121,8 @@ extern "C" int q6moe_moe_unpack(const uint8_t* table, int qtype, int64_t experts
                     width <= (1 << 24) && (!block32_qtype(qtype) || width % 32 == 0),
                 "moe_unpack: bad shape");
   Q6MOE_REQUIRE(path >= 0 && path <= 2, "moe_unpack: path must be 0 (generic), 1 (decode) or 2 (prefill)");
-  Q6MOE_REQUIRE(path != 2 || qtype == Q6MOE_Q6_K, "moe_unpack: the prefill path decodes Q6_K only");
+  Q6MOE_REQUIRE(path != 2 || pf_unpack_supported(fmt_of(qtype)),
+                "moe_unpack: the prefill path decodes Q6_K, Q8_0, Q5_1 and Q4_K");
   const int64_t need = unit_table_bytes(qtype, rows, width);
   Q6MOE_REQUIRE(aligned(table, 16) && (experts == 1 || (stride >= need && stride % 16 == 0)),
                 "moe_unpack: table must be 16-byte aligned with a stride covering one expert");
@@ -1135,7 +1136,7 @@ extern "C" int q6moe_moe_unpack(const uint8_t* table, int qtype, int64_t experts
   if (path == 1) {
     launch_dec_unpack(fmt, p, (int)experts, out, s);
   } else if (path == 2) {
-    launch_pf_unpack(p, (int)experts, out, s);
+    launch_pf_unpack(fmt, p, (int)experts, out, s);
   } else if (fmt == FMT_Q6) {
     hipLaunchKernelGGL(moe_unit_unpack_kernel<FMT_Q6>, grid, dim3(64), 0, s, p, out);
   } else if (fmt == FMT_Q4K) {
@@ -1380,10 +1381,16 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
   const int max_tokens = (int)B;  // an expert sees each token at most once
   // int8_q8 policy: the Q8_0 projections run W8A8 (compute.py:20-34)
   const bool w8_gu = w8 && fmt == FMT_Q8, w8_dn = w8 && fmt_dn == FMT_Q8;
-  // The tiled MFMA path addresses token rows with 32-bit byte offsets.
-  const bool tiled = pf_supported(fmt, H, I) && B * H * 2 < (1ll << 31) && B * K * I * 2 < (1ll << 31);
+  // The tiled MFMA kernels address token rows with 32-bit byte offsets.
+  const bool rows32 = B * H * 2 < (1ll << 31) && B * K * I * 2 < (1ll << 31);
+  const bool tiled_gu = !w8_gu && rows32 && pf_gate_up_supported(fmt, H, I);
+  const bool tiled_dn = !w8_dn && rows32 && pf_down_supported(fmt_dn, H, I);
+  const int max_tiles = (int)(E + B * K / kPrefillTile + 1);
+  if ((tiled_gu || tiled_dn) && pf_tile_routes() != kPrefillTile) {
+    set_error("moe_forward: prefill tile size mismatch");
+    return Q6MOE_ERR_HIP;
+  }
   // gate/up + SwiGLU
-  bool down_done = false;
   if (w8_gu) {
     mark(1);
     int8_t* xq = reinterpret_cast<int8_t*>(w + L.xq);
@@ -1391,16 +1398,10 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
     launch_act_q8(a->x, B, (int)H, nullptr, xq, xq_s, s);
     launch_w8(true, g, u, routed, slots, 0, W8Src{xq, xq_s, (int)H}, ws.act, s);
     mark(2);
-  } else if (tiled) {
-    if (pf_tile_routes() != kPrefillTile) {
-      set_error("moe_forward: prefill tile size mismatch");
-      return Q6MOE_ERR_HIP;
-    }
-    const int max_tiles = (int)(E + B * K / kPrefillTile + 1);
-    down_done = fmt_dn == FMT_Q6 && !w8_dn;  // a Q6_K down runs tiled in the same call
+  } else if (tiled_gu) {
     // events[1] and [2] take the gate/up kernel's own start and end timestamps
-    launch_moe_prefill(g, u, d, ws, max_tiles, a->x, (int)B, (int)(B * K), (int)H, (int)I, s,
-                       a->events ? a->events[1] : nullptr, a->events ? a->events[2] : nullptr, down_done);
+    launch_moe_prefill_gate_up(fmt, g, u, ws, max_tiles, a->x, (int)B, (int)H, (int)I, s,
+                               a->events ? a->events[1] : nullptr, a->events ? a->events[2] : nullptr);
   } else {
     mark(1);
     dispatch_format(fmt, [&](auto fg) {
@@ -1414,7 +1415,9 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
     float* aq_s = reinterpret_cast<float*>(w + L.aq_s);
     launch_act_q8(ws.act, B * K, (int)I, ws.hdr + 1, aq, aq_s, s);  // rows beyond the routes are skipped
     launch_w8(false, d, d, routed, slots, 1, W8Src{aq, aq_s, (int)I}, ws.y, s);
-  } else if (!down_done) {
+  } else if (tiled_dn) {
+    launch_moe_prefill_down(fmt_dn, d, ws, max_tiles, (int)(B * K), (int)H, (int)I, s);
+  } else {
     dispatch_format(fmt_dn, [&](auto fd) {
       launch_down<decltype(fd)::value>(d, routed, slots, max_tokens, ws.act, (int)H, (int)I, ws.y, s);
     });

@@ -191,14 +191,21 @@ int launch_moe_decode(int fmt_gu, int fmt_dn, const DecArgs& A, hipStream_t s);
 // Unit-decode probes (q6moe_moe_unpack): the decode kernels' LDS-staged path
 // and the prefill kernels' whole-block register path, for the bit-exact tests.
 int launch_dec_unpack(int fmt, const Proj& p, int experts, uint16_t* out, hipStream_t s);
-int launch_pf_unpack(const Proj& p, int experts, uint16_t* out, hipStream_t s);
+bool pf_unpack_supported(int fmt);
+int launch_pf_unpack(int fmt, const Proj& p, int experts, uint16_t* out, hipStream_t s);
 
-// Prefill grouped GEMM (Q6_K, hidden and intermediate multiples of 256).
-bool pf_supported(int fmt, int64_t H, int64_t I);
+// Prefill grouped GEMM, tiled on the matrix cores: gate/up (Q6_K, Q8_0 or
+// Q4_K; hidden a multiple of 128, intermediate of 64) and down (Q6_K, Q8_0,
+// Q5_1 or Q4_K; intermediate a multiple of 128, hidden of 128), each launched
+// on its own.
+bool pf_gate_up_supported(int fmt, int64_t H, int64_t I);
+bool pf_down_supported(int fmt, int64_t H, int64_t I);
 int64_t pf_tile_routes();
-int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
-                       const uint16_t* x, int B, int routes, int H, int I, hipStream_t s, void* gate_up_start,
-                       void* after_gate_up, bool with_down);
+int launch_moe_prefill_gate_up(int fmt, const Proj& g, const Proj& u, const MoeWs& ws, int max_tiles,
+                               const uint16_t* x, int B, int H, int I, hipStream_t s, void* gate_up_start,
+                               void* after_gate_up);
+int launch_moe_prefill_down(int fmt, const Proj& d, const MoeWs& ws, int max_tiles, int routes, int H, int I,
+                            hipStream_t s);
 
 // ---------------------------------------------------------------------------
 // Unit decoders: 16 output rows x one 256-wide K block -> 8 MFMA A operands.

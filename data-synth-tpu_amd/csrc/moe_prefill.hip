@@ -1,4 +1,6 @@
-// Prefill-shaped routed experts on Q6_K tables: tiled grouped GEMM on BF16 MFMA.
+// Prefill-shaped routed experts: tiled grouped GEMM on BF16 MFMA over
+// unit-major expert tables (gate/up Q6_K, Q8_0 or Q4_K; down Q6_K, Q8_0, Q5_1
+// or Q4_K).
 //
 // The routing kernel (moe.hip) groups the routes by expert (ascending id,
 // tokens ascending) and splits each expert's routes into tiles of 128. One
@@ -15,7 +17,9 @@
 // Each wave owns 2 units (16 weight rows x one 256-wide K block) per K block,
 // loads a unit's bytes into one of two register sets during the previous
 // block's first K half, and decodes each half straight into MFMA A operands;
-// decoded weights never leave registers. The 128 token
+// decoded weights never leave registers. K runs in halves of 128 (so K needs
+// only be a multiple of 128: a last, half K block multiplies its first half,
+// and the unit's zero padding beyond K is never decoded). The 128 token
 // rows of the current K half sit in LDS (double-buffered, XOR-swizzled so the
 // 16 token columns of an MFMA read hit distinct banks), filled by direct
 // buffer->LDS DMA, and every wave multiplies them against its own rows. The
@@ -39,7 +43,6 @@ constexpr int kM = 128;            // routes per tile (MFMA column groups of 16)
 constexpr int kUnits = 2;          // units per wave per K block
 constexpr int kHalfBytes = kM * 128 * 2;  // one K half of the token tile (32 KB)
 constexpr int kXStages = 2;        // token-tile stages in LDS: the K half being multiplied and the next
-constexpr int kWLoads = 5;         // weight loads per unit per K block (3 code chunks, sub-scales, d)
 // A tile of NCG (2, 4, 6 or 8) 16-route column groups: the token rows of a K
 // half take NCG KB per wave, i.e. NCG DMA instructions of 1 KB per wave.
 constexpr int kLds = kXStages * kHalfBytes;
@@ -79,41 +82,167 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// The weights of one unit (a whole K block), in the registers of the lane
-// that decodes them (row j = lane % 16, k-group jA = lane / 16): its four code
-// words of each of the three code chunks (bit-planar layout), its sub-scale
-// word and the row's FP16 scale. Both K halves decode from one load.
-struct BlockRegs {
+// The weights of one unit (a whole K block) in the registers of the lane that
+// decodes them (row j = lane % 16, k-group jA = lane / 16); both K halves
+// decode from one load. ``load`` issues kLoads vector-memory instructions;
+// ``half(h)`` gives the 4 A fragments of K half h; ``gran(f, jA)`` is the
+// 8-column granule, within the half, of fragment f for k-group jA (the token
+// operand it pairs with); ``pin`` makes the registers opaque to the compiler.
+template <int FMT>
+struct Block;
+
+// Q6_K (bit-planar unit): the lane's four code words of each of the three code
+// chunks, its sub-scale word and the row's FP16 scale. Fragment 2g + e of the
+// unit covers positions 64g + 16jA + 8e + [0, 8) (q6_xfrag_offset).
+template <>
+struct Block<FMT_Q6> {
+  static constexpr int kLoads = 5;
   u32x4 c0, c1, c2;
   uint32_t sc, d;
+  __device__ __forceinline__ void load(const uint8_t* v, int lane) {
+    c0 = *reinterpret_cast<const u32x4*>(v + 16 * lane);
+    c1 = *reinterpret_cast<const u32x4*>(v + 1024 + 16 * lane);
+    c2 = *reinterpret_cast<const u32x4*>(v + 2048 + 16 * lane);
+    sc = *reinterpret_cast<const uint32_t*>(v + 3072 + 4 * lane);
+    d = *reinterpret_cast<const uint16_t*>(v + 3328 + 2 * (lane & 15));
+  }
+  __device__ __forceinline__ void pin() { asm volatile("" : "+v"(c0), "+v"(c1), "+v"(c2), "+v"(sc), "+v"(d)); }
+  __device__ __forceinline__ void half(int h, int, u32x4 a[4]) const {
+    const float dd = half_bits_to_float(d);
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg)
+      q6p_group(c0[2 * h + gg], c1[2 * h + gg], c2[2 * h + gg], q6p_ds(dd, sc, 2 * h + gg), a[2 * gg],
+                a[2 * gg + 1]);
+  }
+  static __device__ __forceinline__ int gran(int f, int jA) { return 8 * (f >> 1) + 2 * jA + (f & 1); }
 };
 
-__device__ __forceinline__ void load_block(const uint8_t* units, int kbs, int rg, int kb, int lane, BlockRegs& r) {
-  const uint8_t* v = units + ((int64_t)rg * kbs + kb) * kQ6Unit;
-  r.c0 = *reinterpret_cast<const u32x4*>(v + 16 * lane);
-  r.c1 = *reinterpret_cast<const u32x4*>(v + 1024 + 16 * lane);
-  r.c2 = *reinterpret_cast<const u32x4*>(v + 2048 + 16 * lane);
-  r.sc = *reinterpret_cast<const uint32_t*>(v + 3072 + 4 * lane);
-  r.d = *reinterpret_cast<const uint16_t*>(v + 3328 + 2 * (lane & 15));
-}
-
-// The 4 A fragments of K half h (f = 4h..4h+3) of a unit.
-__device__ __forceinline__ void decode_half(const BlockRegs& w, int h, int lane, u32x4 a[4]) {
-  const float d = half_bits_to_float(w.d);
+// Q8_0: the lane's four code chunks (chunk g: fragments 2g, 2g+1 at the Q6_K
+// positions) and the FP16 scales of its blocks 2g + jA/2; w = d * q exact,
+// RNE to BF16 (gguf_quant.py:111-114).
+template <>
+struct Block<FMT_Q8> {
+  static constexpr int kLoads = 5;
+  u32x4 c[4];
+  u32x2 dw;
+  __device__ __forceinline__ void load(const uint8_t* v, int lane) {
 #pragma unroll
-  for (int gg = 0; gg < 2; ++gg)
-    q6p_group(w.c0[2 * h + gg], w.c1[2 * h + gg], w.c2[2 * h + gg], q6p_ds(d, w.sc, 2 * h + gg), a[2 * gg],
-              a[2 * gg + 1]);
+    for (int g = 0; g < 4; ++g) c[g] = *reinterpret_cast<const u32x4*>(v + 1024 * g + 16 * lane);
+    dw = *reinterpret_cast<const u32x2*>(v + 4096 + 8 * (2 * (lane & 15) + (lane >> 5)));
+  }
+  __device__ __forceinline__ void pin() { asm volatile("" : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(dw)); }
+  __device__ __forceinline__ void half(int h, int, u32x4 a[4]) const {
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      const int g = 2 * h + gg;
+      const float d = half_bits_to_float((dw[g >> 1] >> (16 * (g & 1))) & 0xffffu);
+      a[2 * gg] = q8_frag<true>(c[g][0], c[g][1], d);
+      a[2 * gg + 1] = q8_frag<true>(c[g][2], c[g][3], d);
+    }
+  }
+  static __device__ __forceinline__ int gran(int f, int jA) { return Block<FMT_Q6>::gran(f, jA); }
+};
+
+// Q5_1: the lane's four nibble chunks (chunk g: fragments 2g, 2g+1 at the
+// Q6_K positions, the low or high nibbles of block 2g + jA/2) and the blocks'
+// high-bit words and FP16 d, m; w = fma(q, d, m), one rounding, RNE to BF16
+// (kaggle/qwen38_tpu/quant.py:34-53).
+template <>
+struct Block<FMT_Q51> {
+  static constexpr int kLoads = 6;
+  u32x4 q[4];
+  u32x4 aux[2];  // blocks 2g + jA/2 of g = 0, 1 and of g = 2, 3: (high word, d | m << 16)
+  __device__ __forceinline__ void load(const uint8_t* v, int lane) {
+    const int j = lane & 15, hb = lane >> 5;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) q[g] = *reinterpret_cast<const u32x4*>(v + 512 * g + 256 * hb + 16 * j);
+    aux[0] = *reinterpret_cast<const u32x4*>(v + 2048 + 64 * j + 32 * hb);
+    aux[1] = *reinterpret_cast<const u32x4*>(v + 2048 + 64 * j + 32 * hb + 16);
+  }
+  __device__ __forceinline__ void pin() {
+    asm volatile("" : "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(aux[0]), "+v"(aux[1]));
+  }
+  __device__ __forceinline__ void half(int h, int lane, u32x4 a[4]) const {
+    const int odd = (lane >> 4) & 1;
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      const int g = 2 * h + gg;
+      const uint32_t qh = aux[h][2 * gg], dm = aux[h][2 * gg + 1];
+      const float d = half_bits_to_float(dm & 0xffff), m = half_bits_to_float(dm >> 16);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        uint32_t c0 = q[g][2 * e], c1 = q[g][2 * e + 1];
+        c0 = (odd ? c0 >> 4 : c0) & 0x0f0f0f0fu;
+        c1 = (odd ? c1 >> 4 : c1) & 0x0f0f0f0fu;
+        const uint32_t hb8 = qh >> (16 * odd + 8 * e);
+        c0 |= spread4(hb8) << 4;
+        c1 |= spread4(hb8 >> 4) << 4;
+        a[2 * gg + e] = q6_frag(c0, c1, d, m);
+      }
+    }
+  }
+  static __device__ __forceinline__ int gran(int f, int jA) { return Block<FMT_Q6>::gran(f, jA); }
+};
+
+// Q4_K, with a lane map of its own (the unit's bytes are those of the other
+// kernels): in K half h the lane decodes sub-block 4h + jA, positions
+// 128h + 32jA + [0, 32), i.e. the low (jA even) or high (jA odd) nibbles of
+// its row's qs bytes 32(2h + jA/2) + [0, 32) (chunks 1 + 2c and 2 + 2c of the
+// unit, c = 2h + jA/2); fragment f holds positions 8f + [0, 8) of it. The
+// codes enter v_fma_mix_f32 as FP16 subnormals (sub_frag): w = fma(q, d*sc,
+// -dmin*m), one rounding, RNE to BF16 (gguf_quant.py:115-157).
+template <>
+struct Block<FMT_Q4K> {
+  static constexpr int kLoads = 5;
+  u32x4 hdr;
+  u32x4 qs[2][2];  // [half][chunk]
+  __device__ __forceinline__ void load(const uint8_t* v, int lane) {
+    const int j = lane & 15, jA = lane >> 4;
+    hdr = *reinterpret_cast<const u32x4*>(v + 16 * j);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int c = 2 * h + (jA >> 1);
+      qs[h][0] = *reinterpret_cast<const u32x4*>(v + 16 * (16 * (1 + 2 * c) + j));
+      qs[h][1] = *reinterpret_cast<const u32x4*>(v + 16 * (16 * (2 + 2 * c) + j));
+    }
+  }
+  __device__ __forceinline__ void pin() {
+    asm volatile("" : "+v"(hdr), "+v"(qs[0][0]), "+v"(qs[0][1]), "+v"(qs[1][0]), "+v"(qs[1][1]));
+  }
+  __device__ __forceinline__ void half(int h, int lane, u32x4 a[4]) const {
+    const int jA = lane >> 4, odd = jA & 1;
+    const float d = half_bits_to_float(hdr[0] & 0xffff);
+    const float dmin = half_bits_to_float(hdr[0] >> 16);
+    // sub-block 4h + jA: its 6-bit scale and min (gguf_quant.py:118-135)
+    uint32_t scb, mnb;
+    if (h == 0) {
+      scb = (hdr[1] >> (8 * jA)) & 63;
+      mnb = (hdr[2] >> (8 * jA)) & 63;
+    } else {
+      const uint32_t xb = hdr[3] >> (8 * jA);
+      scb = (xb & 15) | ((hdr[1] >> (8 * jA + 2)) & 48);
+      mnb = ((xb >> 4) & 15) | ((hdr[2] >> (8 * jA + 2)) & 48);
+    }
+    const float ds = d * (float)scb, dm = -(dmin * (float)mnb);
+    const uint32_t m = odd ? 0x00F000F0u : 0x000F000Fu;
+    const float s = ds * (odd ? 1048576.f : 16777216.f);
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const uint32_t w0 = qs[h][f >> 1][2 * (f & 1)], w1 = qs[h][f >> 1][2 * (f & 1) + 1];
+      a[f] = sub_frag(w0 & m, (w0 >> 8) & m, w1 & m, (w1 >> 8) & m, s, dm);
+    }
+  }
+  static __device__ __forceinline__ int gran(int f, int jA) { return 4 * jA + f; }
+};
+
+// K position, inside a 256-wide block, of fragment f (0..7: K half f / 4) of k-group jA.
+template <int FMT>
+__device__ __forceinline__ int block_xoff(int f, int jA) {
+  return 128 * (f >> 2) + 8 * Block<FMT>::gran(f & 3, jA);
 }
 
 // LDS byte offset of token-tile granule (token t, 8-column granule c) of a K half.
 __device__ __forceinline__ int xgran(int t, int c) { return (t * 16 + (c ^ (t & 15))) * 16; }
-
-// Granule of the x operand of fragment f (within its K half) for k-group jA.
-__device__ __forceinline__ int xfrag_gran(int f, int jA) {
-  const int g = f >> 1, e = f & 1;
-  return 4 * ((jA >> 1) + 2 * (g & 1)) + 2 * (jA & 1) + e;
-}
 
 struct Tile {
   int64_t expert;
@@ -180,14 +309,16 @@ __device__ __forceinline__ void x_offsets(uint32_t (&xoff)[NCG], const int (&row
 // first-half step, the next block's weights for unit 0 and unit 1), so that
 // the four waves of a workgroup do not all queue their vector-memory
 // instructions at once right after the barrier.
-template <int NCG, typename RowFn, typename RowOf>
+template <int FMT, int NCG, typename RowFn, typename RowOf>
 __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
                                           const uint16_t* x, int x_rows, RowOf row_of, int K, int64_t expert,
                                           f32x4 (&acc)[kUnits][NCG]) {
   const int wave = wave_id(), lane = threadIdx.x & 63;
   const int j = lane & 15, jA = lane >> 4;
-  const int kbs = K / kQK;
-  const int S = 2 * kbs;
+  const int S = K / 128;           // K halves (K is a multiple of 128)
+  const int kbs = (S + 1) >> 1;    // K blocks of the table, the last one possibly half used
+  constexpr int kWLoads = Block<FMT>::kLoads;
+  constexpr int kUB = UnitBytes<FMT>::value;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(x), (short)0, (int)((uint32_t)x_rows * (uint32_t)K * 2u), 0x00020000);
   const uint8_t* units[kUnits];
@@ -203,7 +334,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
   // DMA), so they have a step and a half to arrive; the second-half step that
   // follows waits only for its token DMA.
   static_assert(kXStages == 2, "two K halves per block");
-  BlockRegs wr[2][kUnits];
+  Block<FMT> wr[2][kUnits];
   uint32_t xoff[NCG];  // per-lane byte offsets of the token rows, set in the prologue
   // Issued step s (the step after the current one): token DMA in parts 0 and
   // 1; for a second-half s (block b = s/2), block b+1's weights in parts 2
@@ -220,7 +351,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
 #pragma unroll
       for (int i = i0; i < i0 + per; ++i) bdma16(xr, xoff[i], (uint32_t)(kb * kQK + h * 128) * 2u, xs + i * 1024);
     } else if constexpr (slot == 1 && part - 2 < kUnits) {
-      if (kb + 1 < kbs) load_block(units[part - 2], kbs, rgs[part - 2], kb + 1, lane, wr[wset][part - 2]);
+      if (kb + 1 < kbs) wr[wset][part - 2].load(units[part - 2] + ((int64_t)rgs[part - 2] * kbs + kb + 1) * kUB, lane);
     }
   };
   auto step = [&](int s, auto slot_c, auto set_c) {
@@ -237,18 +368,15 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     // here so that the compiler does not also wait, after the next step's
     // loads are issued, for everything in flight before decoding them.
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) {
-      BlockRegs& w = wr[set][u];
-      asm volatile("" : "+v"(w.c0), "+v"(w.c1), "+v"(w.c2), "+v"(w.sc), "+v"(w.d));
-    }
+    for (int u = 0; u < kUnits; ++u) wr[set][u].pin();
     const bool more = s + 1 < S;
     const uint8_t* xs = smem + slot * kHalfBytes;
     u32x4 a[kUnits][4];
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) decode_half(wr[set][u], slot, lane, a[u]);  // slot == s % 2 == h
+    for (int u = 0; u < kUnits; ++u) wr[set][u].half(slot, lane, a[u]);  // slot == s % 2 == h
     static_for<0, 4>([&](auto fc) {
       constexpr int f = decltype(fc)::value;
-      const int c = xfrag_gran(f, jA);
+      const int c = Block<FMT>::gran(f, jA);
 #pragma unroll
       for (int tg = 0; tg < NCG; ++tg) {
         const u32x4 xv = *reinterpret_cast<const u32x4*>(xs + xgran(tg * 16 + j, c));
@@ -268,7 +396,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     int rows[NCG];
     tile_rows(rows, row_of);
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) load_block(units[u], kbs, rgs[u], 0, lane, wr[0][u]);
+    for (int u = 0; u < kUnits; ++u) wr[0][u].load(units[u] + (int64_t)rgs[u] * kbs * kUB, lane);
     asm volatile("" ::: "memory");  // every load above issues before the offsets wait on the rows
     x_offsets(xoff, rows, K);
   }
@@ -277,11 +405,9 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
   });
   for (int s0 = 0; s0 < S; s0 += 4) {
     step(s0, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-    step(s0 + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
-    if (s0 + 2 < S) {
-      step(s0 + 2, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
-      step(s0 + 3, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
-    }
+    if (s0 + 1 < S) step(s0 + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+    if (s0 + 2 < S) step(s0 + 2, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+    if (s0 + 3 < S) step(s0 + 3, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
   }
 }
 
@@ -300,6 +426,7 @@ __device__ __forceinline__ void with_column_groups(int nv, F&& f) {
 
 }  // namespace pf
 
+template <int FMT>
 __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     moe_pf_gate_up_kernel(Proj gate, Proj up, MoeWs ws, const uint16_t* __restrict__ x, int tokens, int hidden,
                           uint16_t* __restrict__ act, int inter) {
@@ -321,8 +448,9 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
       for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pf_stream<NCG>(smem, projs, unit_proj, [&](int) { return rgb; }, x, tokens,
-                   [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; }, hidden, T.expert, acc);
+    pf_stream<FMT, NCG>(smem, projs, unit_proj, [&](int) { return rgb; }, x, tokens,
+                        [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; }, hidden, T.expert,
+                        acc);
     const int row = rgb * 16 + 4 * jA;
 #pragma unroll
     for (int tg = 0; tg < NCG; ++tg) {
@@ -344,6 +472,7 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
   });
 }
 
+template <int FMT>
 __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     moe_pf_down_kernel(Proj down, MoeWs ws, const uint16_t* __restrict__ act, int routes, int inter,
                        uint16_t* __restrict__ y, int hidden) {
@@ -365,8 +494,8 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
       for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pf_stream<NCG>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, routes,
-                   [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); }, inter, T.expert, acc);
+    pf_stream<FMT, NCG>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, routes,
+                        [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); }, inter, T.expert, acc);
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
       const int row = (rgb + u) * 16 + 4 * jA;
@@ -384,53 +513,91 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
   });
 }
 
-bool pf_supported(int fmt, int64_t H, int64_t I) {
-  return fmt == FMT_Q6 && H % 256 == 0 && I % 256 == 0;
+// The tiled kernels take K in halves of 128 and whole workgroup row blocks:
+// gate/up 64 intermediate rows, down 128 hidden rows.
+bool pf_gate_up_supported(int fmt, int64_t H, int64_t I) {
+  return (fmt == FMT_Q6 || fmt == FMT_Q8 || fmt == FMT_Q4K) && H % 128 == 0 && I % (16 * pf::kWaves) == 0;
+}
+bool pf_down_supported(int fmt, int64_t H, int64_t I) {
+  return (fmt == FMT_Q6 || fmt == FMT_Q8 || fmt == FMT_Q51 || fmt == FMT_Q4K) && I % 128 == 0 &&
+         H % (32 * pf::kWaves) == 0;
 }
 
 int64_t pf_tile_routes() { return pf::kM; }
 
-int launch_moe_prefill(const Proj& g, const Proj& u, const Proj& d, const MoeWs& ws, int max_tiles,
-                       const uint16_t* x, int B, int routes, int H, int I, hipStream_t s, void* gate_up_start,
-                       void* after_gate_up, bool with_down) {
-  static std::atomic<uint64_t> attr_done{0};
-  once_per_device(attr_done, [] {
-    (void)hipFuncSetAttribute((const void*)moe_pf_gate_up_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
-    (void)hipFuncSetAttribute((const void*)moe_pf_down_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pf::kLds);
-  });
-  const auto grid = [&](int ncol) { return dim3((unsigned)(((int64_t)ncol * max_tiles + 7) / 8 * 8)); };
-  if (gate_up_start && after_gate_up) {
-    // the events take the kernel's own start and end timestamps
-    hipExtLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds, s,
-                          (hipEvent_t)gate_up_start, (hipEvent_t)after_gate_up, 0, g, u, ws, x, B, H, ws.act, I);
-  } else {
-    hipLaunchKernelGGL(moe_pf_gate_up_kernel, grid(I / (16 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds,
-                       s, g, u, ws, x, B, H, ws.act, I);
-    if (after_gate_up) (void)hipEventRecord((hipEvent_t)after_gate_up, s);
+template <typename F>
+static void dispatch_pf_format(int fmt, F&& f) {
+  switch (fmt) {
+    case FMT_Q8: f(std::integral_constant<int, FMT_Q8>{}); break;
+    case FMT_Q51: f(std::integral_constant<int, FMT_Q51>{}); break;
+    case FMT_Q4K: f(std::integral_constant<int, FMT_Q4K>{}); break;
+    default: f(std::integral_constant<int, FMT_Q6>{}); break;
   }
-  if (with_down)
-    hipLaunchKernelGGL(moe_pf_down_kernel, grid(H / (32 * pf::kWaves)), dim3(64 * pf::kWaves), pf::kLds, s,
-                       d, ws, ws.act, routes, I, ws.y, H);
+}
+
+static dim3 pf_grid(int ncol, int max_tiles) { return dim3((unsigned)(((int64_t)ncol * max_tiles + 7) / 8 * 8)); }
+
+int launch_moe_prefill_gate_up(int fmt, const Proj& g, const Proj& u, const MoeWs& ws, int max_tiles,
+                               const uint16_t* x, int B, int H, int I, hipStream_t s, void* gate_up_start,
+                               void* after_gate_up) {
+  dispatch_pf_format(fmt, [&](auto fc) {
+    constexpr int FMT = decltype(fc)::value;
+    static std::atomic<uint64_t> attr_done{0};
+    once_per_device(attr_done, [] {
+      (void)hipFuncSetAttribute((const void*)moe_pf_gate_up_kernel<FMT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                pf::kLds);
+    });
+    const dim3 grid = pf_grid(I / (16 * pf::kWaves), max_tiles);
+    if (gate_up_start && after_gate_up) {
+      // the events take the kernel's own start and end timestamps
+      hipExtLaunchKernelGGL(moe_pf_gate_up_kernel<FMT>, grid, dim3(64 * pf::kWaves), pf::kLds, s,
+                            (hipEvent_t)gate_up_start, (hipEvent_t)after_gate_up, 0, g, u, ws, x, B, H, ws.act, I);
+    } else {
+      hipLaunchKernelGGL(moe_pf_gate_up_kernel<FMT>, grid, dim3(64 * pf::kWaves), pf::kLds, s, g, u, ws, x, B, H,
+                         ws.act, I);
+      if (after_gate_up) (void)hipEventRecord((hipEvent_t)after_gate_up, s);
+    }
+  });
   return Q6MOE_OK;
 }
 
-// Unit-decode probe of this path (Q6_K): load_block + decode_half of both K
+int launch_moe_prefill_down(int fmt, const Proj& d, const MoeWs& ws, int max_tiles, int routes, int H, int I,
+                            hipStream_t s) {
+  dispatch_pf_format(fmt, [&](auto fc) {
+    constexpr int FMT = decltype(fc)::value;
+    static std::atomic<uint64_t> attr_done{0};
+    once_per_device(attr_done, [] {
+      (void)hipFuncSetAttribute((const void*)moe_pf_down_kernel<FMT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                pf::kLds);
+    });
+    hipLaunchKernelGGL(moe_pf_down_kernel<FMT>, pf_grid(H / (32 * pf::kWaves), max_tiles), dim3(64 * pf::kWaves),
+                       pf::kLds, s, d, ws, ws.act, routes, I, ws.y, H);
+  });
+  return Q6MOE_OK;
+}
+
+// Unit-decode probe of this path: Block::load and Block::half of both K
 // halves, the prefill kernels' register path. grid (units per expert, experts).
+template <int FMT>
 __global__ void __launch_bounds__(64) moe_pf_unpack_kernel(Proj p, uint16_t* __restrict__ out) {
   const int lane = threadIdx.x;
   const int e = blockIdx.y, rg = blockIdx.x / p.kb, kb = blockIdx.x - rg * p.kb;
-  pf::BlockRegs w;
-  pf::load_block(p.data + (int64_t)e * p.dstride, p.kb, rg, kb, lane, w);
+  pf::Block<FMT> w;
+  w.load(p.data + (int64_t)e * p.dstride + ((int64_t)rg * p.kb + kb) * UnitBytes<FMT>::value, lane);
   u32x4 a[8];
-  pf::decode_half(w, 0, lane, a);
-  pf::decode_half(w, 1, lane, a + 4);
+  w.half(0, lane, a);
+  w.half(1, lane, a + 4);
   store_unit_frags(a, out + (int64_t)e * p.rows * p.k, p, rg, kb, lane,
-                   [](int f, int jA) { return q6_xfrag_offset(f, jA); });
+                   [](int f, int jA) { return pf::block_xoff<FMT>(f, jA); });
 }
 
-int launch_pf_unpack(const Proj& p, int experts, uint16_t* out, hipStream_t s) {
-  hipLaunchKernelGGL(moe_pf_unpack_kernel, dim3((unsigned)(cdiv(p.rows, 16) * p.kb), (unsigned)experts), dim3(64), 0,
-                     s, p, out);
+bool pf_unpack_supported(int fmt) { return fmt == FMT_Q6 || fmt == FMT_Q8 || fmt == FMT_Q51 || fmt == FMT_Q4K; }
+
+int launch_pf_unpack(int fmt, const Proj& p, int experts, uint16_t* out, hipStream_t s) {
+  const dim3 grid((unsigned)(cdiv(p.rows, 16) * p.kb), (unsigned)experts);
+  dispatch_pf_format(fmt, [&](auto fc) {
+    hipLaunchKernelGGL(moe_pf_unpack_kernel<decltype(fc)::value>, grid, dim3(64), 0, s, p, out);
+  });
   return Q6MOE_OK;
 }
 

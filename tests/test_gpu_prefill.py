@@ -31,6 +31,27 @@ def test_prefill_matches_oracle(device, tokens, experts, top_k, hidden, inter):
     assert_moe_close(got, _oracle(L))
 
 
+@pytest.mark.parametrize("qtype,down,hidden,inter", [
+    ("Q6_K", "Q8_0", 512, 640),   # the Q6 checkpoint's mix; down K = 5 halves of 128
+    ("Q8_0", "Q8_0", 384, 384),   # K of 3 halves for both projections
+    ("Q4_K", "Q5_1", 512, 384),   # the Q4 checkpoint's mix
+    ("Q4_K", "Q4_K", 256, 512),
+    ("Q6_K", "Q5_1", 256, 128),   # down K of a single half
+    ("Q8_0", "Q6_K", 640, 256),
+    ("Q4_K", "Q8_0", 768, 640),
+])
+def test_tiled_prefill_format_mixes(device, qtype, down, hidden, inter):
+    # Every format pair the tiled kernels take, with K not a multiple of 256
+    # (odd counts of 128-wide K halves) and skewed routes (partial tiles of
+    # every column-group count, experts over several 128-route tiles).
+    L = moe_layer(seed=hidden + inter, experts=6, top_k=2, hidden=hidden, intermediate=inter, tokens=300,
+                  qtype=qtype, down_qtype=down, bias_sigma=1.0, pack=False)
+    got, ctx = _run(L, device, mode=2)
+    assert_moe_close(got, _oracle(L))
+    fn, tabs, x, ids, w, _ = ctx
+    np.testing.assert_array_equal(got, fn(*tabs, x, ids, w).float().cpu().numpy())
+
+
 def test_prefill_partial_tiles_of_every_width(device):
     # Top-1 routes assigned so that expert e holds counts[e] routes: partial
     # tiles of 1-32, 33-64, 65-96 and 97-128 routes (2, 4, 6 and 8 column

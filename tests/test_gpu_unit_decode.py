@@ -3,7 +3,7 @@ MoE kernels use, against the oracle's ``dequantize_rows`` (gguf_quant.py:111-173
 
 ``q6moe_moe_unpack`` runs the generic kernels' register decode (path 0), the
 decode-step kernels' LDS-staged decode (path 1) and the prefill kernels'
-whole-block decode (path 2, Q6_K) on a packed table and returns the BF16
+whole-block decode (path 2: Q6_K, Q8_0, Q5_1, Q4_K) on a packed table and returns the BF16
 weights those kernels feed to the matrix cores. Every weight must equal
 RNE_bf16 of the oracle's FP32 value bit for bit; the one allowed difference
 is the sign of an exact zero (a Q6_K code of 32 decodes to +0 where d*sc < 0
@@ -62,11 +62,20 @@ def test_unit_decoders_are_bit_exact(device, qtype, path, rows, width):
     _check(unpack_experts(table, path), _want(raw, qtype, rows, width))
 
 
+@pytest.mark.parametrize("qtype", ["Q6_K", "Q8_0", "Q5_1", "Q4_K"])
 @pytest.mark.parametrize("rows,width", [(16, 256), (48, 768), (33, 512)])
-def test_prefill_unit_decoder_is_bit_exact(device, rows, width):
-    raw = _random_table("Q6_K", 2, rows, width, seed=rows + width)
-    table = pack_experts(raw.reshape(2, -1), "Q6_K", rows, width, device)
-    _check(unpack_experts(table, "prefill"), _want(raw, "Q6_K", rows, width))
+def test_prefill_unit_decoder_is_bit_exact(device, qtype, rows, width):
+    raw = _random_table(qtype, 2, rows, width, seed=rows + width)
+    table = pack_experts(raw.reshape(2, -1), qtype, rows, width, device)
+    _check(unpack_experts(table, "prefill"), _want(raw, qtype, rows, width))
+
+
+@pytest.mark.parametrize("qtype", ["Q8_0", "Q5_1"])
+def test_prefill_unit_decoder_half_block(device, qtype):
+    # a width of 640: the last unit holds one used K half and zero padding
+    raw = _random_table(qtype, 2, 40, 640, seed=640)
+    table = pack_experts(raw.reshape(2, -1), qtype, 40, 640, device)
+    _check(unpack_experts(table, "prefill"), _want(raw, qtype, 40, 640))
 
 
 @pytest.mark.parametrize("qtype,down", [("Q6_K", "Q6_K"), ("Q4_K", "Q4_K"), ("Q6_K", "Q8_0"), ("Q4_K", "Q5_1"),
