@@ -44,6 +44,16 @@ HBM traffic per launch from the committed rocprofv3 counter summaries
   always-on shared expert of 4096, N(0, 0.015), seed 3, at 1, 8 and 64 tokens.
 * kv_gather   paged INT8 KV gather + dequant of 8 x 32768 tokens, 4 KV heads of
   128, pages of 256, FP32 per-token-per-head scales, seed 4.
+* wide_layer  the reference model's MoE layer (512 experts, top-10, hidden
+  2560, intermediate 640, Q6_K gate/up + Q8_0 down, seed 5): decode steps of 1,
+  8 and 64 tokens and the 2048-token prefill.
+* prefill_q6_mix  the prefill layer with the Q6 checkpoint's Q8_0 down.
+* reference_harness  the reference harnesses' own cases: the packed-Q6 grid
+  (N 320/640/1280 x M 1/2/4/8 at K 2560) and the dense-cache KV gather (2051
+  of 8192 tokens, B 1/2/4/8), with the harnesses' host-side timing beside the
+  device time.
+* compute_policy  int8_q8 against bf16 on an all-Q8_0 layer at 8 and 4096
+  tokens, with the reference's selection rule (>= 10 % faster on both).
 
 The CPU baseline is the NumPy oracle (``kind: port``) on this host with the
 stated number of threads (the host's CPU affinity, at most 16), on a bounded
@@ -73,6 +83,7 @@ PREFILL_TOKENS, PREFILL_SEED, PREFILL_BIAS = 4096, 2, 0.5
 PREFILL_FLOPS = 2 * PREFILL_TOKENS * TOP_K * 3 * HIDDEN * INTER
 Q6_PROJ_BYTES = 768 * 8 * 210  # one 768x2048 (or 2048x768) Q6_K projection: 210 bytes per 256 weights
 PROFILES = ROOT / "profiles"
+PF_FORMAT_ID = {"Q6_K": 0, "Q4_K": 1, "Q8_0": 2, "Q5_1": 4}  # template argument of the tiled prefill kernels
 REPS = 7  # interleaved repetitions per method (>= 7, as the reference harness)
 
 
@@ -442,8 +453,222 @@ def measure_projection(dev, with_cpu):
     return res
 
 
-def measure_prefill(dev, steps, warmup, with_cpu):
-    """Prefill step (routing, gate/up, down, combine) on the seed-2 4096-token layer."""
+def _graph_per_call(bodies, per=20, reps=REPS):
+    """Device time per call (us) of each body(k), from replays of a captured HIP
+    graph of ``per`` calls, the methods' repetitions interleaved (timed_reps)."""
+    import torch
+
+    graphs = {}
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for name, body in bodies.items():
+            for k in range(2):
+                body(k)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for k in range(per):
+                    body(k)
+            graphs[name] = g
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    t = timed_reps({n: (lambda i, g=g: g.replay()) for n, g in graphs.items()}, reps=reps, inner=3)
+    return {n: round(st["median"] / per, 3) for n, st in t.items()}
+
+
+def _host_per_call(bodies, reps=REPS, seed=42):
+    """The reference harnesses' timing scope: host dispatch + execution +
+    synchronisation of one call, the methods interleaved in a seeded order per
+    repetition (kaggle/packed_q6/benchmark.py:127-149); median ms per method."""
+    import numpy as np
+    import torch
+
+    names = list(bodies)
+    for n in names:
+        for k in range(2):
+            bodies[n](k)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(seed)
+    samples = {n: [] for n in names}
+    for _ in range(reps):
+        for n in rng.permutation(names):
+            t0 = time.perf_counter()
+            bodies[n](0)
+            torch.cuda.synchronize()
+            samples[n].append((time.perf_counter() - t0) * 1e3)
+    return {n: round(float(np.median(v)), 4) for n, v in samples.items()}
+
+
+def measure_projection_grid(dev, with_cpu):
+    """The reference packed-Q6 harness's own cases (kaggle/packed_q6/benchmark.py:
+    110-126, 178-191): a canary M=1, N=64, K=256, then N in {320, 640, 1280} x M in
+    {1, 2, 4, 8} at K = 2560; methods: the fused projection, decode-then-BF16-GEMM
+    and predecoded BF16 GEMM. x N(0, 1) from seed 721 as the harness draws it; W
+    N(0, 0.02) quantized to Q6_K (the harness's legal random bytes stand in)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    from q6moe import _lib, pack_q6
+    from q6moe.kernel import q6_decode
+    from q6moe.quantize import QUANTIZERS
+
+    lib = _lib.load()
+    rows = []
+    cases = [(1, 64, 256)] + [(m, n, 2560) for n in (320, 640, 1280) for m in (1, 2, 4, 8)]
+    for m, n, k in cases:
+        rng = np.random.default_rng(3826 + n)
+        raw = QUANTIZERS["Q6_K"](rng.normal(0, 0.02, (n, k)).astype(np.float32))
+        packed = pack_q6(raw, k)
+        data = torch.from_numpy(packed.data).to(dev)
+        scales = torch.from_numpy(packed.scales).to(dev)
+        xf = np.random.default_rng(721).normal(size=(m, k)).astype(np.float32)
+        x = torch.from_numpy(xf).to(dev).to(torch.bfloat16)
+        y = torch.empty((m, n), dtype=torch.float32, device=dev)
+
+        def fused(_k, x=x, data=data, scales=scales, y=y, m=m, n=n, k=k):
+            rc = lib.q6moe_q6_matmul(ctypes.c_void_p(x.data_ptr()), m, k, k, ctypes.c_void_p(data.data_ptr()),
+                                     ctypes.c_void_p(scales.data_ptr()), n, ctypes.c_void_p(y.data_ptr()),
+                                     _lib.F32, n, _lib.stream_handle(dev))
+            _lib.check(rc, "q6_matmul")
+
+        xt = x.t().contiguous()
+        wpre = q6_decode(data, scales, output_features=n, input_features=k)
+        bodies = {"fused_q6": fused,
+                  "decode_then_bf16_gemm": lambda _k, d=data, s=scales, n=n, k=k, xt=xt: torch.mm(
+                      q6_decode(d, s, output_features=n, input_features=k), xt),
+                  "predecoded_bf16_gemm": lambda _k, w=wpre, xt=xt: torch.mm(w, xt)}
+        fused(0)
+        got = y.cpu().numpy()
+        if not np.isfinite(got).all():
+            raise CheckFailed(f"projection grid M={m} N={n}: nonfinite output rejected before timing")
+        row = {"M": m, "N": n, "K": k, "canary": (m, n, k) == (1, 64, 256)}
+        if with_cpu:
+            from oracle import packed_q6
+
+            want = packed_q6.projection_reference(x.float().cpu().numpy(), raw)
+            np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-4)
+            row["check"] = "rtol 2e-5, atol 2e-4 against the FP64 oracle"
+        dev_us = _graph_per_call(bodies)
+        host_ms = _host_per_call(bodies)
+        row.update({"device_us_per_call": dev_us, "host_ms_per_call": host_ms,
+                    "decode_gemm_over_fused": round(dev_us["decode_then_bf16_gemm"] / dev_us["fused_q6"], 3),
+                    "fused_over_predecoded": round(dev_us["fused_q6"] / dev_us["predecoded_bf16_gemm"], 3),
+                    "weight_bytes": int(raw.nbytes)})
+        rows.append(row)
+    return {"workload": "reference_packed_q6_grid_k2560_n320_640_1280_m1_2_4_8",
+            "timing": "device_us_per_call: replays of captured HIP graphs of 20 calls; host_ms_per_call: one "
+                      "call plus synchronisation from the host, as the reference harness times it",
+            "cases": rows}
+
+
+def measure_kv_harness(dev):
+    """The reference KV-gather harness's own cases (scripts/benchmark_qwen38_kv_gather.py:
+    54-70, 127-139): the reference model's dense cache (int8 codes [B, 8192, 512],
+    BF16 scale plane [B*16, 8192] of group 32, uniform(0, 0.03) with column 0 zero,
+    seed 413 + B), 2051 selected tokens per sequence in the "uniform" and
+    "short_prefix" index patterns, B in {1, 2, 4, 8}; scopes: the scale-plane
+    gather (gather_scale_plane, both methods name one kernel) and the complete
+    read (read_quantized to BF16). Checked bit-exact against the harness's
+    closed form before timing."""
+    import numpy as np
+    import torch
+
+    from q6moe.attention_cache import gather_scale_plane, read_quantized
+
+    class Cfg:
+        kv_heads, head_dim, cache_group = 2, 256, 32  # kaggle/qwen38_tpu/config.py:24-26, 512 channels
+
+    cap, sel, G = 8192, 2051, 16
+    rows = []
+    for b in (1, 2, 4, 8):
+        rng = np.random.default_rng(413 + b)
+        scale = rng.uniform(0, 0.03, (b * G, cap)).astype(np.float32)
+        scale_t = torch.from_numpy(scale).to(torch.bfloat16)
+        scale_t[:, 0] = 0
+        codes_h = rng.integers(-127, 128, (b, cap, 512), dtype=np.int8)
+        cache = {"k": torch.from_numpy(codes_h).to(dev), "k_scale": scale_t.to(dev)}
+        sb = scale_t.float().numpy()
+        for pattern in ("uniform", "short_prefix"):
+            limit = cap if pattern == "uniform" else 256
+            idx = rng.integers(0, limit, (b, sel), dtype=np.int32)
+            idx[:, :4] = [0, cap - 1, 0, cap // 8]
+            if pattern == "short_prefix":
+                idx[:, 257:] = 0
+            it = torch.from_numpy(idx).to(dev)
+            want_s = np.stack([sb[i * G:(i + 1) * G][:, idx[i]].T for i in range(b)])
+            want_r = (np.stack([codes_h[i, idx[i]] for i in range(b)]).reshape(b, sel, G, 32).astype(np.float32)
+                      * want_s[..., None]).reshape(b, sel, 512)
+            got_s = gather_scale_plane(cache["k_scale"], it, G).float().cpu().numpy()
+            got_r = read_quantized(cache, "k", it, Cfg).reshape(b, sel, 512)
+            want_r_bf = torch.from_numpy(want_r).to(torch.bfloat16)
+            if not (np.array_equal(got_s, want_s) and torch.equal(got_r.cpu().view(torch.int16),
+                                                                  want_r_bf.view(torch.int16))):
+                raise CheckFailed(f"kv harness B={b} {pattern}: result differs from the closed form")
+            bodies = {"scales": lambda _k, it=it: gather_scale_plane(cache["k_scale"], it, G),
+                      "complete_read": lambda _k, it=it: read_quantized(cache, "k", it, Cfg)}
+            dev_us = _graph_per_call(bodies)
+            host_ms = _host_per_call(bodies)
+            nbytes = b * sel * (512 + G * 2 + 4 + 512 * 2)
+            rows.append({"B": b, "pattern": pattern, "selected": sel, "capacity": cap, "check": "bit-exact",
+                         "device_us_per_call": dev_us, "host_ms_per_call": host_ms,
+                         "complete_read_bytes": nbytes,
+                         "complete_read_GBps": round(nbytes / (dev_us["complete_read"] * 1e-6) / 1e9, 1)})
+        del cache
+    return {"workload": "reference_kv_gather_dense_bf16plane_g32_cap8192_sel2051_b1_2_4_8",
+            "timing": "device_us_per_call: replays of captured HIP graphs of 20 calls (the graph holds the "
+                      "wrapper's output allocations); host_ms_per_call: one call plus synchronisation",
+            "cases": rows}
+
+
+def measure_policy(dev):
+    """The expert compute policy gate of kaggle/qwen38_tpu/compute.py:92-160
+    (choose_policy): ``int8_q8`` is selected only if it is at least 10 % faster
+    than ``bf16`` on both a decode and a prompt shape. Timed here as whole MoE
+    steps of an all-Q8_0 layer (the calibrator's "q8" quantization,
+    expert_calibration.py:262) of the headline shape (128 experts, top-8, H 2048,
+    I 768, seed 1) at 8 and 4096 tokens, each policy on its own kernels."""
+    import numpy as np
+    import torch
+
+    from q6moe.experts import expert_parallel, pack_experts
+    from q6moe.synth import moe_layer
+
+    L = moe_layer(seed=1, experts=EXPERTS, top_k=TOP_K, hidden=HIDDEN, intermediate=INTER, tokens=PREFILL_TOKENS,
+                  qtype="Q8_0", pack=False)
+    tabs = [pack_experts(L[n], "Q8_0", INTER if n != "down" else HIDDEN, HIDDEN if n != "down" else INTER, dev)
+            for n in ("gate", "up", "down")]
+    xa = torch.from_numpy(L["x"]).to(dev).to(torch.bfloat16)
+    ida = torch.from_numpy(L["ids"]).to(dev)
+    wa = torch.from_numpy(L["weights"]).to(dev).to(torch.bfloat16)
+    res = {"workload": "moe_q8_0_e128_top8_h2048_i768_seed1", "shapes": {}}
+    for b in (TOKENS, PREFILL_TOKENS):
+        x, ids, w = xa[:b].contiguous(), ida[:b].contiguous(), wa[:b].contiguous()
+        outs, methods = {}, {}
+        for policy in ("bf16", "int8_q8"):
+            fn = expert_parallel(None, gate_type="Q8_0", up_type="Q8_0", down_type="Q8_0", hidden=HIDDEN,
+                                 intermediate=INTER, compute=policy)
+            ws = torch.empty(fn.workspace_bytes(b, TOP_K, EXPERTS), dtype=torch.uint8, device=dev)
+            o = torch.empty((b, HIDDEN), dtype=torch.bfloat16, device=dev)
+            fn(*tabs, x, ids, w, workspace=ws, out=o)
+            check_finite(f"policy {policy} B={b}", o)
+            outs[policy] = o.float().cpu().numpy()
+            methods[policy] = lambda i, fn=fn, ws=ws, o=o: fn(*tabs, x, ids, w, workspace=ws, out=o)
+        t = timed_reps(methods, inner=20 if b == TOKENS else 5)
+        rel = float(np.linalg.norm(outs["int8_q8"] - outs["bf16"]) / max(np.linalg.norm(outs["bf16"]), 1e-12))
+        bf, i8 = t["bf16"]["median"], t["int8_q8"]["median"]
+        res["shapes"][str(b)] = {"bf16_us": bf, "int8_q8_us": i8, "int8_over_bf16": round(i8 / bf, 3),
+                                 "relative_l2_error": round(rel, 5), "accuracy_pass": rel <= 0.012,
+                                 "speed_pass": i8 <= 0.9 * bf}
+    ok = all(v["accuracy_pass"] and v["speed_pass"] for v in res["shapes"].values())
+    res["selected"] = "int8_q8" if ok else "bf16"
+    return res
+
+
+def measure_prefill(dev, steps, warmup, with_cpu, down_qtype="Q6_K"):
+    """Prefill step (routing, gate/up, down, combine) on the seed-2 4096-token layer;
+    ``down_qtype`` "Q8_0" gives the Q6 checkpoint's mix (checkpoints/q6.json)."""
     import numpy as np
     import torch
 
@@ -451,17 +676,19 @@ def measure_prefill(dev, steps, warmup, with_cpu):
     from q6moe.synth import moe_layer
 
     L = moe_layer(seed=PREFILL_SEED, experts=EXPERTS, top_k=TOP_K, hidden=HIDDEN, intermediate=INTER,
-                  tokens=PREFILL_TOKENS, bias_sigma=PREFILL_BIAS, pack=False)
-    tabs = [pack_experts(L[n], "Q6_K", INTER if n != "down" else HIDDEN, HIDDEN if n != "down" else INTER, dev)
-            for n in ("gate", "up", "down")]
+                  tokens=PREFILL_TOKENS, bias_sigma=PREFILL_BIAS, pack=False, down_qtype=down_qtype)
+    types = ("Q6_K", "Q6_K", down_qtype)
+    tabs = [pack_experts(L[n], types[i], INTER if n != "down" else HIDDEN, HIDDEN if n != "down" else INTER, dev)
+            for i, n in enumerate(("gate", "up", "down"))]
     x = torch.from_numpy(L["x"]).to(dev).to(torch.bfloat16)
     ids = torch.from_numpy(L["ids"]).to(dev)
     w = torch.from_numpy(L["weights"]).to(dev).to(torch.bfloat16)
-    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q6_K", hidden=HIDDEN,
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type=down_qtype, hidden=HIDDEN,
                          intermediate=INTER)
     ws = torch.empty(fn.workspace_bytes(PREFILL_TOKENS, TOP_K, EXPERTS), dtype=torch.uint8, device=dev)
     out = torch.empty((PREFILL_TOKENS, HIDDEN), dtype=torch.bfloat16, device=dev)
-    res = {"workload": "moe_prefill_q6k_e128_top8_h2048_i768_t4096_skew0.5_seed2"}
+    res = {"workload": "moe_prefill_q6k_e128_top8_h2048_i768_t4096_skew0.5_seed2" if down_qtype == "Q6_K" else
+           f"moe_prefill_q6k_gateup_{down_qtype.lower()}_down_e128_top8_h2048_i768_t4096_skew0.5_seed2"}
     fn(*tabs, x, ids, w, workspace=ws, out=out)
     got = out.float().cpu().numpy()
     if not np.isfinite(got).all():
@@ -469,7 +696,7 @@ def measure_prefill(dev, steps, warmup, with_cpu):
     if with_cpu:
         rows = np.random.default_rng(7).choice(PREFILL_TOKENS, 1024, replace=False)
         rows.sort()
-        want, secs, n, runs = cpu_oracle_moe(L, rows, ("Q6_K",) * 3, HIDDEN, INTER, min_seconds=8.0)
+        want, secs, n, runs = cpu_oracle_moe(L, rows, types, HIDDEN, INTER, min_seconds=8.0)
         res["check"] = dict(check_close("prefill", got[rows], want), sample_tokens=int(rows.size))
         flops = 2 * rows.size * TOP_K * 3 * HIDDEN * INTER
         res["cpu_baseline"] = {"value": round(flops / secs / 1e12, 6), "unit": "TFLOP/s", "cores": n,
@@ -488,8 +715,10 @@ def measure_prefill(dev, steps, warmup, with_cpu):
         "mfma_fraction": round(tflops / MFMA_PEAK_TFLOPS, 4), "flops_per_step": PREFILL_FLOPS,
         "step_us": t["fused"],
         "phases_us": {k: round(float(v), 1) for k, v in zip(("route", "gate_up", "down", "combine"), ph)},
-        "roofline": roofline("q6moe::moe_pf_gate_up_kernel", "mfma", PREFILL_FLOPS * 2 / 3, ph[1],
+        "roofline": roofline("q6moe::moe_pf_gate_up_kernel<0>", "mfma", PREFILL_FLOPS * 2 / 3, ph[1],
                              work_unit="flops_per_launch"),
+        "down_roofline": roofline(f"q6moe::moe_pf_down_kernel<{PF_FORMAT_ID[down_qtype]}>", "mfma",
+                                  PREFILL_FLOPS / 3, ph[2], work_unit="flops_per_launch"),
     })
     return res
 
@@ -1020,6 +1249,13 @@ def run(args):
                             "hbm_copy": copy_ceiling(dev)}
         log("timing the 512-expert layer of the reference model (seed 5) ...")
         configs["wide_layer"] = measure_wide_layer(dev, with_cpu)
+        log("timing the Q6_K gate/up + Q8_0 down prefill step (4096 tokens, seed 2) ...")
+        configs["prefill_q6_mix"] = measure_prefill(dev, steps=10, warmup=2, with_cpu=with_cpu, down_qtype="Q8_0")
+        log("timing the reference harnesses' own cases (packed-Q6 grid, dense KV gather) ...")
+        configs["reference_harness"] = {"packed_q6_grid": measure_projection_grid(dev, with_cpu),
+                                        "kv_gather": measure_kv_harness(dev)}
+        log("timing the compute policy gate (bf16 against int8_q8) ...")
+        configs["compute_policy"] = measure_policy(dev)
     if "prefill" in configs:
         result["prefill"] = configs["prefill"]
     result["configs"] = configs

@@ -27,6 +27,7 @@ with the raw tensor.
 """
 
 import ctypes
+import warnings
 import weakref
 from dataclasses import dataclass
 from functools import lru_cache
@@ -149,11 +150,15 @@ class _PackCache:
     A view made afresh on every call (``table[layer]`` inside the layer loop)
     is a new object each time and is repacked each time; pass the same
     object, or pack once at load time with ``pack_experts`` /
-    ``ExpertFFN.prepare``.
+    ``ExpertFFN.prepare``. While an entry lives, the raw bytes and the packed
+    copy are both held (at the reference model's size, 512 experts x 4.43 MB
+    per layer): the first repack of a process issues a ResourceWarning that
+    says so.
     """
 
     def __init__(self):
         self.entries = {}
+        self.warned = False  # one ResourceWarning per process for the doubled memory
 
     def get(self, raw, qtype, rows, width, single=False):
         """``single``: ``raw`` is one projection [rows, blocks, bytes], packed as one expert."""
@@ -165,6 +170,13 @@ class _PackCache:
         table = pack_experts(raw.reshape(1, -1) if single else raw, qtype, rows, width, raw.device)
         if hit is None:
             weakref.finalize(raw, self.entries.pop, key, None)
+            if not self.warned:
+                self.warned = True
+                warnings.warn(
+                    f"a raw GGUF expert table ({raw.numel()} bytes) was repacked on the device for this call; the "
+                    "packed copy lives as long as the raw tensor, so the layer's expert memory is held twice. "
+                    "Pack once at load time (ExpertFFN.prepare / pack_experts) and pass the packed tables, "
+                    "or free the raw tensor.", ResourceWarning, stacklevel=4)
         self.entries[key] = (sig, table)
         return table
 

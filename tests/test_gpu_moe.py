@@ -321,6 +321,29 @@ def test_raw_table_cache_follows_the_tensor_not_its_address(device):
     assert not np.array_equal(first, second)
 
 
+def test_raw_table_repack_warns_of_the_doubled_memory(device, monkeypatch):
+    # The first device repack of a raw table in a process warns that the raw
+    # and packed bytes are both held; packed tables never warn.
+    import warnings
+
+    from q6moe import experts as ex
+
+    monkeypatch.setattr(ex._CACHE, "warned", False)
+    L = moe_layer(seed=18, experts=2, top_k=1, hidden=256, intermediate=256, tokens=2, pack=False)
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q6_K", hidden=256, intermediate=256)
+    x = torch.from_numpy(L["x"]).to(device).to(torch.bfloat16)
+    ids = torch.from_numpy(L["ids"]).to(device)
+    w = torch.from_numpy(L["weights"]).to(device).to(torch.bfloat16)
+    raw = [torch.from_numpy(L[n].reshape(2, -1)).to(device) for n in ("gate", "up", "down")]
+    with pytest.warns(ResourceWarning, match="held twice"):
+        fn(*raw, x, ids, w)
+    packed = fn.prepare(*raw, device)
+    monkeypatch.setattr(ex._CACHE, "warned", False)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", ResourceWarning)
+        fn(*packed, x, ids, w)
+
+
 def test_raw_table_cache_packs_each_live_table_once(device, monkeypatch):
     # 48 layers x 3 raw tables: the first pass packs each of the 144 tables,
     # later passes pack nothing.

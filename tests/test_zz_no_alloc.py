@@ -95,3 +95,47 @@ def test_noalloc_rejects_calls_beyond_the_scratch(device):
     assert rc == -1
     assert b"takes no workspace" in _lib.load().q6moe_last_error()
     del keep
+
+
+@pytest.mark.parametrize("case", ["decode", "grouped"])
+def test_noalloc_call_replays_in_a_captured_graph(device, case):
+    # The entry point captured once in a HIP graph (after a first eager call on
+    # the device), then replayed with new inputs written in place into the
+    # captured x / ids / weights, with eager work of the program between the
+    # replays: each replay must equal q6moe_moe_forward on the same inputs bit
+    # for bit (decode kernels at 8 tokens; grouped kernels at 200 tokens).
+    if case == "decode":
+        E, H, I, B, mode = 128, 2048, 768, 8, 0
+        L = moe_layer(seed=1, tokens=4 * B, pack=False)
+    else:
+        E, H, I, B, mode = 16, 512, 256, 200, 2
+        L = moe_layer(seed=64, experts=E, top_k=4, hidden=H, intermediate=I, tokens=4 * B, pack=False)
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q6_K", hidden=H,
+                         intermediate=I).with_mode(mode)
+    tabs = fn.prepare(*(L[n].reshape(E, -1) for n in ("gate", "up", "down")), device)
+    x, ids, w = (t.clone() for t in _inputs(L, device, B))
+    args, out, keep = fn.args(*tabs, x, ids, w, with_workspace=False)
+    call = _noalloc()
+    with torch.cuda.device(device):
+        assert call(ctypes.byref(args), _lib.stream_handle(device)) == 0  # first use on this device
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.graph(g, stream=s):
+        rc = call(ctypes.byref(args), _lib.stream_handle(device))
+    torch.cuda.current_stream(device).wait_stream(s)
+    assert rc == 0
+    for r in range(1, 4):
+        xs, ids_s, ws_ = _inputs(L, device, 4 * B)
+        x.copy_(xs[r * B:(r + 1) * B])
+        ids.copy_(ids_s[r * B:(r + 1) * B])
+        w.copy_(ws_[r * B:(r + 1) * B])
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.view(torch.int16).cpu().numpy()
+        want = fn(*tabs, x, ids, w).view(torch.int16).cpu().numpy()  # eager, with a workspace
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got, want)
+        assert not np.array_equal(got, np.zeros_like(got))
+    del keep
