@@ -611,7 +611,8 @@ __global__ void __launch_bounds__(64)
 // ---------------------------------------------------------------------------
 struct WsLayout {
   size_t hdr, active, act_off, tile, ent_r, route_tok, route_w, tok_pos, act,
-      y, sh_act, sh_y, sh_gate, xq, xq_s, aq, aq_s, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, chunk_cnt, total;
+      y, sh_act, sh_y, sh_gate, xq, xq_s, aq, aq_s, slot_e, slot_t0, slot_cnt, tok_n, route_dst, contrib, chunk_cnt,
+      flags, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -644,6 +645,7 @@ static WsLayout ws_layout(int64_t B, int64_t K, int64_t E, int64_t H, int64_t I,
     L.tok_n = take(4 * B);
     L.route_dst = take(4 * n);
     L.contrib = take(4 * n * H);
+    L.flags = take(8 * std::min(E, n) * cdiv(I, 16));  // the fused kernel's per-(slot, row group) tags
   } else {
     L.active = take(4 * E);
     L.act_off = take(4 * (E + 1));
@@ -1330,6 +1332,7 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
     D.max_slots = (int)(E < B * K ? E : B * K);
     D.act = ws.act;
     D.contrib = reinterpret_cast<float*>(w + L.contrib);
+    D.flags = reinterpret_cast<uint64_t*>(w + L.flags);
     D.sh_y = ws.sh_y;
     D.sh_scale = sh_scale;
     D.out = a->out;

@@ -144,7 +144,7 @@ struct DecRoute {
 };
 
 struct DecTables {
-  int* hdr;          // [0] active experts, [1] routes
+  int* hdr;          // [0] active experts, [1] routes, [8] call counter, [9] wait gave up (fused kernel)
   int* slot_e;       // [E] expert of slot
   int* slot_t0;      // [E] first route position
   int* slot_cnt;     // [E] routes
@@ -173,6 +173,7 @@ struct DecArgs {
   int H, I, max_slots;
   uint16_t* act;
   float* contrib;  // [B*K, H] FP32 f32(y) * f32(r), token-major
+  uint64_t* flags; // [max_slots, I/16] per-call tags of the fused decode kernel (NULL: separate launches)
   const uint16_t* sh_y;
   const uint16_t* sh_scale;
   uint16_t* out;

@@ -112,6 +112,31 @@ def test_decode_workload_full_size(device):
     np.testing.assert_array_equal(got, again)
 
 
+def test_one_launch_decode_on_a_reused_workspace(device):
+    # Routes spread thin (512 experts, top-10, 8 tokens: 80 routes) take the
+    # one-launch decode kernel, whose down items wait on per-call flags in the
+    # workspace. Consecutive calls on one workspace, with new inputs each time,
+    # and a workspace whose bytes start as zeros or all ones, must all give the
+    # oracle's values; a repeat call is bitwise identical.
+    L = moe_layer(seed=66, experts=512, top_k=10, hidden=512, intermediate=256, tokens=40, pack=False)
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q6_K", hidden=512,
+                         intermediate=256).with_mode(1)
+    tabs = fn.prepare(*(L[n].reshape(512, -1) for n in ("gate", "up", "down")), device)
+    need = fn.workspace_bytes(8, 10, 512)
+    for fill in (0, 255):
+        ws = torch.full((need,), fill, dtype=torch.uint8, device=device)
+        for r in range(5):
+            rows = slice(8 * r, 8 * r + 8)
+            x = torch.from_numpy(L["x"][rows]).to(device).to(torch.bfloat16)
+            ids = torch.from_numpy(L["ids"][rows]).to(device)
+            w = torch.from_numpy(L["weights"][rows]).to(device).to(torch.bfloat16)
+            got = fn(*tabs, x, ids, w, workspace=ws).float().cpu().numpy()
+            want = oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"][rows], L["ids"][rows],
+                                         L["weights"][rows], types=("Q6_K",) * 3, hidden=512, intermediate=256)
+            assert_moe_close(got, want)
+            np.testing.assert_array_equal(got, fn(*tabs, x, ids, w, workspace=ws).float().cpu().numpy())
+
+
 def test_duplicate_routes_sum_and_zero_rows_are_exact_zero(device):
     L = moe_layer(seed=9, experts=6, top_k=3, hidden=256, intermediate=256, tokens=9, pack=False)
     ids = L["ids"].copy()

@@ -97,7 +97,7 @@ def test_noalloc_rejects_calls_beyond_the_scratch(device):
     del keep
 
 
-@pytest.mark.parametrize("case", ["decode", "grouped"])
+@pytest.mark.parametrize("case", ["decode", "grouped", "thin"])
 def test_noalloc_call_replays_in_a_captured_graph(device, case):
     # The entry point captured once in a HIP graph (after a first eager call on
     # the device), then replayed with new inputs written in place into the
@@ -107,6 +107,9 @@ def test_noalloc_call_replays_in_a_captured_graph(device, case):
     if case == "decode":
         E, H, I, B, mode = 128, 2048, 768, 8, 0
         L = moe_layer(seed=1, tokens=4 * B, pack=False)
+    elif case == "thin":  # 512 experts, top-10, 8 tokens: the one-launch decode kernel and its call counter
+        E, H, I, B, mode = 512, 512, 256, 8, 0
+        L = moe_layer(seed=65, experts=E, top_k=10, hidden=H, intermediate=I, tokens=4 * B, pack=False)
     else:
         E, H, I, B, mode = 16, 512, 256, 200, 2
         L = moe_layer(seed=64, experts=E, top_k=4, hidden=H, intermediate=I, tokens=4 * B, pack=False)
