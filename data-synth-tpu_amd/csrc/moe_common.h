@@ -100,6 +100,12 @@ struct Proj {
   int rows, k, kb;
 };
 
+// The K block whose second half lies wholly past the matrix (k % 256 in
+// (0, 128]), or -1: in 32-value formats its units hold only zero padding there.
+__host__ __device__ __forceinline__ int half_block(const Proj& p) {
+  return p.k % 256 != 0 && p.k % 256 <= 128 ? p.kb - 1 : -1;
+}
+
 template <int FMT>
 __device__ __forceinline__ const uint8_t* unit_ptr(const Proj& p, int64_t e, int rgroup, int kb) {
   return p.data + e * p.dstride + ((int64_t)rgroup * p.kb + kb) * UnitBytes<FMT>::value;

@@ -220,21 +220,27 @@ template <>
 struct WStream<FMT_Q8> {
   static constexpr int kDma = 5;
   const uint8_t* data;
-  int kbs;
+  int kbs, hk;
   uint32_t v16, v4;
   __device__ __forceinline__ WStream(const Proj& p, int64_t e, int lane) {
     data = p.data + e * p.dstride;
     kbs = p.kb;
+    hk = half_block(p);
     v16 = opaque(16 * lane);
     v4 = opaque(4 * lane);
   }
-  // unit: four 1 KB code chunks and the 256 B of scales, copied as they lie
+  // unit: four 1 KB code chunks and the 256 B of scales, copied as they lie;
+  // in a K block whose second half lies past the matrix (K block hk), code
+  // chunks 2 and 3 hold only zero padding, so their DMA re-reads chunks 0 and
+  // 1 (cache hits) instead: those positions meet zeroed token operands and
+  // zero scales.
   __device__ __forceinline__ void issue(int rg, int kb, uint8_t* st) const {
     const uint8_t* u = data + ((int64_t)rg * kbs + kb) * kQ8Unit;
+    const int o2 = kb == hk ? 0 : 2048;
     dma16(u, v16, st);
     dma16(u + 1024, v16, st + 1024);
-    dma16(u + 2048, v16, st + 2048);
-    dma16(u + 3072, v16, st + 3072);
+    dma16(u + o2, v16, st + 2048);
+    dma16(u + o2 + 1024, v16, st + 3072);
     dma4(u + 4096, v4, st + 4096);
   }
   static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {
@@ -284,18 +290,21 @@ template <>
 struct WStream<FMT_Q51> {
   static constexpr int kDma = 3;
   const uint8_t* data;
-  int kbs;
+  int kbs, hk;
   uint32_t v16;
   __device__ __forceinline__ WStream(const Proj& p, int64_t e, int lane) {
     data = p.data + e * p.dstride;
     kbs = p.kb;
+    hk = half_block(p);
     v16 = opaque(16 * lane);
   }
-  // unit: three 1 KB runs, copied as they lie
+  // unit: three 1 KB runs, copied as they lie; in K block hk (second half past
+  // the matrix) the nibble run of blocks 4-7 holds only padding and re-reads
+  // the first run instead (zero scales there)
   __device__ __forceinline__ void issue(int rg, int kb, uint8_t* st) const {
     const uint8_t* u = data + ((int64_t)rg * kbs + kb) * kQ51Unit;
     dma16(u, v16, st);
-    dma16(u + 1024, v16, st + 1024);
+    dma16(u + (kb == hk ? 0 : 1024), v16, st + 1024);
     dma16(u + 2048, v16, st + 2048);
   }
   static __device__ __forceinline__ void decode(const uint8_t* st, int lane, u32x4 a[8]) {

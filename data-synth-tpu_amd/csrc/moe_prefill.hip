@@ -84,7 +84,9 @@ __device__ __forceinline__ void wait_vm() {
 
 // The weights of one unit (a whole K block) in the registers of the lane that
 // decodes them (row j = lane % 16, k-group jA = lane / 16); both K halves
-// decode from one load. ``load`` issues kLoads vector-memory instructions;
+// decode from one load. ``load`` issues kLoads vector-memory instructions
+// (``half``: only the first K half is used, and a 32-value format re-reads
+// its first half's code words for the second instead of the zero padding);
 // ``half(h)`` gives the 4 A fragments of K half h; ``gran(f, jA)`` is the
 // 8-column granule, within the half, of fragment f for k-group jA (the token
 // operand it pairs with); ``pin`` makes the registers opaque to the compiler.
@@ -99,7 +101,7 @@ struct Block<FMT_Q6> {
   static constexpr int kLoads = 5;
   u32x4 c0, c1, c2;
   uint32_t sc, d;
-  __device__ __forceinline__ void load(const uint8_t* v, int lane) {
+  __device__ __forceinline__ void load(const uint8_t* v, int lane, bool = false) {
     c0 = *reinterpret_cast<const u32x4*>(v + 16 * lane);
     c1 = *reinterpret_cast<const u32x4*>(v + 1024 + 16 * lane);
     c2 = *reinterpret_cast<const u32x4*>(v + 2048 + 16 * lane);
@@ -125,9 +127,10 @@ struct Block<FMT_Q8> {
   static constexpr int kLoads = 5;
   u32x4 c[4];
   u32x2 dw;
-  __device__ __forceinline__ void load(const uint8_t* v, int lane) {
+  __device__ __forceinline__ void load(const uint8_t* v, int lane, bool half = false) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) c[g] = *reinterpret_cast<const u32x4*>(v + 1024 * g + 16 * lane);
+    for (int g = 0; g < 4; ++g)
+      c[g] = *reinterpret_cast<const u32x4*>(v + 1024 * (half ? g & 1 : g) + 16 * lane);
     dw = *reinterpret_cast<const u32x2*>(v + 4096 + 8 * (2 * (lane & 15) + (lane >> 5)));
   }
   __device__ __forceinline__ void pin() { asm volatile("" : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(dw)); }
@@ -152,10 +155,11 @@ struct Block<FMT_Q51> {
   static constexpr int kLoads = 6;
   u32x4 q[4];
   u32x4 aux[2];  // blocks 2g + jA/2 of g = 0, 1 and of g = 2, 3: (high word, d | m << 16)
-  __device__ __forceinline__ void load(const uint8_t* v, int lane) {
+  __device__ __forceinline__ void load(const uint8_t* v, int lane, bool half = false) {
     const int j = lane & 15, hb = lane >> 5;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) q[g] = *reinterpret_cast<const u32x4*>(v + 512 * g + 256 * hb + 16 * j);
+    for (int g = 0; g < 4; ++g)
+      q[g] = *reinterpret_cast<const u32x4*>(v + 512 * (half ? g & 1 : g) + 256 * hb + 16 * j);
     aux[0] = *reinterpret_cast<const u32x4*>(v + 2048 + 64 * j + 32 * hb);
     aux[1] = *reinterpret_cast<const u32x4*>(v + 2048 + 64 * j + 32 * hb + 16);
   }
@@ -196,7 +200,7 @@ struct Block<FMT_Q4K> {
   static constexpr int kLoads = 5;
   u32x4 hdr;
   u32x4 qs[2][2];  // [half][chunk]
-  __device__ __forceinline__ void load(const uint8_t* v, int lane) {
+  __device__ __forceinline__ void load(const uint8_t* v, int lane, bool = false) {
     const int j = lane & 15, jA = lane >> 4;
     hdr = *reinterpret_cast<const u32x4*>(v + 16 * j);
 #pragma unroll
@@ -351,7 +355,9 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
 #pragma unroll
       for (int i = i0; i < i0 + per; ++i) bdma16(xr, xoff[i], (uint32_t)(kb * kQK + h * 128) * 2u, xs + i * 1024);
     } else if constexpr (slot == 1 && part - 2 < kUnits) {
-      if (kb + 1 < kbs) wr[wset][part - 2].load(units[part - 2] + ((int64_t)rgs[part - 2] * kbs + kb + 1) * kUB, lane);
+      if (kb + 1 < kbs)
+        wr[wset][part - 2].load(units[part - 2] + ((int64_t)rgs[part - 2] * kbs + kb + 1) * kUB, lane,
+                                kb + 2 == kbs && (S & 1));
     }
   };
   auto step = [&](int s, auto slot_c, auto set_c) {
@@ -396,7 +402,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     int rows[NCG];
     tile_rows(rows, row_of);
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) wr[0][u].load(units[u] + (int64_t)rgs[u] * kbs * kUB, lane);
+    for (int u = 0; u < kUnits; ++u) wr[0][u].load(units[u] + (int64_t)rgs[u] * kbs * kUB, lane, S == 1);
     asm volatile("" ::: "memory");  // every load above issues before the offsets wait on the rows
     x_offsets(xoff, rows, K);
   }
