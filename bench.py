@@ -447,7 +447,8 @@ def measure_projection(dev, with_cpu):
         "cold_GBps": round(nbytes / (cold * 1e-6) / 1e9, 1), "bytes_per_call": nbytes, "cold_copies": copies,
         "timing": "device time per call from replays of captured HIP graphs",
         "methods_us_per_call": per_call,
-        "roofline": roofline("q6moe::q6_skinny_kernel<1>", "hbm", nbytes, cold, work_unit="bytes_per_launch"),
+        "roofline": roofline("q6moe::q6_skinny_kernel<1>", "hbm", nbytes, cold, work_unit="bytes_per_launch",
+                             tag="single projection"),
     })
     res["roofline"]["note"] = "cold calls: 640 distinct weight copies (826 MB) in rotation"
     return res
@@ -716,9 +717,9 @@ def measure_prefill(dev, steps, warmup, with_cpu, down_qtype="Q6_K"):
         "step_us": t["fused"],
         "phases_us": {k: round(float(v), 1) for k, v in zip(("route", "gate_up", "down", "combine"), ph)},
         "roofline": roofline("q6moe::moe_pf_gate_up_kernel<0>", "mfma", PREFILL_FLOPS * 2 / 3, ph[1],
-                             work_unit="flops_per_launch"),
+                             work_unit="flops_per_launch", tag="4096 tokens"),
         "down_roofline": roofline(f"q6moe::moe_pf_down_kernel<{PF_FORMAT_ID[down_qtype]}>", "mfma",
-                                  PREFILL_FLOPS / 3, ph[2], work_unit="flops_per_launch"),
+                                  PREFILL_FLOPS / 3, ph[2], work_unit="flops_per_launch", tag="4096 tokens"),
     })
     return res
 
@@ -900,13 +901,22 @@ def measure_wide_layer(dev, with_cpu):
         us = t["fused"]["median"]
         ph = phase_means(call, 50)
         gu_bytes = active * 2 * WIDE_GATE_BYTES + b * WIDE_H * 2 + routes * WIDE_I * 2
+        # Routes spread thin (5 B K < 2 E) with one wave per item in both
+        # projections run gate/up and down in one launch (the library's rule
+        # for the decode kernels; at 8 tokens both launches have ~3 200 items),
+        # whose span the gate/up phase then measures: its bytes are the whole
+        # step's but the combine's.
+        fused = 5 * b * WIDE_K < 2 * WIDE_E and b >= 8
+        kernel = "q6moe::moe_dec_fused_kernel<0, 2, false>" if fused else "q6moe::moe_dec_gate_up_kernel<0, false>"
+        if fused:
+            gu_bytes += active * WIDE_DOWN_BYTES + routes * WIDE_H * 4
         row.update({"us_per_step": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
                     "tokens_per_s": round(b / (us * 1e-6), 1),
                     "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "step_us": t["fused"],
                     "phases_us": {k: round(float(v), 2) for k, v in zip(("pre", "gate_up", "down", "combine"), ph)},
                     "active_experts": active, "bytes_per_step": nbytes, "layer_copies": copies,
-                    "roofline": roofline("q6moe::moe_dec_gate_up_kernel<0, false>", "hbm", gu_bytes, ph[1],
-                                         work_unit="bytes_per_launch", tag=f"wide {b} token")})
+                    "roofline": roofline(kernel, "hbm", gu_bytes, ph[1], work_unit="bytes_per_launch",
+                                         tag=f"wide {b} token")})
         out["decode"][str(b)] = row
     del layers[1:]
     # prefill: all 2048 tokens on the grouped kernels
@@ -1013,7 +1023,7 @@ def measure_kv(dev, with_cpu):
                 "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes,
                 "call_us": t["fused"],
                 "roofline": roofline("q6moe::kv_read_vec_kernel<unsigned int>", "hbm", per_launch, launch_us,
-                                     work_unit="bytes_per_launch")})
+                                     work_unit="bytes_per_launch", tag="paged KV gather")})
     # fused decode attention over the same cache
     q = torch.from_numpy(K["q"]).to(dev).to(torch.bfloat16)
     lengths = torch.full((B,), T, dtype=torch.int32, device=dev)
@@ -1220,7 +1230,7 @@ def run(args):
         "step_us": reps["fused"],
         "phases_us": {k: round(float(v), 2) for k, v in zip(("pre", "gate_up", "down", "combine"), ph)},
         "roofline": roofline("q6moe::moe_dec_gate_up_kernel<0, true>", "hbm", gu_bytes, ph[1],
-                             work_unit="bytes_per_launch"),
+                             work_unit="bytes_per_launch", tag="headline decode step"),
         "baselines_us_per_step": {k: v for k, v in reps.items() if k != "fused"},
     }
     if check is not None:
