@@ -313,7 +313,9 @@ __device__ __forceinline__ void x_offsets(uint32_t (&xoff)[NCG], const int (&row
 // first-half step, the next block's weights for unit 0 and unit 1), so that
 // the four waves of a workgroup do not all queue their vector-memory
 // instructions at once right after the barrier.
-template <int FMT, int NCG, typename RowFn, typename RowOf>
+// kEven: K is a multiple of 256 (whole K blocks); the loop then runs its
+// steps in pairs with no branch between a block's two halves.
+template <int FMT, int NCG, bool kEven, typename RowFn, typename RowOf>
 __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, const int* unit_proj, RowFn rg_of,
                                           const uint16_t* x, int x_rows, RowOf row_of, int K, int64_t expert,
                                           f32x4 (&acc)[kUnits][NCG]) {
@@ -321,6 +323,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
   const int j = lane & 15, jA = lane >> 4;
   const int S = K / 128;           // K halves (K is a multiple of 128)
   const int kbs = (S + 1) >> 1;    // K blocks of the table, the last one possibly half used
+  const bool odd = !kEven && (S & 1);
   constexpr int kWLoads = Block<FMT>::kLoads;
   constexpr int kUB = UnitBytes<FMT>::value;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
@@ -357,7 +360,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     } else if constexpr (slot == 1 && part - 2 < kUnits) {
       if (kb + 1 < kbs)
         wr[wset][part - 2].load(units[part - 2] + ((int64_t)rgs[part - 2] * kbs + kb + 1) * kUB, lane,
-                                kb + 2 == kbs && (S & 1));
+                                kb + 2 == kbs && odd);
     }
   };
   auto step = [&](int s, auto slot_c, auto set_c) {
@@ -402,7 +405,7 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
     int rows[NCG];
     tile_rows(rows, row_of);
 #pragma unroll
-    for (int u = 0; u < kUnits; ++u) wr[0][u].load(units[u] + (int64_t)rgs[u] * kbs * kUB, lane, S == 1);
+    for (int u = 0; u < kUnits; ++u) wr[0][u].load(units[u] + (int64_t)rgs[u] * kbs * kUB, lane, odd && S == 1);
     asm volatile("" ::: "memory");  // every load above issues before the offsets wait on the rows
     x_offsets(xoff, rows, K);
   }
@@ -411,9 +414,17 @@ __device__ __forceinline__ void pf_stream(uint8_t* smem, const Proj* projs, cons
   });
   for (int s0 = 0; s0 < S; s0 += 4) {
     step(s0, std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
-    if (s0 + 1 < S) step(s0 + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
-    if (s0 + 2 < S) step(s0 + 2, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
-    if (s0 + 3 < S) step(s0 + 3, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    if constexpr (kEven) {
+      step(s0 + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+      if (s0 + 2 < S) {
+        step(s0 + 2, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+        step(s0 + 3, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+      }
+    } else {
+      if (s0 + 1 < S) step(s0 + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+      if (s0 + 2 < S) step(s0 + 2, std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+      if (s0 + 3 < S) step(s0 + 3, std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
+    }
   }
 }
 
@@ -454,9 +465,13 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
       for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pf_stream<FMT, NCG>(smem, projs, unit_proj, [&](int) { return rgb; }, x, tokens,
-                        [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; }, hidden, T.expert,
-                        acc);
+    auto row_of = [&](int t) { return ws.route_tok[T.r0 + (t < T.nv ? t : T.nv - 1)]; };
+    if (hidden % 256 == 0)
+      pf_stream<FMT, NCG, true>(smem, projs, unit_proj, [&](int) { return rgb; }, x, tokens, row_of, hidden,
+                                T.expert, acc);
+    else
+      pf_stream<FMT, NCG, false>(smem, projs, unit_proj, [&](int) { return rgb; }, x, tokens, row_of, hidden,
+                                 T.expert, acc);
     const int row = rgb * 16 + 4 * jA;
 #pragma unroll
     for (int tg = 0; tg < NCG; ++tg) {
@@ -500,8 +515,13 @@ __global__ void __launch_bounds__(64 * pf::kWaves, 2)
     for (int u = 0; u < kUnits; ++u)
 #pragma unroll
       for (int t = 0; t < NCG; ++t) acc[u][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    pf_stream<FMT, NCG>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, routes,
-                        [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); }, inter, T.expert, acc);
+    auto row_of = [&](int t) { return T.r0 + (t < T.nv ? t : T.nv - 1); };
+    if (inter % 256 == 0)
+      pf_stream<FMT, NCG, true>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, routes, row_of, inter,
+                                T.expert, acc);
+    else
+      pf_stream<FMT, NCG, false>(smem, projs, unit_proj, [&](int u) { return rgb + u; }, act, routes, row_of, inter,
+                                 T.expert, acc);
 #pragma unroll
     for (int u = 0; u < kUnits; ++u) {
       const int row = (rgb + u) * 16 + 4 * jA;
