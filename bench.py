@@ -849,9 +849,10 @@ def measure_wide_layer(dev, with_cpu):
     """The reference model's MoE layer (kaggle/qwen38_tpu/config.py:13-19: 512
     experts, top-10, hidden 2560, intermediate 640) in its Q6 checkpoint's formats
     (checkpoints/q6.json: Q6_K gate/up, Q8_0 down), weights N(0, 0.02) per expert,
-    seed 5: decode steps of 1, 8 and 64 tokens (the first rows of the 2048-token
-    layer) and the 2048-token prefill step. Layer copies rotate so that one
-    rotation's active bytes exceed 3x the Infinity Cache."""
+    seed 5: steps of 1, 8 and 64 tokens (the first rows of the 2048-token layer)
+    on the operator's default kernel family (decode-step kernels at 1 and 8
+    tokens, grouped at 64) and the 2048-token prefill step. Layer copies rotate
+    so that one rotation's active bytes exceed 3x the Infinity Cache."""
     import numpy as np
     import torch
 
@@ -878,7 +879,10 @@ def measure_wide_layer(dev, with_cpu):
         while len(layers) < copies:
             layers.append(clone_tables(base))
         x, ids, w = xa[:b].contiguous(), ida[:b].contiguous(), wa[:b].contiguous()
-        f = fn.with_mode(1)
+        # the operator's default family (mode 0): the decode-step kernels, or
+        # the grouped ones once tokens x top-k x experts reaches 2^17
+        f = fn
+        family = "grouped" if b * WIDE_K * WIDE_E >= 1 << 17 else "decode"
         ws = torch.empty(f.workspace_bytes(b, WIDE_K, WIDE_E), dtype=torch.uint8, device=dev)
         o = torch.empty((b, WIDE_H), dtype=torch.bfloat16, device=dev)
 
@@ -906,8 +910,9 @@ def measure_wide_layer(dev, with_cpu):
         # for the decode kernels; at 8 tokens both launches have ~3 200 items),
         # whose span the gate/up phase then measures: its bytes are the whole
         # step's but the combine's.
-        fused = 5 * b * WIDE_K < 2 * WIDE_E and b >= 8
-        kernel = "q6moe::moe_dec_fused_kernel<0, 2, false>" if fused else "q6moe::moe_dec_gate_up_kernel<0, false>"
+        fused = family == "decode" and 5 * b * WIDE_K < 2 * WIDE_E and b >= 8
+        kernel = ("q6moe::moe_pf_gate_up_kernel<0>" if family == "grouped" else
+                  "q6moe::moe_dec_fused_kernel<0, 2, false>" if fused else "q6moe::moe_dec_gate_up_kernel<0, false>")
         if fused:
             gu_bytes += active * WIDE_DOWN_BYTES + routes * WIDE_H * 4
         row.update({"us_per_step": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
@@ -915,6 +920,7 @@ def measure_wide_layer(dev, with_cpu):
                     "hbm_fraction": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "step_us": t["fused"],
                     "phases_us": {k: round(float(v), 2) for k, v in zip(("pre", "gate_up", "down", "combine"), ph)},
                     "active_experts": active, "bytes_per_step": nbytes, "layer_copies": copies,
+                    "kernels": family + (" (gate/up and down in one launch)" if fused else ""),
                     "roofline": roofline(kernel, "hbm", gu_bytes, ph[1], work_unit="bytes_per_launch",
                                          tag=f"wide {b} token")})
         out["decode"][str(b)] = row

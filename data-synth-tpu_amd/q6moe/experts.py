@@ -242,8 +242,9 @@ class ExpertFFN:
 
     ``expert_parallel`` caches its result, so one object serves every caller
     with the same configuration; it holds no per-call state. ``mode`` picks the
-    kernel family: 0 (the default) the decode-step kernels up to 64 tokens and
-    the grouped ones above, 1 always the decode-step kernels, 2 always the
+    kernel family: 0 (the default) the decode-step kernels up to 64 tokens
+    (without a shared expert, only while tokens x top-k x experts < 2^17) and
+    the grouped ones otherwise, 1 always the decode-step kernels, 2 always the
     grouped kernels. ``with_mode`` returns a copy that runs another family.
     """
 

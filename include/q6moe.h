@@ -179,8 +179,8 @@ typedef struct q6moe_moe_args {
   uint16_t* out;               /* BF16 [B, H] */
   void* workspace;             /* >= q6moe_moe_workspace_size(...) bytes, 256-byte aligned */
   size_t workspace_bytes;
-  /* kernel family: 0 the decode-step kernels up to 64 tokens where they apply, else the
-     grouped ones; 1 the decode-step kernels (B <= 256, B*top_k <= 1024, E <= 1024 and
+  /* kernel family: 0 the decode-step kernels up to 64 tokens where they apply (and, without
+     a shared expert, tokens*top_k*E < 2^17), else the grouped ones; 1 the decode-step kernels (B <= 256, B*top_k <= 1024, E <= 1024 and
      B*top_k*max(H, I, Is) < 2^30, else Q6MOE_ERR_INVALID); 2 the grouped-GEMM (prefill)
      kernels, tiled on the matrix cores for Q6_K with H and I multiples of 256 */
   int mode;

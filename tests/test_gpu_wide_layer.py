@@ -69,6 +69,20 @@ def test_wide_layer_grouped_kernels_64_tokens(device, wide):
     assert_moe_close(got, _oracle(L, np.arange(64)))
 
 
+@pytest.mark.parametrize("tokens", [16, 32, 64])
+def test_wide_layer_default_family_matches_both(device, wide, tokens):
+    # mode 0 takes the decode-step kernels at 16 tokens and the grouped ones
+    # at 32 and 64 (tokens x top-10 x 512 experts >= 2^17); both families
+    # round at the same points and sum in the same order, so all three agree
+    # bitwise, and the oracle checks the result
+    L, fn, tabs, d = wide
+    args = (d["x"][:tokens], d["ids"][:tokens], d["w"][:tokens])
+    outs = [fn.with_mode(m)(*tabs, *args).float().cpu().numpy() for m in (0, 1, 2)]
+    np.testing.assert_array_equal(outs[0], outs[1])
+    np.testing.assert_array_equal(outs[0], outs[2])
+    assert_moe_close(outs[0], _oracle(L, np.arange(tokens)))
+
+
 def test_wide_layer_prefill_2048_tokens_sampled(device, wide):
     L, fn, tabs, d = wide
     f = fn.with_mode(0)  # 2048 tokens: the grouped kernels
