@@ -29,7 +29,7 @@ def _max_rel(got, want):
 
 
 def assert_moe_close(got, want, exact_frac=0.9, ref_gate=True):
-    """BASELINE's gate (max relative error 1e-2, >= 90 % bit-identical) and, with
+    """The MoE gate (max relative error 1e-2, >= 90 % bit-identical) and, with
     ``ref_gate``, the reference's own routed-FFN tolerance atol = rtol = 3e-3
     (kaggle/qwen38_tpu/routing_validation.py:90,105)."""
     assert np.isfinite(got).all()

@@ -15,7 +15,7 @@ seed 5), x N(0, 1), router logits N(0, 1) -> softmax -> top-10 -> BF16.
   x N(0, 0.3), weights 1/10 with the last row zeroed, "spread" and "hot"
   routes, at its row counts 1 to 512.
 
-Tolerance: BASELINE's (max relative error 1e-2, >= 90 % bit-identical) and
+Tolerance: the MoE gate (max relative error 1e-2, >= 90 % bit-identical) and
 the reference's routed-FFN gate atol = rtol = 3e-3 (routing_validation.py:90),
 as in test_gpu_moe.py; repeat runs are bitwise identical.
 """

@@ -15,7 +15,7 @@ routed-FFN gate restated.
   expected values (per-expert NumPy loop, FP32 matmuls) and its tolerance
   atol = rtol = 3e-3, zero rows exactly zero.
 
-MoE tolerance elsewhere: BASELINE's max relative error 1e-2 and >= 90 % of
+MoE tolerance elsewhere: max relative error 1e-2 and >= 90 % of
 outputs bit-identical (see test_gpu_moe.py), plus the reference's
 atol = rtol = 3e-3 where it holds.
 """
@@ -77,7 +77,7 @@ def test_q4k_shared_layer_full_shape(device, q4_layer, tokens):
     # this shape (4096-wide expert and shared sums, outputs near 1) a differing
     # FP32 summation order flips an intermediate BF16 rounding now and then,
     # which moves an output by a few BF16 steps (2^-7 each near 1). So:
-    # BASELINE's gate, and >= 99.9 % of outputs within the reference's 3e-3.
+    # the MoE gate, and >= 99.9 % of outputs within the reference's 3e-3.
     assert_moe_close(got, want, ref_gate=False)
     within = np.abs(got - want) <= 3e-3 + 3e-3 * np.abs(want)
     assert within.mean() >= 0.999
