@@ -57,24 +57,12 @@ __device__ __forceinline__ void stage_chunk2(DA* da, const SA* __restrict__ sa, 
   }
 }
 
-// Routing, pass 1 (one workgroup per chunk of kChunk tokens, one lane per
-// token): merged BF16 weight of each first occurrence of an id in a token
-// (experts.py:66-73; 0 for repeats and out-of-range ids) and the chunk's
-// route count per expert.
-__global__ void __launch_bounds__(kChunk)
-    moe_route_count_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B, int K,
-                           int E, MoeWs ws, int* __restrict__ chunk_cnt) {
-  extern __shared__ int sm[];
-  int* s_ids = sm;                                            // [kChunk * K]
-  float* s_w = reinterpret_cast<float*>(sm + kChunk * K);     // [kChunk * K] weights, then merged weights
-  __shared__ int cnt[kMaxExperts];
-  const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
-  const int nb = B - b0 < kChunk ? B - b0 : kChunk;
-  const int64_t e0 = (int64_t)b0 * K;
-  for (int e = tid; e < E; e += kChunk) cnt[e] = 0;
-  stage_chunk2(s_ids, ids + e0, [](int v) { return v; }, s_w, wts + e0, [](uint16_t v) { return bf16_to_float(v); },
-               nb * K);
-  __syncthreads();
+// Merged BF16 weight of each first occurrence of an id in a token
+// (experts.py:66-73; 0 for repeats and out-of-range ids), in place of the
+// staged weights s_w, and the per-expert route counts cnt, for the nb staged
+// tokens of a chunk (lane tid = token tid).
+__device__ __forceinline__ void route_merge(const int* s_ids, float* s_w, int* cnt, int nb, int K, int E) {
+  const int tid = threadIdx.x;
   if (tid < nb && K <= 8) {
     // top_k <= 8: the token's entries in registers, every loop unrolled (the
     // same comparisons and the same summation order as below)
@@ -122,38 +110,40 @@ __global__ void __launch_bounds__(kChunk)
       w[kk] = is_route(m) ? m : 0.f;
     }
   }
+}
+
+// Routing, pass 1 (one workgroup per chunk of kChunk tokens, one lane per
+// token): merged BF16 weight of each first occurrence of an id in a token
+// (experts.py:66-73; 0 for repeats and out-of-range ids) and the chunk's
+// route count per expert.
+__global__ void __launch_bounds__(kChunk)
+    moe_route_count_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B, int K,
+                           int E, MoeWs ws, int* __restrict__ chunk_cnt) {
+  extern __shared__ int sm[];
+  int* s_ids = sm;                                            // [kChunk * K]
+  float* s_w = reinterpret_cast<float*>(sm + kChunk * K);     // [kChunk * K] weights, then merged weights
+  __shared__ int cnt[kMaxExperts];
+  const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
+  const int nb = B - b0 < kChunk ? B - b0 : kChunk;
+  const int64_t e0 = (int64_t)b0 * K;
+  for (int e = tid; e < E; e += kChunk) cnt[e] = 0;
+  stage_chunk2(s_ids, ids + e0, [](int v) { return v; }, s_w, wts + e0, [](uint16_t v) { return bf16_to_float(v); },
+               nb * K);
+  __syncthreads();
+  route_merge(s_ids, s_w, cnt, nb, K, E);
   __syncthreads();
   for (int i = tid; i < nb * K; i += kChunk) ws.ent_r[e0 + i] = s_w[i];
   for (int e = tid; e < E; e += kChunk) chunk_cnt[(int64_t)blockIdx.x * E + e] = cnt[e];
 }
 
-// Routing, pass 2 (one workgroup of E lanes rounded up to whole waves, one
-// lane per expert): active experts in ascending id (experts.py:74-76), each
-// expert's first route position, the 128-route prefill tiles, each chunk's
-// first position per expert relative to the expert's first (chunk_cnt is
-// rewritten in place) and, in row nchunks of chunk_cnt, each expert's first
-// position.
-__global__ void __launch_bounds__(kMaxExperts)
-    moe_route_scan_kernel(int E, int nchunks, int mtile, MoeWs ws, int* __restrict__ chunk_cnt) {
-  __shared__ int s_wt[3][kMaxExperts / 64];  // per-wave totals of the three scans
-  const int e = threadIdx.x, lane = e & 63, wv = e >> 6;
-  int total = 0;
-  if (e < E) {
-    for (int c0 = 0; c0 < nchunks; c0 += 8) {
-      int v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int c = c0 + u < nchunks ? c0 + u : nchunks - 1;
-        v[u] = chunk_cnt[(int64_t)c * E + e];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (c0 + u < nchunks) {
-          chunk_cnt[(int64_t)(c0 + u) * E + e] = total;
-          total += v[u];
-        }
-    }
-  }
+// Scans over experts (lane e = expert e, whole waves of the workgroup; lanes
+// from E on carry nothing): active experts in ascending id (experts.py:74-76)
+// into ws.active, their first route positions (returned, and in ws.act_off),
+// the prefill tiles of mtile routes, and the totals in ws.hdr (written by the
+// workgroup's last lane).
+__device__ __forceinline__ int route_scan(int e, int E, int total, int mtile, MoeWs ws,
+                                          int (*s_wt)[kMaxExperts / 64]) {
+  const int lane = e & 63, wv = e >> 6;
   const int act = total > 0, nt = (total + mtile - 1) / mtile;
   // inclusive scans of (active, routes, tiles) in expert order: within each
   // wave by shuffles, then plus the totals of the earlier waves
@@ -180,7 +170,6 @@ __global__ void __launch_bounds__(kMaxExperts)
   }
   const int slot = ia - act, base = ic - total, t0 = it - nt;
   if (e < E) {
-    chunk_cnt[(int64_t)nchunks * E + e] = base;
     if (act) {
       ws.active[slot] = e;
       ws.act_off[slot] = base;
@@ -196,44 +185,48 @@ __global__ void __launch_bounds__(kMaxExperts)
     ws.hdr[1] = ic;
     ws.hdr[2] = it;
   }
+  return base;
 }
 
-// Routing, pass 3 (one workgroup per chunk): a route's position is its
-// expert's first position, plus its chunk's first position within the
-// expert, plus the number of earlier tokens of the chunk routed to that expert
-// (per-expert token bitmaps), so routes are grouped by expert with tokens
-// ascending. Per token, its positions in ascending expert id feed the combine.
-__global__ void __launch_bounds__(kChunk)
-    moe_route_scatter_kernel(const int32_t* __restrict__ ids, int B, int K, int E, int nchunks, MoeWs ws,
-                             const int* __restrict__ chunk_pos) {
-  extern __shared__ int sm[];
-  int* s_ids = sm;                                          // [kChunk * K]
-  float* s_r = reinterpret_cast<float*>(sm + kChunk * K);   // [kChunk * K]
-  int* s_tp = sm + 2 * kChunk * K;                          // [kChunk * K]
-  uint32_t* bits = reinterpret_cast<uint32_t*>(sm + 3 * kChunk * K);  // [E][kChunkWords] token bitmaps
-  int* s_pos = sm + 3 * kChunk * K + E * kChunkWords;       // [E]
-  const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
-  const int nb = B - b0 < kChunk ? B - b0 : kChunk;
-  const int64_t e0 = (int64_t)b0 * K;
-  for (int i = tid; i < E * kChunkWords; i += kChunk) bits[i] = 0u;
-  // experts tid + kChunk * q: their first positions and this chunk's offsets
-  // within them, loaded together with the chunk's entries (indexes past E
-  // repeat expert E - 1; the loads past the first kChunk experts are skipped
-  // for smaller layers)
-  int pe[kExpertsPerLane];
+// Routing, pass 2 (one workgroup of E lanes rounded up to whole waves, one
+// lane per expert): active experts in ascending id (experts.py:74-76), each
+// expert's first route position, the 128-route prefill tiles, each chunk's
+// first position per expert relative to the expert's first (chunk_cnt is
+// rewritten in place) and, in row nchunks of chunk_cnt, each expert's first
+// position.
+__global__ void __launch_bounds__(kMaxExperts)
+    moe_route_scan_kernel(int E, int nchunks, int mtile, MoeWs ws, int* __restrict__ chunk_cnt) {
+  __shared__ int s_wt[3][kMaxExperts / 64];  // per-wave totals of the three scans
+  const int e = threadIdx.x;
+  int total = 0;
+  if (e < E) {
+    for (int c0 = 0; c0 < nchunks; c0 += 8) {
+      int v[8];
 #pragma unroll
-  for (int q = 0; q < kExpertsPerLane; ++q) {
-    pe[q] = 0;
-    if (q == 0 || q * kChunk < E) {
-      const int ec = tid + q * kChunk < E ? tid + q * kChunk : E - 1;
-      pe[q] = chunk_pos[(int64_t)nchunks * E + ec] + chunk_pos[(int64_t)blockIdx.x * E + ec];
+      for (int u = 0; u < 8; ++u) {
+        const int c = c0 + u < nchunks ? c0 + u : nchunks - 1;
+        v[u] = chunk_cnt[(int64_t)c * E + e];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (c0 + u < nchunks) {
+          chunk_cnt[(int64_t)(c0 + u) * E + e] = total;
+          total += v[u];
+        }
     }
   }
-  stage_chunk2(s_ids, ids + e0, [](int v) { return v; }, s_r, ws.ent_r + e0, [](float v) { return v; }, nb * K);
-#pragma unroll
-  for (int q = 0; q < kExpertsPerLane; ++q)
-    if (tid + q * kChunk < E) s_pos[tid + q * kChunk] = pe[q];
-  __syncthreads();
+  const int base = route_scan(e, E, total, mtile, ws, s_wt);
+  if (e < E) chunk_cnt[(int64_t)nchunks * E + e] = base;
+}
+
+// Places a chunk's routes (lane tid = token b0 + tid of the nb staged ones):
+// per-expert token bitmaps give each route its rank among the chunk's tokens
+// of its expert, so its position is s_pos[e] (the expert's first position
+// plus the chunk's offset within it) plus that rank; route_tok and route_w at
+// the position; per token, its positions in ascending expert id into s_tp.
+__device__ __forceinline__ void route_place(const int* s_ids, const float* s_r, int* s_tp, uint32_t* bits,
+                                            const int* s_pos, int nb, int K, int b0, MoeWs ws) {
+  const int tid = threadIdx.x;
   if (tid < nb)
     for (int kk = 0; kk < K; ++kk)
       if (is_route(s_r[tid * K + kk]))
@@ -296,7 +289,76 @@ __global__ void __launch_bounds__(kChunk)
     for (int q = m; q < K; ++q) tp[q] = -1;
   }
   __syncthreads();
+}
+
+// Routing, pass 3 (one workgroup per chunk): a route's position is its
+// expert's first position, plus its chunk's first position within the
+// expert, plus the number of earlier tokens of the chunk routed to that expert
+// (per-expert token bitmaps), so routes are grouped by expert with tokens
+// ascending. Per token, its positions in ascending expert id feed the combine.
+__global__ void __launch_bounds__(kChunk)
+    moe_route_scatter_kernel(const int32_t* __restrict__ ids, int B, int K, int E, int nchunks, MoeWs ws,
+                             const int* __restrict__ chunk_pos) {
+  extern __shared__ int sm[];
+  int* s_ids = sm;                                          // [kChunk * K]
+  float* s_r = reinterpret_cast<float*>(sm + kChunk * K);   // [kChunk * K]
+  int* s_tp = sm + 2 * kChunk * K;                          // [kChunk * K]
+  uint32_t* bits = reinterpret_cast<uint32_t*>(sm + 3 * kChunk * K);  // [E][kChunkWords] token bitmaps
+  int* s_pos = sm + 3 * kChunk * K + E * kChunkWords;       // [E]
+  const int tid = threadIdx.x, b0 = blockIdx.x * kChunk;
+  const int nb = B - b0 < kChunk ? B - b0 : kChunk;
+  const int64_t e0 = (int64_t)b0 * K;
+  for (int i = tid; i < E * kChunkWords; i += kChunk) bits[i] = 0u;
+  // experts tid + kChunk * q: their first positions and this chunk's offsets
+  // within them, loaded together with the chunk's entries (indexes past E
+  // repeat expert E - 1; the loads past the first kChunk experts are skipped
+  // for smaller layers)
+  int pe[kExpertsPerLane];
+#pragma unroll
+  for (int q = 0; q < kExpertsPerLane; ++q) {
+    pe[q] = 0;
+    if (q == 0 || q * kChunk < E) {
+      const int ec = tid + q * kChunk < E ? tid + q * kChunk : E - 1;
+      pe[q] = chunk_pos[(int64_t)nchunks * E + ec] + chunk_pos[(int64_t)blockIdx.x * E + ec];
+    }
+  }
+  stage_chunk2(s_ids, ids + e0, [](int v) { return v; }, s_r, ws.ent_r + e0, [](float v) { return v; }, nb * K);
+#pragma unroll
+  for (int q = 0; q < kExpertsPerLane; ++q)
+    if (tid + q * kChunk < E) s_pos[tid + q * kChunk] = pe[q];
+  __syncthreads();
+  route_place(s_ids, s_r, s_tp, bits, s_pos, nb, K, b0, ws);
   for (int i = tid; i < nb * K; i += kChunk) ws.tok_pos[e0 + i] = s_tp[i];
+}
+
+// Routing of at most kChunk tokens in one launch: the three passes above in
+// one workgroup of max(kChunk, E rounded up to whole waves) lanes, the
+// chunk's counts and positions kept in LDS (its offsets within each expert
+// are 0). Same outputs as the three launches.
+__global__ void __launch_bounds__(kMaxExperts)
+    moe_route_small_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B, int K, int E,
+                           int mtile, MoeWs ws) {
+  extern __shared__ int sm[];
+  int* s_ids = sm;                                                     // [kChunk * K]
+  float* s_w = reinterpret_cast<float*>(sm + kChunk * K);              // [kChunk * K]
+  int* s_tp = sm + 2 * kChunk * K;                                     // [kChunk * K]
+  uint32_t* bits = reinterpret_cast<uint32_t*>(sm + 3 * kChunk * K);   // [E][kChunkWords]
+  int* s_pos = sm + 3 * kChunk * K + E * kChunkWords;                  // [E]
+  int* cnt = s_pos + E;                                                // [E]
+  __shared__ int s_wt[3][kMaxExperts / 64];
+  const int tid = threadIdx.x, n = (int)blockDim.x;
+  for (int e = tid; e < E; e += n) cnt[e] = 0;
+  for (int i = tid; i < E * kChunkWords; i += n) bits[i] = 0u;
+  if (tid < kChunk)
+    stage_chunk2(s_ids, ids, [](int v) { return v; }, s_w, wts, [](uint16_t v) { return bf16_to_float(v); }, B * K);
+  __syncthreads();
+  route_merge(s_ids, s_w, cnt, B, K, E);
+  __syncthreads();
+  const int base = route_scan(tid, E, tid < E ? cnt[tid] : 0, mtile, ws, s_wt);
+  if (tid < E) s_pos[tid] = base;
+  __syncthreads();
+  route_place(s_ids, s_w, s_tp, bits, s_pos, B, K, 0, ws);
+  for (int i = tid; i < B * K; i += n) ws.tok_pos[i] = s_tp[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -1373,15 +1435,24 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
                                 kChunk * 32 * 8);
       (void)hipFuncSetAttribute((const void*)moe_route_scatter_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)scatter_lds(32, kMaxExperts));
+      (void)hipFuncSetAttribute((const void*)moe_route_small_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)(scatter_lds(32, kMaxExperts) + kMaxExperts * 4));
     });
     const int nchunks = (int)cdiv(B, kChunk);
     int* chunk_cnt = reinterpret_cast<int*>(w + L.chunk_cnt);
-    hipLaunchKernelGGL(moe_route_count_kernel, dim3(nchunks), dim3(kChunk), (size_t)kChunk * K * 8, s, a->ids,
-                       a->weights, (int)B, (int)K, (int)E, ws, chunk_cnt);
-    hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3((unsigned)cdiv(E, 64) * 64), 0, s, (int)E, nchunks,
-                       (int)kPrefillTile, ws, chunk_cnt);
-    hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nchunks), dim3(kChunk), scatter_lds(K, E), s, a->ids,
-                       (int)B, (int)K, (int)E, nchunks, ws, chunk_cnt);
+    if (nchunks == 1) {
+      // one chunk: the three passes in one launch (its counts and positions in LDS)
+      const unsigned lanes = (unsigned)std::max<int64_t>(kChunk, cdiv(E, 64) * 64);
+      hipLaunchKernelGGL(moe_route_small_kernel, dim3(1), dim3(lanes), scatter_lds(K, E) + (size_t)E * 4, s, a->ids,
+                         a->weights, (int)B, (int)K, (int)E, (int)kPrefillTile, ws);
+    } else {
+      hipLaunchKernelGGL(moe_route_count_kernel, dim3(nchunks), dim3(kChunk), (size_t)kChunk * K * 8, s, a->ids,
+                         a->weights, (int)B, (int)K, (int)E, ws, chunk_cnt);
+      hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3((unsigned)cdiv(E, 64) * 64), 0, s, (int)E, nchunks,
+                         (int)kPrefillTile, ws, chunk_cnt);
+      hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nchunks), dim3(kChunk), scatter_lds(K, E), s, a->ids,
+                         (int)B, (int)K, (int)E, nchunks, ws, chunk_cnt);
+    }
     if ((rc = check_launch("moe routing kernels"))) return rc;
   }
 
