@@ -15,9 +15,11 @@
 //   1. attn_scores_kernel: per (256-token chunk, KV head, sequence), the
 //      chunk's keys are dequantised into MFMA A operands (16 tokens x 32
 //      channels per v_mfma_f32_16x16x32_bf16) against the group's query
-//      heads as B operand; scores go to the workspace as BF16.
-//   2. attn_stats_kernel: per (sequence, query head), the maximum and the sum
-//      of exp(score - max) over the attended tokens (fixed reduction order).
+//      heads as B operand; scores go to the workspace as BF16, and each
+//      wave's maximum m_w and sum l_w of exp(score - m_w) over its 64 tokens.
+//   2. attn_stats_kernel: per (sequence, query head), the maximum over the
+//      attended tokens, max = max_w m_w, and the sum of exp(score - max),
+//      sum_w l_w exp(m_w - max), in a fixed order.
 //   3. attn_pv_kernel: per chunk, the workgroup forms RNE_bf16(prob) once per
 //      (head, token) in LDS; each wave then runs P.V for its 64 tokens on
 //      MFMA with the dequantised values as A operand (row = 8 channels apart,
@@ -48,6 +50,7 @@ struct AttnParams {
   int64_t pool_pages;
   int pps, page, kvh, hq, r, cap, nchunks;
   uint16_t* s;                       // [B, Hq, cap] BF16 scores
+  float* wstats;                     // [B, Hq, cap / 64, 2]: per 64 tokens, max m_w and sum of exp(score - m_w)
   float* stats;                      // [B, Hq, 2]: max, sum
   float* part;                       // [B, KVH, nchunks, kAttnR, D]
   uint16_t* out;                     // [B, Hq, D]
@@ -105,6 +108,7 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnParams p) {
   // the next block's loads are issued before this block is multiplied
   u32x4 cw[4][2];
   float scw[4];
+  float sv[4][4];  // the lane's scores
   auto load_rb = [&](int rb) {
     const int t = t0 + 16 * rb + col;
     cw[rb][0] = cw[rb][1] = u32x4{0u, 0u, 0u, 0u};
@@ -135,67 +139,60 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnParams p) {
       acc = mfma16(a, qb[ks], acc);
     }
     // lane holds tokens t0 + 16rb + 4g + [0, 4) of query head col
+    const int tt = t0 + 16 * rb + 4 * g;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sv[rb][v] = bf16_round(bf16_round(acc[v]) / kDiv);
     if (col < p.r) {
-      uint32_t o[2];
-#pragma unroll
-      for (int v = 0; v < 4; v += 2) {
-        const float s0 = bf16_round(bf16_round(acc[v]) / kDiv);
-        const float s1 = bf16_round(bf16_round(acc[v + 1]) / kDiv);
-        o[v >> 1] = pack_bf16x2(s0, s1);
-      }
-      const int tt = t0 + 16 * rb + 4 * g;
       uint16_t* dst = p.s + ((int64_t)b * p.hq + kh * p.r + col) * p.cap + tt;
-      *reinterpret_cast<u32x2*>(dst) = u32x2{o[0], o[1]};
+      *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(sv[rb][0], sv[rb][1]), pack_bf16x2(sv[rb][2], sv[rb][3])};
     }
   }
-}
-
-constexpr int kStatsThreads = 1024;
-
-// Max or sum over a kStatsThreads block in a fixed order (tree in LDS).
-__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
-  red[threadIdx.x] = v;
-  __syncthreads();
-  for (int off = kStatsThreads / 2; off > 0; off >>= 1) {
-    if ((int)threadIdx.x < off) {
-      const float a = red[threadIdx.x], c = red[threadIdx.x + off];
-      red[threadIdx.x] = is_max ? fmaxf(a, c) : a + c;
-    }
-    __syncthreads();
-  }
-  const float r = red[0];
-  __syncthreads();
-  return r;
-}
-
-__global__ void __launch_bounds__(kStatsThreads) attn_stats_kernel(AttnParams p) {
-  __shared__ float red[kStatsThreads];
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int n = attn_len(p, b);
-  const uint16_t* s = p.s + ((int64_t)b * p.hq + h) * p.cap;
-  // 8 scores (16 bytes) per thread and step; cap is a multiple of 64, so the
-  // loads stay inside the row, and tokens from n on are skipped
-  auto score = [&](const u32x4& v, int k) { return bf16_to_float((uint16_t)(v[k >> 1] >> (16 * (k & 1)))); };
+  // The wave's statistics of head col over its attended tokens: the maximum
+  // over the lane's scores and the four K groups (lanes col + 16g), then the
+  // sum of exp(score - max) (hardware exponential: the sum only normalises,
+  // and the merge below weighs it by an accurate exp) the same way.
   float m = -__builtin_inff();
-  for (int t0 = 8 * threadIdx.x; t0 < n; t0 += 8 * kStatsThreads) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(s + t0);
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (t0 + k < n) m = fmaxf(m, score(v, k));
-  }
-  m = block_reduce(m, red, true);
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (t0 + 16 * rb + 4 * g + v < n) m = fmaxf(m, sv[rb][v]);
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32));
   float l = 0.f;
-  for (int t0 = 8 * threadIdx.x; t0 < n; t0 += 8 * kStatsThreads) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(s + t0);
 #pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (t0 + k < n) l += expf(score(v, k) - m);
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      if (t0 + 16 * rb + 4 * g + v < n) l += __expf(sv[rb][v] - m);
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (g == 0 && col < p.r) {
+    float* ws = p.wstats + (((int64_t)b * p.hq + kh * p.r + col) * (p.cap / kAttnWaveTok) + t0 / kAttnWaveTok) * 2;
+    *reinterpret_cast<f32x2*>(ws) = f32x2{m, l};
   }
-  l = block_reduce(l, red, false);
-  if (threadIdx.x == 0) {
-    p.stats[((int64_t)b * p.hq + h) * 2] = m;
-    p.stats[((int64_t)b * p.hq + h) * 2 + 1] = l;
+}
+
+// Per (sequence, query head), one wave: max = max_w m_w and sum =
+// sum_w l_w exp(m_w - max) over the sequence's 64-token groups; lane i takes
+// groups i, i + 64, ... in order, then the 64 lanes are merged in a fixed xor
+// tree.
+__global__ void __launch_bounds__(64) attn_stats_kernel(AttnParams p) {
+  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+  const int nw = (attn_len(p, b) + kAttnWaveTok - 1) / kAttnWaveTok;
+  const float* ws = p.wstats + ((int64_t)b * p.hq + h) * (p.cap / kAttnWaveTok) * 2;
+  float m = -__builtin_inff();
+  for (int w = lane; w < nw; w += 64) m = fmaxf(m, ws[2 * w]);
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+  float l = 0.f;
+  for (int w = lane; w < nw; w += 64) {
+    const f32x2 v = *reinterpret_cast<const f32x2*>(ws + 2 * w);
+    l += v[1] * expf(v[0] - m);
   }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) l += __shfl_xor(l, off);
+  if (lane == 0) *reinterpret_cast<f32x2*>(p.stats + ((int64_t)b * p.hq + h) * 2) = f32x2{m, l};
 }
 
 __global__ void __launch_bounds__(256) attn_pv_kernel(AttnParams p) {
@@ -334,7 +331,7 @@ __global__ void __launch_bounds__(8 * kAttnD) attn_combine_kernel(AttnParams p) 
 }
 
 struct AttnLayout {
-  size_t s, stats, part, total;
+  size_t s, wstats, stats, part, total;
 };
 
 static size_t attn_align(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -343,7 +340,8 @@ static AttnLayout attn_layout(int64_t B, int64_t hq, int64_t kvh, int64_t cap) {
   AttnLayout L;
   const int64_t nchunks = (cap + kAttnChunk - 1) / kAttnChunk;
   L.s = 0;
-  L.stats = attn_align(L.s + (size_t)B * hq * cap * 2);
+  L.wstats = attn_align(L.s + (size_t)B * hq * cap * 2);
+  L.stats = attn_align(L.wstats + (size_t)B * hq * (cap / kAttnWaveTok) * 2 * 4);
   L.part = attn_align(L.stats + (size_t)B * hq * 2 * 4);
   L.total = attn_align(L.part + (size_t)B * kvh * nchunks * kAttnR * kAttnD * 4);
   return L;
@@ -400,13 +398,14 @@ extern "C" int q6moe_kv_decode_attention(const q6moe_attn_args* a, void* stream)
   p.nchunks = (int)((cap + kAttnChunk - 1) / kAttnChunk);
   uint8_t* w = reinterpret_cast<uint8_t*>(a->workspace);
   p.s = reinterpret_cast<uint16_t*>(w + L.s);
+  p.wstats = reinterpret_cast<float*>(w + L.wstats);
   p.stats = reinterpret_cast<float*>(w + L.stats);
   p.part = reinterpret_cast<float*>(w + L.part);
   p.out = a->out;
   hipStream_t s = (hipStream_t)stream;
   const dim3 chunks((unsigned)p.nchunks, (unsigned)p.kvh, (unsigned)a->batch);
   hipLaunchKernelGGL(attn_scores_kernel, chunks, dim3(256), 0, s, p);
-  hipLaunchKernelGGL(attn_stats_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(kStatsThreads), 0, s, p);
+  hipLaunchKernelGGL(attn_stats_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(64), 0, s, p);
   hipLaunchKernelGGL(attn_pv_kernel, chunks, dim3(256), 0, s, p);
   hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(8 * kAttnD), 0, s, p);
   return check_launch("decode_attention kernels");
