@@ -486,3 +486,33 @@ def test_profiling_events_leave_results_and_bracket_gate_up(device, tokens, mode
         ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(4)]
         assert all(m >= 0.0 for m in ms), ms
         assert 0.0 < ms[1] <= evs[0].elapsed_time(evs[4]), ms
+
+
+@pytest.fixture(scope="module")
+def largest_layer(device):
+    L = moe_layer(seed=77, experts=1024, top_k=32, hidden=256, intermediate=256, tokens=300, pack=False,
+                  down_qtype="Q8_0")
+    fn = expert_parallel(None, gate_type="Q6_K", up_type="Q6_K", down_type="Q8_0", hidden=256, intermediate=256)
+    tabs = fn.prepare(*(L[n].reshape(1024, -1) for n in ("gate", "up", "down")), device)
+    return L, fn, tabs
+
+
+@pytest.mark.parametrize("tokens", [1, 8, 32, 100, 300])
+def test_largest_layer_every_family(device, largest_layer, tokens):
+    # The operator's limits: 1024 experts and top-32. 32 tokens x 32 routes is
+    # the decode-step kernels' most entries (1024); 100 tokens route in one
+    # launch (one chunk of 256 tokens), 300 in three passes over two chunks.
+    # Every family the call can take agrees bitwise with the others, and the
+    # result meets the oracle's gate.
+    L, fn, tabs = largest_layer
+    rows = slice(0, tokens)
+    x = torch.from_numpy(L["x"][rows]).to(device).to(torch.bfloat16)
+    ids = torch.from_numpy(L["ids"][rows]).to(device)
+    w = torch.from_numpy(L["weights"][rows]).to(device).to(torch.bfloat16)
+    modes = [0, 2] + ([1] if tokens * 32 <= 1024 else [])
+    outs = [fn.with_mode(m)(*tabs, x, ids, w).float().cpu().numpy() for m in modes]
+    for o in outs[1:]:
+        np.testing.assert_array_equal(outs[0], o)
+    want = oracle_moe.expert_ffn(L["gate"], L["up"], L["down"], L["x"][rows], L["ids"][rows], L["weights"][rows],
+                                 types=("Q6_K", "Q6_K", "Q8_0"), hidden=256, intermediate=256, workers=8)
+    assert_moe_close(outs[0], want)
