@@ -61,35 +61,43 @@ __device__ __forceinline__ void stage_chunk2(DA* da, const SA* __restrict__ sa, 
 // (experts.py:66-73; 0 for repeats and out-of-range ids), in place of the
 // staged weights s_w, and the per-expert route counts cnt, for the nb staged
 // tokens of a chunk (lane tid = token tid).
+// top_k <= KM: the token's entries in registers, every loop unrolled (the
+// same comparisons and the same summation order as route_merge's loops)
+template <int KM>
+__device__ __forceinline__ void route_merge_regs(const int* s_ids, float* s_w, int* cnt, int K, int E) {
+  const int tid = threadIdx.x;
+  int id[KM];
+  float w[KM], mg[KM];
+#pragma unroll
+  for (int kk = 0; kk < KM; ++kk) {
+    id[kk] = kk < K ? s_ids[tid * K + kk] : -1;
+    w[kk] = kk < K ? s_w[tid * K + kk] : 0.f;
+  }
+#pragma unroll
+  for (int kk = 0; kk < KM; ++kk) {
+    const int e = id[kk];
+    bool first = kk < K && e >= 0 && e < E;
+#pragma unroll
+    for (int k2 = 0; k2 < kk; ++k2) first = first && id[k2] != e;
+    float sum = 0.f;
+#pragma unroll
+    for (int k2 = kk; k2 < KM; ++k2)
+      if (k2 < K && id[k2] == e) sum += w[k2];
+    const float m = first ? bf16_round(sum) : 0.f;
+    if (first && is_route(m)) atomicAdd(&cnt[e], 1);
+    mg[kk] = is_route(m) ? m : 0.f;
+  }
+#pragma unroll
+  for (int kk = 0; kk < KM; ++kk)
+    if (kk < K) s_w[tid * K + kk] = mg[kk];
+}
+
 __device__ __forceinline__ void route_merge(const int* s_ids, float* s_w, int* cnt, int nb, int K, int E) {
   const int tid = threadIdx.x;
   if (tid < nb && K <= 8) {
-    // top_k <= 8: the token's entries in registers, every loop unrolled (the
-    // same comparisons and the same summation order as below)
-    int id[8];
-    float w[8], mg[8];
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      id[kk] = kk < K ? s_ids[tid * K + kk] : -1;
-      w[kk] = kk < K ? s_w[tid * K + kk] : 0.f;
-    }
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const int e = id[kk];
-      bool first = kk < K && e >= 0 && e < E;
-#pragma unroll
-      for (int k2 = 0; k2 < kk; ++k2) first = first && id[k2] != e;
-      float sum = 0.f;
-#pragma unroll
-      for (int k2 = kk; k2 < 8; ++k2)
-        if (k2 < K && id[k2] == e) sum += w[k2];
-      const float m = first ? bf16_round(sum) : 0.f;
-      if (first && is_route(m)) atomicAdd(&cnt[e], 1);
-      mg[kk] = is_route(m) ? m : 0.f;
-    }
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      if (kk < K) s_w[tid * K + kk] = mg[kk];
+    route_merge_regs<8>(s_ids, s_w, cnt, K, E);
+  } else if (tid < nb && K <= 16) {
+    route_merge_regs<16>(s_ids, s_w, cnt, K, E);
   } else if (tid < nb) {
     const int* id = s_ids + tid * K;
     float* w = s_w + tid * K;
@@ -224,6 +232,44 @@ __global__ void __launch_bounds__(kMaxExperts)
 // of its expert, so its position is s_pos[e] (the expert's first position
 // plus the chunk's offset within it) plus that rank; route_tok and route_w at
 // the position; per token, its positions in ascending expert id into s_tp.
+// top_k <= KM: the token's entries and its position list in registers; the
+// list is sorted by an odd-even transposition network (non-routes last)
+template <int KM>
+__device__ __forceinline__ void route_place_regs(const int* s_ids, const float* s_r, int* s_tp,
+                                                 const uint32_t* bits, const int* s_pos, int K, int b0, MoeWs ws) {
+  const int tid = threadIdx.x;
+  int pos[KM];
+#pragma unroll
+  for (int kk = 0; kk < KM; ++kk) {
+    pos[kk] = 0x7fffffff;
+    const float r = kk < K ? s_r[tid * K + kk] : 0.f;
+    if (kk < K && is_route(r)) {
+      const int e = s_ids[tid * K + kk];
+      int rank = __popc(bits[e * kChunkWords + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
+#pragma unroll
+      for (int w = 0; w < kChunkWords - 1; ++w)
+        if (w < (tid >> 5)) rank += __popc(bits[e * kChunkWords + w]);
+      const int p = s_pos[e] + rank;
+      ws.route_tok[p] = b0 + tid;
+      ws.route_w[p] = r;
+      pos[kk] = p;
+    }
+  }
+#pragma unroll
+  for (int pass = 0; pass < KM; ++pass)
+#pragma unroll
+    for (int i = pass & 1; i + 1 < KM; i += 2)
+      if (pos[i] > pos[i + 1]) {
+        const int t = pos[i];
+        pos[i] = pos[i + 1];
+        pos[i + 1] = t;
+      }
+  int* tp = s_tp + tid * K;
+#pragma unroll
+  for (int q = 0; q < KM; ++q)
+    if (q < K) tp[q] = pos[q] == 0x7fffffff ? -1 : pos[q];
+}
+
 __device__ __forceinline__ void route_place(const int* s_ids, const float* s_r, int* s_tp, uint32_t* bits,
                                             const int* s_pos, int nb, int K, int b0, MoeWs ws) {
   const int tid = threadIdx.x;
@@ -233,38 +279,9 @@ __device__ __forceinline__ void route_place(const int* s_ids, const float* s_r, 
         atomicOr(&bits[s_ids[tid * K + kk] * kChunkWords + (tid >> 5)], 1u << (tid & 31));
   __syncthreads();
   if (tid < nb && K <= 8) {
-    // top_k <= 8: the token's entries and its position list in registers; the
-    // list is sorted by an odd-even transposition network (non-routes last)
-    int pos[8];
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      pos[kk] = 0x7fffffff;
-      const float r = kk < K ? s_r[tid * K + kk] : 0.f;
-      if (kk < K && is_route(r)) {
-        const int e = s_ids[tid * K + kk];
-        int rank = __popc(bits[e * kChunkWords + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
-#pragma unroll
-        for (int w = 0; w < kChunkWords - 1; ++w)
-          if (w < (tid >> 5)) rank += __popc(bits[e * kChunkWords + w]);
-        const int p = s_pos[e] + rank;
-        ws.route_tok[p] = b0 + tid;
-        ws.route_w[p] = r;
-        pos[kk] = p;
-      }
-    }
-#pragma unroll
-    for (int pass = 0; pass < 8; ++pass)
-#pragma unroll
-      for (int i = pass & 1; i + 1 < 8; i += 2)
-        if (pos[i] > pos[i + 1]) {
-          const int t = pos[i];
-          pos[i] = pos[i + 1];
-          pos[i + 1] = t;
-        }
-    int* tp = s_tp + tid * K;
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      if (q < K) tp[q] = pos[q] == 0x7fffffff ? -1 : pos[q];
+    route_place_regs<8>(s_ids, s_r, s_tp, bits, s_pos, K, b0, ws);
+  } else if (tid < nb && K <= 16) {
+    route_place_regs<16>(s_ids, s_r, s_tp, bits, s_pos, K, b0, ws);
   } else if (tid < nb) {
     int* tp = s_tp + tid * K;
     int m = 0;
