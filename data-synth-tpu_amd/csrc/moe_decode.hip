@@ -570,7 +570,33 @@ __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTa
     const int i = i0 + lane;
     float r = 0.f;
     int id = -1;
-    if (i < n) {
+    if (i < n && R.K <= 16) {
+      // top_k <= 16: the token's entries read in one batch (clamped to entry
+      // 0 past top_k, and masked below), then the same comparisons and
+      // summation order as the loops of the general case
+      const int b = i / R.K, kk = i - b * R.K;
+      int id2[16];
+      float r2[16];
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) {
+        const int o = b * R.K + (k2 < R.K ? k2 : 0);
+        id2[k2] = s_ids[o];
+        r2[k2] = s_r[o];
+      }
+      id = s_ids[i];
+      bool first = id >= 0 && id < R.E;
+      float s = 0.f;
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) {
+        const bool same = k2 < R.K && id2[k2] == id;
+        first = first && !(same && k2 < kk);
+        s += (same && k2 >= kk) ? r2[k2] : 0.f;
+      }
+      if (first) {
+        r = bf16_round(s);
+        r = r != 0.f ? r : 0.f;
+      }
+    } else if (i < n) {
       const int b = i / R.K, kk = i - b * R.K;
       id = s_ids[i];
       bool first = id >= 0 && id < R.E;
@@ -662,9 +688,22 @@ __device__ bool dec_route(const DecRoute& R, int slot, bool publish, const DecTa
         tok[rank] = b;
         if (publish) {
           int er = 0;  // routed experts of this token with a smaller id
-          for (int kk = 0; kk < R.K; ++kk) {
-            const int o = b * R.K + kk;
-            er += (s_r[o] != 0.f) && s_ids[o] < e;
+          if (R.K <= 16) {
+            int id2[16];
+            float r2[16];
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) {
+              const int o = b * R.K + (kk < R.K ? kk : 0);
+              id2[kk] = s_ids[o];
+              r2[kk] = s_r[o];
+            }
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) er += kk < R.K && r2[kk] != 0.f && id2[kk] < e;
+          } else {
+            for (int kk = 0; kk < R.K; ++kk) {
+              const int o = b * R.K + kk;
+              er += (s_r[o] != 0.f) && s_ids[o] < e;
+            }
           }
           st_agent(&T.route_w[t0 + rank], s_r[i]);
           st_agent(&T.route_dst[t0 + rank], b * R.K + er);
