@@ -57,12 +57,89 @@ __device__ __forceinline__ void stage_chunk2(DA* da, const SA* __restrict__ sa, 
   }
 }
 
+// Routing with G lanes per token (top_k <= KM, the token's row in registers;
+// lane g of a group takes slots g, g + G, ...), used by the one-launch
+// routing of few tokens.
+template <int KM>
+__device__ __forceinline__ void load_row(const int* s_ids, const float* s_v, int b, int K, int (&rid)[KM],
+                                         float (&rv)[KM]) {
+#pragma unroll
+  for (int k2 = 0; k2 < KM; ++k2) {
+    rid[k2] = k2 < K ? s_ids[b * K + k2] : -1;
+    rv[k2] = k2 < K ? s_v[b * K + k2] : 0.f;
+  }
+}
+
+// Merged BF16 weight of slot kk of token b (experts.py:66-73: the sum of the
+// weights of slots kk.. with its id, in slot order, on the first occurrence of
+// an id in range; 0 otherwise, as route_merge) into s_m, the expert's route
+// count in cnt and the token's bit in the expert's token bitmap.
+template <int KM>
+__device__ __forceinline__ void merge_grp(const int* s_ids, const float* s_w, float* s_m, int* cnt, uint32_t* bits,
+                                          int b, int g, int G, int K, int E) {
+  int rid[KM];
+  float rw[KM];
+  load_row<KM>(s_ids, s_w, b, K, rid, rw);
+  for (int kk = g; kk < K; kk += G) {
+    const int e = s_ids[b * K + kk];  // from LDS: a run-time index into rid would go to scratch
+    bool first = e >= 0 && e < E;
+    float sum = 0.f;
+#pragma unroll
+    for (int k2 = 0; k2 < KM; ++k2) {
+      first = first && !(k2 < kk && rid[k2] == e);
+      if (k2 >= kk && rid[k2] == e) sum += rw[k2];
+    }
+    const float m = first ? bf16_round(sum) : 0.f;
+    const bool route = first && is_route(m);
+    s_m[b * K + kk] = route ? m : 0.f;
+    if (route) {
+      atomicAdd(&cnt[e], 1);
+      atomicOr(&bits[e * kChunkWords + (b >> 5)], 1u << (b & 31));
+    }
+  }
+}
+
+// Places the routes of token b (of the chunk; bglob in the batch): a route's
+// position is its expert's first position s_pos[e] plus the number of earlier
+// tokens of the chunk routed to e (token bitmaps); route_tok and route_w at
+// that position, and the position into the token's row tp at the number of
+// the token's routes to smaller expert ids (positions are expert-major, so the
+// row is ascending); the row's slots from the token's route count on hold -1.
+template <int KM>
+__device__ __forceinline__ void place_grp(const int* s_ids, const float* s_m, const uint32_t* bits, const int* s_pos,
+                                          int b, int g, int G, int K, int bglob, int* tp, MoeWs ws) {
+  int rid[KM];
+  float rm[KM];
+  load_row<KM>(s_ids, s_m, b, K, rid, rm);
+  int nr = 0;
+#pragma unroll
+  for (int k2 = 0; k2 < KM; ++k2) nr += is_route(rm[k2]);
+  for (int kk = g; kk < K; kk += G) {
+    const int e = s_ids[b * K + kk];
+    const float r = s_m[b * K + kk];
+    if (is_route(r)) {
+      int q = 0;
+#pragma unroll
+      for (int k2 = 0; k2 < KM; ++k2) q += is_route(rm[k2]) && rid[k2] < e;
+      int rank = __popc(bits[e * kChunkWords + (b >> 5)] & ((1u << (b & 31)) - 1u));
+#pragma unroll
+      for (int w = 0; w < kChunkWords - 1; ++w)
+        if (w < (b >> 5)) rank += __popc(bits[e * kChunkWords + w]);
+      const int p = s_pos[e] + rank;
+      ws.route_tok[p] = bglob;
+      ws.route_w[p] = r;
+      tp[q] = p;
+    }
+    if (kk >= nr) tp[kk] = -1;
+  }
+}
+
 // Merged BF16 weight of each first occurrence of an id in a token
 // (experts.py:66-73; 0 for repeats and out-of-range ids), in place of the
 // staged weights s_w, and the per-expert route counts cnt, for the nb staged
 // tokens of a chunk (lane tid = token tid).
 // top_k <= KM: the token's entries in registers, every loop unrolled (the
-// same comparisons and the same summation order as route_merge's loops)
+// same comparisons and the same summation order as merge_grp)
 template <int KM>
 __device__ __forceinline__ void route_merge_regs(const int* s_ids, float* s_w, int* cnt, int K, int E) {
   const int tid = threadIdx.x;
@@ -99,24 +176,7 @@ __device__ __forceinline__ void route_merge(const int* s_ids, float* s_w, int* c
   } else if (tid < nb && K <= 16) {
     route_merge_regs<16>(s_ids, s_w, cnt, K, E);
   } else if (tid < nb) {
-    const int* id = s_ids + tid * K;
-    float* w = s_w + tid * K;
-    // The sum for entry kk reads weights kk..K-1 only, so entry kk's merged
-    // weight can replace its raw weight in place.
-    for (int kk = 0; kk < K; ++kk) {
-      const int e = id[kk];
-      bool first = e >= 0 && e < E;
-      for (int k2 = 0; k2 < kk && first; ++k2) first = id[k2] != e;
-      float m = 0.f;
-      if (first) {
-        float sum = 0.f;
-        for (int k2 = kk; k2 < K; ++k2)
-          if (id[k2] == e) sum += w[k2];
-        m = bf16_round(sum);
-        if (is_route(m)) atomicAdd(&cnt[e], 1);
-      }
-      w[kk] = is_route(m) ? m : 0.f;
-    }
+    route_merge_regs<32>(s_ids, s_w, cnt, K, E);
   }
 }
 
@@ -283,27 +343,7 @@ __device__ __forceinline__ void route_place(const int* s_ids, const float* s_r, 
   } else if (tid < nb && K <= 16) {
     route_place_regs<16>(s_ids, s_r, s_tp, bits, s_pos, K, b0, ws);
   } else if (tid < nb) {
-    int* tp = s_tp + tid * K;
-    int m = 0;
-    for (int kk = 0; kk < K; ++kk) {
-      const float r = s_r[tid * K + kk];
-      if (is_route(r)) {
-        const int e = s_ids[tid * K + kk];
-        int rank = __popc(bits[e * kChunkWords + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
-        for (int w = 0; w < (tid >> 5); ++w) rank += __popc(bits[e * kChunkWords + w]);
-        const int pos = s_pos[e] + rank;
-        ws.route_tok[pos] = b0 + tid;
-        ws.route_w[pos] = r;
-        // positions are expert-major: keep the token's list sorted (insertion)
-        int q = m++;
-        while (q > 0 && tp[q - 1] > pos) {
-          tp[q] = tp[q - 1];
-          --q;
-        }
-        tp[q] = pos;
-      }
-    }
-    for (int q = m; q < K; ++q) tp[q] = -1;
+    route_place_regs<32>(s_ids, s_r, s_tp, bits, s_pos, K, b0, ws);
   }
   __syncthreads();
 }
@@ -349,33 +389,64 @@ __global__ void __launch_bounds__(kChunk)
 }
 
 // Routing of at most kChunk tokens in one launch: the three passes above in
-// one workgroup of max(kChunk, E rounded up to whole waves) lanes, the
-// chunk's counts and positions kept in LDS (its offsets within each expert
-// are 0). Same outputs as the three launches.
+// one workgroup of max(kChunk, E rounded up to whole waves) lanes, merge and
+// placement with G lanes per token (so few tokens still spread over every
+// wave), the chunk's counts and positions kept in LDS (its offsets within
+// each expert are 0). Same outputs as the three launches.
 __global__ void __launch_bounds__(kMaxExperts)
     moe_route_small_kernel(const int32_t* __restrict__ ids, const uint16_t* __restrict__ wts, int B, int K, int E,
                            int mtile, MoeWs ws) {
   extern __shared__ int sm[];
   int* s_ids = sm;                                                     // [kChunk * K]
-  float* s_w = reinterpret_cast<float*>(sm + kChunk * K);              // [kChunk * K]
-  int* s_tp = sm + 2 * kChunk * K;                                     // [kChunk * K]
+  float* s_w = reinterpret_cast<float*>(sm + kChunk * K);              // [kChunk * K] staged weights
+  float* s_m = reinterpret_cast<float*>(sm + 2 * kChunk * K);          // [kChunk * K] merged weights
   uint32_t* bits = reinterpret_cast<uint32_t*>(sm + 3 * kChunk * K);   // [E][kChunkWords]
   int* s_pos = sm + 3 * kChunk * K + E * kChunkWords;                  // [E]
   int* cnt = s_pos + E;                                                // [E]
   __shared__ int s_wt[3][kMaxExperts / 64];
-  const int tid = threadIdx.x, n = (int)blockDim.x;
+  const int tid = threadIdx.x, n = (int)blockDim.x, nent = B * K;
   for (int e = tid; e < E; e += n) cnt[e] = 0;
   for (int i = tid; i < E * kChunkWords; i += n) bits[i] = 0u;
   if (tid < kChunk)
-    stage_chunk2(s_ids, ids, [](int v) { return v; }, s_w, wts, [](uint16_t v) { return bf16_to_float(v); }, B * K);
+    stage_chunk2(s_ids, ids, [](int v) { return v; }, s_w, wts, [](uint16_t v) { return bf16_to_float(v); }, nent);
   __syncthreads();
-  route_merge(s_ids, s_w, cnt, B, K, E);
+  // G lanes per token: doubled while below top_k and B * G stays within the
+  // lanes; with one lane per token the token-parallel passes' functions
+  int G = 1;
+  while (G < K && B * G * 2 <= n) G <<= 1;
+  if (G == 1) {
+    route_merge(s_ids, s_w, cnt, B, K, E);
+    __syncthreads();
+    const int base = route_scan(tid, E, tid < E ? cnt[tid] : 0, mtile, ws, s_wt);
+    if (tid < E) s_pos[tid] = base;
+    __syncthreads();
+    int* s_tp = reinterpret_cast<int*>(s_m);
+    route_place(s_ids, s_w, s_tp, bits, s_pos, B, K, 0, ws);
+    for (int i = tid; i < nent; i += n) ws.tok_pos[i] = s_tp[i];
+    return;
+  }
+  const int b = tid / G, g = tid & (G - 1);
+  if (b < B) {
+    if (K <= 8)
+      merge_grp<8>(s_ids, s_w, s_m, cnt, bits, b, g, G, K, E);
+    else if (K <= 16)
+      merge_grp<16>(s_ids, s_w, s_m, cnt, bits, b, g, G, K, E);
+    else
+      merge_grp<32>(s_ids, s_w, s_m, cnt, bits, b, g, G, K, E);
+  }
   __syncthreads();
   const int base = route_scan(tid, E, tid < E ? cnt[tid] : 0, mtile, ws, s_wt);
   if (tid < E) s_pos[tid] = base;
   __syncthreads();
-  route_place(s_ids, s_w, s_tp, bits, s_pos, B, K, 0, ws);
-  for (int i = tid; i < B * K; i += n) ws.tok_pos[i] = s_tp[i];
+  if (b < B) {
+    int* tp = ws.tok_pos + (int64_t)b * K;
+    if (K <= 8)
+      place_grp<8>(s_ids, s_m, bits, s_pos, b, g, G, K, b, tp, ws);
+    else if (K <= 16)
+      place_grp<16>(s_ids, s_m, bits, s_pos, b, g, G, K, b, tp, ws);
+    else
+      place_grp<32>(s_ids, s_m, bits, s_pos, b, g, G, K, b, tp, ws);
+  }
 }
 
 // ---------------------------------------------------------------------------

@@ -93,7 +93,7 @@ def test_small_layers_match_oracle(device, qtype, tokens, experts, top_k):
 def test_top_k_above_eight_matches_oracle(device, mode, tokens, top_k):
     # More than 8 routes per token: the decode-step combine sums the rank rows
     # past the first eight in a second loop, and the routing kernels of every
-    # path take their general (non-register) branches.
+    # path take their 16-entry register branches.
     L = moe_layer(seed=60 + tokens + top_k, experts=20, top_k=top_k, hidden=512, intermediate=256,
                   tokens=tokens, pack=False)
     got, _ = _run(L, device, mode=mode)
@@ -149,6 +149,38 @@ def test_duplicate_routes_sum_and_zero_rows_are_exact_zero(device):
     assert_moe_close(got, want)
     zero, _ = _run(L, device, ids=ids, weights=np.zeros_like(w))
     assert np.all(zero == 0)
+
+
+@pytest.mark.parametrize("tokens,top_k,experts", [
+    (6, 8, 64),      # one launch, a group of 8 lanes per token
+    (40, 16, 128),   # one launch, 4 lanes per token
+    (100, 32, 256),  # one launch, 2 lanes per token, top-k above 16
+    (256, 8, 64),    # one launch, one lane per token
+    (180, 20, 48),   # one launch, one lane per token, top-k above 16
+    (513, 8, 16),    # three passes over three chunks
+    (600, 24, 96),   # three passes, top-k above 16
+])
+def test_grouped_routing_edge_entries(device, tokens, top_k, experts):
+    # The grouped family's routing in each of its branches, fed a token whose
+    # entries all name one expert, repeats at both ends of a row, ids past the
+    # last expert and -1, an all-zero row and a lone zero weight: the result
+    # meets the oracle's gate and, where the decode family takes the call, is
+    # bitwise equal to it.
+    L = moe_layer(seed=70 + top_k, experts=experts, top_k=top_k, hidden=256, intermediate=256, tokens=tokens,
+                  pack=False)
+    ids = L["ids"].copy()
+    w = L["weights"].copy()
+    ids[0, :] = ids[0, 0]
+    ids[1, -1] = ids[1, 0]
+    ids[2, 1] = experts + 5
+    ids[2, -1] = -1
+    w[3] = 0
+    w[4, top_k // 2] = 0
+    got, _ = _run(L, device, mode=2, ids=ids, weights=w)
+    assert np.all(got[3] == 0)
+    assert_moe_close(got, _oracle(L, ids=ids, weights=w))
+    if tokens <= 256 and tokens * top_k <= 1024:
+        np.testing.assert_array_equal(got, _run(L, device, mode=1, ids=ids, weights=w)[0])
 
 
 def test_poisoned_unrouted_experts_do_not_leak(device):
