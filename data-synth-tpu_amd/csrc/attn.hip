@@ -20,12 +20,13 @@
 //   2. attn_stats_kernel: per (sequence, query head), the maximum over the
 //      attended tokens, max = max_w m_w, and the sum of exp(score - max),
 //      sum_w l_w exp(m_w - max), in a fixed order.
-//   3. attn_pv_kernel: per chunk, the workgroup forms RNE_bf16(prob) once per
-//      (head, token) in LDS; each wave then runs P.V for its 64 tokens on
-//      MFMA with the dequantised values as A operand (row = 8 channels apart,
-//      so a lane dequantises the 8x8 code block it loaded straight into eight
-//      tiles' operands) and the probabilities as B; the chunk's partial sums
-//      go to the workspace.
+//   3. attn_pv_kernel: per 2048-token chunk (8 waves, four 64-token tiles
+//      each), the workgroup forms RNE_bf16(prob) once per (head, token) in
+//      LDS; each wave then runs P.V for its tiles, in turn, on MFMA with the
+//      dequantised values as A operand (row = 8 channels apart, so a lane
+//      dequantises the 8x8 code block it loaded straight into eight tiles'
+//      operands) and the probabilities as B; the chunk's partial sums go to
+//      the workspace.
 //   4. attn_combine_kernel: partial sums over chunks in a fixed order, RNE.
 //
 // HBM-bound: the INT8 codes and scales of K and V are read once.
@@ -36,8 +37,12 @@ namespace q6moe {
 
 constexpr int kAttnD = 128;      // head_dim
 constexpr int kAttnR = 8;        // at most this many query heads per KV head
-constexpr int kAttnChunk = 256;  // tokens per workgroup: 4 waves x 64
+constexpr int kAttnChunk = 256;  // tokens per scores workgroup: 4 waves x 64
 constexpr int kAttnWaveTok = 64;
+constexpr int kPvWaves = 8;      // waves per P.V workgroup
+constexpr int kPvThreads = kPvWaves * 64;
+constexpr int kPvTiles = 4;      // 64-token tiles per P.V wave
+constexpr int kPvChunk = kPvTiles * kPvThreads;  // tokens per P.V workgroup (one partial sum)
 
 struct AttnParams {
   const uint16_t* q;                 // [B, Hq, D]
@@ -48,7 +53,7 @@ struct AttnParams {
   const int32_t* table;              // [B, pps]
   const int32_t* len;                // [B]
   int64_t pool_pages;
-  int pps, page, kvh, hq, r, cap, nchunks;
+  int pps, page, kvh, hq, r, cap, nchunks;  // nchunks: P.V chunks of kPvChunk tokens
   uint16_t* s;                       // [B, Hq, cap] BF16 scores
   float* wstats;                     // [B, Hq, cap / 64, 2]: per 64 tokens, max m_w and sum of exp(score - m_w)
   float* stats;                      // [B, Hq, 2]: max, sum
@@ -195,17 +200,20 @@ __global__ void __launch_bounds__(64) attn_stats_kernel(AttnParams p) {
   if (lane == 0) *reinterpret_cast<f32x2*>(p.stats + ((int64_t)b * p.hq + h) * 2) = f32x2{m, l};
 }
 
-__global__ void __launch_bounds__(256) attn_pv_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t pr[kAttnR][kAttnChunk];  // RNE_bf16(prob) [head][token]
-  __shared__ float red[4][kAttnR][kAttnD];                              // per-wave partial sums
+__global__ void __launch_bounds__(kPvThreads) attn_pv_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t pr[kAttnR][kPvChunk];  // RNE_bf16(prob) [head][token]
+  __shared__ float red[kPvWaves][kAttnR][kAttnD];                       // per-wave partial sums
   const int chunk = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c0 = chunk * kAttnChunk;
+  const int c0 = chunk * kPvChunk;
   const int r16 = lane & 15, kg = lane >> 4;
-  // The wave's page entry and the heads' softmax statistics (scalar loads;
-  // the head index is clamped into the group's r, and what it stands in for
-  // is never used) are read together with the length.
-  const int64_t pg = attn_page(p, b, c0 + 64 * wave);
+  // The wave's page entries (tile i: tokens c0 + kPvThreads*i + 64*wave + [0, 64))
+  // and the heads' softmax statistics (scalar loads; the head index is clamped
+  // into the group's r, and what it stands in for is never used) are read
+  // together with the length.
+  int64_t pg[kPvTiles];
+#pragma unroll
+  for (int i = 0; i < kPvTiles; ++i) pg[i] = attn_page(p, b, c0 + kPvThreads * i + 64 * wave);
   float sm[kAttnR], sl[kAttnR];
 #pragma unroll
   for (int h = 0; h < kAttnR; ++h) {
@@ -216,76 +224,98 @@ __global__ void __launch_bounds__(256) attn_pv_kernel(AttnParams p) {
   const int n = attn_len(p, b);
   asm volatile("" ::: "memory");  // the loads above issue before the length is waited for
   if (c0 >= n) return;  // uniform over the workgroup
-  const int nv = n - c0 < kAttnChunk ? n - c0 : kAttnChunk;
-  // For the probability pass (thread t = token c0 + t): the chunk's scores of
-  // every head, loaded before the V codes so that the pass waits for them
-  // only (token clamped into the sequence's length).
+  const int nv = n - c0 < kPvChunk ? n - c0 : kPvChunk;
+  // For the probability pass (thread t = tokens c0 + t + kPvThreads*i): the
+  // chunk's scores of every head, loaded before the V codes so that the pass
+  // waits for them only (token clamped into the sequence's length).
   const int t = threadIdx.x;
-  uint16_t sc[kAttnR];
-  {
-    const int tc = c0 + (t < nv ? t : nv - 1);
+  uint16_t sc[kPvTiles][kAttnR];
 #pragma unroll
-    for (int h = 0; h < kAttnR; ++h) sc[h] = p.s[((int64_t)b * p.hq + kh * p.r + (h < p.r ? h : 0)) * p.cap + tc];
+  for (int i = 0; i < kPvTiles; ++i) {
+    const int tt = t + kPvThreads * i;
+    const int tc = c0 + (tt < nv ? tt : nv - 1);
+#pragma unroll
+    for (int h = 0; h < kAttnR; ++h)
+      sc[i][h] = p.s[((int64_t)b * p.hq + kh * p.r + (h < p.r ? h : 0)) * p.cap + tc];
   }
-  // V codes next (their loads overlap the probability pass): lane (r16, kg)
-  // reads channels 8*r16 + [0, 8) of the wave's tokens 32s + 8kg + j (s = 0, 1;
-  // j = 0..7), all in the wave's page (row 0 of the pool for an unmapped one);
-  // tokens from nv on and unmapped pages are zeroed after the loads.
+  // V codes of a tile: lane (r16, kg) reads channels 8*r16 + [0, 8) of the
+  // wave's tokens 32s + 8kg + j (s = 0, 1; j = 0..7), all in the wave's page
+  // (row 0 of the pool for an unmapped one); tokens from nv on and unmapped
+  // pages are zeroed after the loads.
   const int64_t rowbytes = (int64_t)p.kvh * kAttnD;
-  const int64_t base = attn_row(p, pg, c0 + 64 * wave);
-  const int8_t* vw = p.vc + (base < 0 ? 0 : base) * rowbytes + kh * kAttnD;
-  const float* sw = p.vs + ((base < 0 ? 0 : base) + 8 * kg) * p.kvh + kh;
   const uint32_t lane_off = (uint32_t)(8 * kg) * (uint32_t)rowbytes + 8u * r16;
   u32x2 wv[2][8];
   float sv[2][8];
+  int64_t base = 0;
+  auto load_tile = [&](int i) {
+    base = attn_row(p, pg[i], c0 + kPvThreads * i + 64 * wave);
+    const int8_t* vw = p.vc + (base < 0 ? 0 : base) * rowbytes + kh * kAttnD;
+    const float* sw = p.vs + ((base < 0 ? 0 : base) + 8 * kg) * p.kvh + kh;
 #pragma unroll
-  for (int st = 0; st < 2; ++st)
+    for (int st = 0; st < 2; ++st)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      wv[st][j] = *reinterpret_cast<const u32x2*>(vw + lane_off + (uint32_t)(32 * st + j) * (uint32_t)rowbytes);
-      sv[st][j] = sw[(32 * st + j) * p.kvh];
-    }
+      for (int j = 0; j < 8; ++j) {
+        wv[st][j] = *reinterpret_cast<const u32x2*>(vw + lane_off + (uint32_t)(32 * st + j) * (uint32_t)rowbytes);
+        sv[st][j] = sw[(32 * st + j) * p.kvh];
+      }
+  };
+  // the V operands of tokens from nv on, and of an unmapped page, are zero
+  auto mask_tile = [&](int i) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool ok = base >= 0 && kPvThreads * i + 64 * wave + 32 * st + 8 * kg + j < nv;
+        wv[st][j] = ok ? wv[st][j] : u32x2{0u, 0u};
+        sv[st][j] = ok ? sv[st][j] : 0.f;
+      }
+  };
+  load_tile(0);
   // 1. RNE_bf16(prob) of every (head, token) of the chunk, once; heads from r
   //    on are 0 (MFMA columns 8-15 take zero operands below)
 #pragma unroll
-  for (int h = 0; h < kAttnR; ++h) {
-    float q = 0.f;
-    if (t < nv && h < p.r) q = bf16_round(expf(bf16_to_float(sc[h]) - sm[h]) / sl[h]);
-    pr[h][t] = bf16_bits(q);
-  }
-  // the V operands of tokens from nv on, and of an unmapped page, are zero
+  for (int i = 0; i < kPvTiles; ++i)
 #pragma unroll
-  for (int st = 0; st < 2; ++st)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const bool ok = base >= 0 && 64 * wave + 32 * st + 8 * kg + j < nv;
-      wv[st][j] = ok ? wv[st][j] : u32x2{0u, 0u};
-      sv[st][j] = ok ? sv[st][j] : 0.f;
+    for (int h = 0; h < kAttnR; ++h) {
+      const int tt = t + kPvThreads * i;
+      float q = 0.f;
+      if (tt < nv && h < p.r) q = bf16_round(expf(bf16_to_float(sc[i][h]) - sm[h]) / sl[h]);
+      pr[h][tt] = bf16_bits(q);
     }
+  mask_tile(0);
   __syncthreads();
-  // 2. out[h][d] over the wave's 64 tokens as 8 tiles of v_mfma_f32_16x16x32_bf16:
+  // 2. out[h][d] over the wave's tokens as 8 tiles of v_mfma_f32_16x16x32_bf16:
   //    tile T has A[row r][k] = v[token 32s + k][channel 8r + T] (lane (r16, kg)
-  //    dequantises byte T of its 8 tokens) and B[k][col h] = prob[h][token 32s + k]
+  //    dequantises byte T of its 8 tokens) and B[k][col h] = prob[h][token 32s + k];
+  //    the wave's token tiles in order (a tile wholly past nv is skipped)
   f32x4 acc[8];
 #pragma unroll
   for (int T = 0; T < 8; ++T) acc[T] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    u32x4 bq = {0u, 0u, 0u, 0u};
-    if (r16 < kAttnR) bq = *reinterpret_cast<const u32x4*>(&pr[r16][64 * wave + 32 * st + 8 * kg]);
+  for (int i = 0; i < kPvTiles; ++i) {
+    if (kPvThreads * i + 64 * wave >= nv) break;  // uniform over the wave
+    if (i > 0) {  // the loads of a later tile wait for this wave's earlier MFMAs
+      load_tile(i);
+      mask_tile(i);
+    }
 #pragma unroll
-    for (int T = 0; T < 8; ++T) {
-      auto val = [&](int j) {
-        const uint32_t w = T < 4 ? wv[st][j][0] : wv[st][j][1];
-        return (float)(int8_t)(w >> (8 * (T & 3))) * sv[st][j];
-      };
-      u32x4 a;
+    for (int st = 0; st < 2; ++st) {
+      u32x4 bq = {0u, 0u, 0u, 0u};
+      if (r16 < kAttnR) bq = *reinterpret_cast<const u32x4*>(&pr[r16][kPvThreads * i + 64 * wave + 32 * st + 8 * kg]);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) a[q] = pack_bf16x2(val(2 * q), val(2 * q + 1));
-      acc[T] = mfma16(a, bq, acc[T]);
+      for (int T = 0; T < 8; ++T) {
+        auto val = [&](int j) {
+          const uint32_t w = T < 4 ? wv[st][j][0] : wv[st][j][1];
+          return (float)(int8_t)(w >> (8 * (T & 3))) * sv[st][j];
+        };
+        u32x4 a;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[q] = pack_bf16x2(val(2 * q), val(2 * q + 1));
+        acc[T] = mfma16(a, bq, acc[T]);
+      }
     }
   }
-  // 3. lane (h = r16, kg) holds out[h][8*(4kg + v) + T] = acc[T][v]; the four
+  // 3. lane (h = r16, kg) holds out[h][8*(4kg + v) + T] = acc[T][v]; the
   //    waves' sums are added in wave order
   if (r16 < kAttnR) {
 #pragma unroll
@@ -295,9 +325,12 @@ __global__ void __launch_bounds__(256) attn_pv_kernel(AttnParams p) {
   }
   __syncthreads();
   float* dst = p.part + (((int64_t)b * p.kvh + kh) * p.nchunks + chunk) * kAttnR * kAttnD;
-  for (int o = threadIdx.x; o < kAttnR * kAttnD; o += 256) {
+  for (int o = threadIdx.x; o < kAttnR * kAttnD; o += kPvThreads) {
     const int h = o / kAttnD, d = o % kAttnD;
-    dst[o] = ((red[0][h][d] + red[1][h][d]) + red[2][h][d]) + red[3][h][d];
+    float v = red[0][h][d];
+#pragma unroll
+    for (int w = 1; w < kPvWaves; ++w) v += red[w][h][d];
+    dst[o] = v;
   }
 }
 
@@ -307,7 +340,7 @@ __global__ void __launch_bounds__(8 * kAttnD) attn_combine_kernel(AttnParams p) 
   __shared__ float red[8][kAttnD];
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x % kAttnD, grp = threadIdx.x / kAttnD;
   const int kh = h / p.r, hr = h % p.r;
-  const int nc = (attn_len(p, b) + kAttnChunk - 1) / kAttnChunk;
+  const int nc = (attn_len(p, b) + kPvChunk - 1) / kPvChunk;
   const int per = (nc + 7) / 8, cb = grp * per, ce = cb + per < nc ? cb + per : nc;
   const float* src = p.part + (((int64_t)b * p.kvh + kh) * p.nchunks) * kAttnR * kAttnD + hr * kAttnD + d;
   float v = 0.f;
@@ -338,7 +371,7 @@ static size_t attn_align(size_t v) { return (v + 255) & ~(size_t)255; }
 
 static AttnLayout attn_layout(int64_t B, int64_t hq, int64_t kvh, int64_t cap) {
   AttnLayout L;
-  const int64_t nchunks = (cap + kAttnChunk - 1) / kAttnChunk;
+  const int64_t nchunks = (cap + kPvChunk - 1) / kPvChunk;
   L.s = 0;
   L.wstats = attn_align(L.s + (size_t)B * hq * cap * 2);
   L.stats = attn_align(L.wstats + (size_t)B * hq * (cap / kAttnWaveTok) * 2 * 4);
@@ -395,7 +428,7 @@ extern "C" int q6moe_kv_decode_attention(const q6moe_attn_args* a, void* stream)
   p.hq = (int)a->query_heads;
   p.r = (int)(a->query_heads / a->kv_heads);
   p.cap = (int)cap;
-  p.nchunks = (int)((cap + kAttnChunk - 1) / kAttnChunk);
+  p.nchunks = (int)((cap + kPvChunk - 1) / kPvChunk);
   uint8_t* w = reinterpret_cast<uint8_t*>(a->workspace);
   p.s = reinterpret_cast<uint16_t*>(w + L.s);
   p.wstats = reinterpret_cast<float*>(w + L.wstats);
@@ -403,10 +436,11 @@ extern "C" int q6moe_kv_decode_attention(const q6moe_attn_args* a, void* stream)
   p.part = reinterpret_cast<float*>(w + L.part);
   p.out = a->out;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 chunks((unsigned)p.nchunks, (unsigned)p.kvh, (unsigned)a->batch);
+  const dim3 chunks((unsigned)((cap + kAttnChunk - 1) / kAttnChunk), (unsigned)p.kvh, (unsigned)a->batch);
+  const dim3 pv_chunks((unsigned)p.nchunks, (unsigned)p.kvh, (unsigned)a->batch);
   hipLaunchKernelGGL(attn_scores_kernel, chunks, dim3(256), 0, s, p);
   hipLaunchKernelGGL(attn_stats_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(64), 0, s, p);
-  hipLaunchKernelGGL(attn_pv_kernel, chunks, dim3(256), 0, s, p);
+  hipLaunchKernelGGL(attn_pv_kernel, pv_chunks, dim3(kPvThreads), 0, s, p);
   hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(8 * kAttnD), 0, s, p);
   return check_launch("decode_attention kernels");
 }

@@ -64,6 +64,7 @@ def _check(got, want):
     (2, 2, 8, 64, 8, [512, 300]),        # full and partial last chunk
     (3, 1, 3, 128, 3, [1, 129, 384]),    # one token; group of 3 heads; chunk edges
     (1, 4, 8, 256, 2, [257]),            # one token past the first chunk
+    (2, 2, 4, 64, 40, [2560, 2049]),     # two 2048-token P.V chunks, the second partial
 ])
 def test_decode_attention_matches_oracle(device, batch, kvh, r, page_size, pps, lengths):
     pools, scales, table, q = _case(100 + batch * pps, batch, kvh, r, pages=batch * pps + 3,
