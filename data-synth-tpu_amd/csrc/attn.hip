@@ -10,24 +10,23 @@
 //   prob   = exp(score - max) / sum exp(score - max)   (FP32, numerics.softmax)
 //   out    = RNE_bf16(sum_t RNE_bf16(prob) * v)        (FP32 accumulation)
 //
-// Four launches (the normalised probability is rounded before it weighs V,
+// Three launches (the normalised probability is rounded before it weighs V,
 // so the softmax statistics must be complete before the P.V pass):
 //   1. attn_scores_kernel: per (256-token chunk, KV head, sequence), the
 //      chunk's keys are dequantised into MFMA A operands (16 tokens x 32
 //      channels per v_mfma_f32_16x16x32_bf16) against the group's query
 //      heads as B operand; scores go to the workspace as BF16, and each
 //      wave's maximum m_w and sum l_w of exp(score - m_w) over its 64 tokens.
-//   2. attn_stats_kernel: per (sequence, query head), the maximum over the
-//      attended tokens, max = max_w m_w, and the sum of exp(score - max),
-//      sum_w l_w exp(m_w - max), in a fixed order.
-//   3. attn_pv_kernel: per 2048-token chunk (8 waves, four 64-token tiles
-//      each), the workgroup forms RNE_bf16(prob) once per (head, token) in
+//   2. attn_pv_kernel: per 2048-token chunk (8 waves, four 64-token tiles
+//      each), wave h first merges head h's statistics over the attended
+//      tokens, max = max_w m_w and sum = sum_w l_w exp(m_w - max) in a fixed
+//      order; the workgroup forms RNE_bf16(prob) once per (head, token) in
 //      LDS; each wave then runs P.V for its tiles, in turn, on MFMA with the
 //      dequantised values as A operand (row = 8 channels apart, so a lane
 //      dequantises the 8x8 code block it loaded straight into eight tiles'
 //      operands) and the probabilities as B; the chunk's partial sums go to
 //      the workspace.
-//   4. attn_combine_kernel: partial sums over chunks in a fixed order, RNE.
+//   3. attn_combine_kernel: partial sums over chunks in a fixed order, RNE.
 //
 // HBM-bound: the INT8 codes and scales of K and V are read once.
 #include "q6moe_api.h"
@@ -56,7 +55,6 @@ struct AttnParams {
   int pps, page, kvh, hq, r, cap, nchunks;  // nchunks: P.V chunks of kPvChunk tokens
   uint16_t* s;                       // [B, Hq, cap] BF16 scores
   float* wstats;                     // [B, Hq, cap / 64, 2]: per 64 tokens, max m_w and sum of exp(score - m_w)
-  float* stats;                      // [B, Hq, 2]: max, sum
   float* part;                       // [B, KVH, nchunks, kAttnR, D]
   uint16_t* out;                     // [B, Hq, D]
 };
@@ -155,7 +153,7 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnParams p) {
   // The wave's statistics of head col over its attended tokens: the maximum
   // over the lane's scores and the four K groups (lanes col + 16g), then the
   // sum of exp(score - max) (hardware exponential: the sum only normalises,
-  // and the merge below weighs it by an accurate exp) the same way.
+  // and the P.V kernel's merge weighs it by an accurate exp) the same way.
   float m = -__builtin_inff();
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb)
@@ -178,56 +176,26 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnParams p) {
   }
 }
 
-// Per (sequence, query head), one wave: max = max_w m_w and sum =
-// sum_w l_w exp(m_w - max) over the sequence's 64-token groups; lane i takes
-// groups i, i + 64, ... in order, then the 64 lanes are merged in a fixed xor
-// tree.
-__global__ void __launch_bounds__(64) attn_stats_kernel(AttnParams p) {
-  const int h = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const int nw = (attn_len(p, b) + kAttnWaveTok - 1) / kAttnWaveTok;
-  const float* ws = p.wstats + ((int64_t)b * p.hq + h) * (p.cap / kAttnWaveTok) * 2;
-  float m = -__builtin_inff();
-  for (int w = lane; w < nw; w += 64) m = fmaxf(m, ws[2 * w]);
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
-  float l = 0.f;
-  for (int w = lane; w < nw; w += 64) {
-    const f32x2 v = *reinterpret_cast<const f32x2*>(ws + 2 * w);
-    l += v[1] * expf(v[0] - m);
-  }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) l += __shfl_xor(l, off);
-  if (lane == 0) *reinterpret_cast<f32x2*>(p.stats + ((int64_t)b * p.hq + h) * 2) = f32x2{m, l};
-}
-
-__global__ void __launch_bounds__(kPvThreads) attn_pv_kernel(AttnParams p) {
+__global__ void __launch_bounds__(kPvThreads) __attribute__((amdgpu_waves_per_eu(4))) attn_pv_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t pr[kAttnR][kPvChunk];  // RNE_bf16(prob) [head][token]
   __shared__ float red[kPvWaves][kAttnR][kAttnD];                       // per-wave partial sums
   const int chunk = blockIdx.x, kh = blockIdx.y, b = blockIdx.z;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c0 = chunk * kPvChunk;
   const int r16 = lane & 15, kg = lane >> 4;
+  __shared__ f32x2 s_st[kAttnR];                                        // the heads' (max, sum)
   // The wave's page entries (tile i: tokens c0 + kPvThreads*i + 64*wave + [0, 64))
-  // and the heads' softmax statistics (scalar loads; the head index is clamped
-  // into the group's r, and what it stands in for is never used) are read
-  // together with the length.
+  // are read together with the length.
   int64_t pg[kPvTiles];
 #pragma unroll
   for (int i = 0; i < kPvTiles; ++i) pg[i] = attn_page(p, b, c0 + kPvThreads * i + 64 * wave);
-  float sm[kAttnR], sl[kAttnR];
-#pragma unroll
-  for (int h = 0; h < kAttnR; ++h) {
-    const int64_t hh = (int64_t)b * p.hq + kh * p.r + (h < p.r ? h : 0);
-    sm[h] = p.stats[hh * 2];
-    sl[h] = p.stats[hh * 2 + 1];
-  }
   const int n = attn_len(p, b);
   asm volatile("" ::: "memory");  // the loads above issue before the length is waited for
   if (c0 >= n) return;  // uniform over the workgroup
   const int nv = n - c0 < kPvChunk ? n - c0 : kPvChunk;
   // For the probability pass (thread t = tokens c0 + t + kPvThreads*i): the
-  // chunk's scores of every head, loaded before the V codes so that the pass
-  // waits for them only (token clamped into the sequence's length).
+  // chunk's scores of every head (token clamped into the sequence's length),
+  // loaded together with the statistics below.
   const int t = threadIdx.x;
   uint16_t sc[kPvTiles][kAttnR];
 #pragma unroll
@@ -237,6 +205,50 @@ __global__ void __launch_bounds__(kPvThreads) attn_pv_kernel(AttnParams p) {
 #pragma unroll
     for (int h = 0; h < kAttnR; ++h)
       sc[i][h] = p.s[((int64_t)b * p.hq + kh * p.r + (h < p.r ? h : 0)) * p.cap + tc];
+  }
+  // The softmax statistics of head h < r, merged by wave h from the scores
+  // kernel's per-64-token (m_w, l_w): lane i takes groups i, i + 64, ... in
+  // order (the first 8 in one batch of loads), max over them and a fixed xor
+  // tree, then sum of l_w exp(m_w - max) the same way; every workgroup of the
+  // head computes the same values.
+  float sm[kAttnR], sl[kAttnR];
+  {
+    const int nw = (n + kAttnWaveTok - 1) / kAttnWaveTok;
+    const f32x2* wsh = reinterpret_cast<const f32x2*>(p.wstats) +
+                       ((int64_t)b * p.hq + kh * p.r + (wave < p.r ? wave : 0)) * (p.cap / kAttnWaveTok);
+    f32x2 wl[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int w = lane + 64 * u;
+      wl[u] = wsh[w < nw ? w : nw - 1];
+    }
+    if (wave < p.r) {  // uniform over the wave
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (lane + 64 * u < nw) m = fmaxf(m, wl[u][0]);
+      for (int w = lane + 512; w < nw; w += 64) m = fmaxf(m, wsh[w][0]);
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+      float l = 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (lane + 64 * u < nw) l += wl[u][1] * expf(wl[u][0] - m);
+      for (int w = lane + 512; w < nw; w += 64) {
+        const f32x2 v = wsh[w];
+        l += v[1] * expf(v[0] - m);
+      }
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) l += __shfl_xor(l, off);
+      if (lane == 0) s_st[wave] = f32x2{m, l};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < kAttnR; ++h) {
+      const f32x2 v = s_st[h < p.r ? h : 0];
+      sm[h] = v[0];
+      sl[h] = v[1];
+    }
   }
   // V codes of a tile: lane (r16, kg) reads channels 8*r16 + [0, 8) of the
   // wave's tokens 32s + 8kg + j (s = 0, 1; j = 0..7), all in the wave's page
@@ -270,7 +282,7 @@ __global__ void __launch_bounds__(kPvThreads) attn_pv_kernel(AttnParams p) {
         sv[st][j] = ok ? sv[st][j] : 0.f;
       }
   };
-  load_tile(0);
+  load_tile(0);  // the V codes' loads overlap the probability pass
   // 1. RNE_bf16(prob) of every (head, token) of the chunk, once; heads from r
   //    on are 0 (MFMA columns 8-15 take zero operands below)
 #pragma unroll
@@ -364,7 +376,7 @@ __global__ void __launch_bounds__(8 * kAttnD) attn_combine_kernel(AttnParams p) 
 }
 
 struct AttnLayout {
-  size_t s, wstats, stats, part, total;
+  size_t s, wstats, part, total;
 };
 
 static size_t attn_align(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -374,8 +386,7 @@ static AttnLayout attn_layout(int64_t B, int64_t hq, int64_t kvh, int64_t cap) {
   const int64_t nchunks = (cap + kPvChunk - 1) / kPvChunk;
   L.s = 0;
   L.wstats = attn_align(L.s + (size_t)B * hq * cap * 2);
-  L.stats = attn_align(L.wstats + (size_t)B * hq * (cap / kAttnWaveTok) * 2 * 4);
-  L.part = attn_align(L.stats + (size_t)B * hq * 2 * 4);
+  L.part = attn_align(L.wstats + (size_t)B * hq * (cap / kAttnWaveTok) * 2 * 4);
   L.total = attn_align(L.part + (size_t)B * kvh * nchunks * kAttnR * kAttnD * 4);
   return L;
 }
@@ -432,14 +443,12 @@ extern "C" int q6moe_kv_decode_attention(const q6moe_attn_args* a, void* stream)
   uint8_t* w = reinterpret_cast<uint8_t*>(a->workspace);
   p.s = reinterpret_cast<uint16_t*>(w + L.s);
   p.wstats = reinterpret_cast<float*>(w + L.wstats);
-  p.stats = reinterpret_cast<float*>(w + L.stats);
   p.part = reinterpret_cast<float*>(w + L.part);
   p.out = a->out;
   hipStream_t s = (hipStream_t)stream;
   const dim3 chunks((unsigned)((cap + kAttnChunk - 1) / kAttnChunk), (unsigned)p.kvh, (unsigned)a->batch);
   const dim3 pv_chunks((unsigned)p.nchunks, (unsigned)p.kvh, (unsigned)a->batch);
   hipLaunchKernelGGL(attn_scores_kernel, chunks, dim3(256), 0, s, p);
-  hipLaunchKernelGGL(attn_stats_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(64), 0, s, p);
   hipLaunchKernelGGL(attn_pv_kernel, pv_chunks, dim3(kPvThreads), 0, s, p);
   hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)p.hq, (unsigned)a->batch), dim3(8 * kAttnD), 0, s, p);
   return check_launch("decode_attention kernels");
