@@ -205,12 +205,13 @@ __global__ void __launch_bounds__(kChunk)
 }
 
 // Scans over experts (lane e = expert e, whole waves of the workgroup; lanes
-// from E on carry nothing): active experts in ascending id (experts.py:74-76)
-// into ws.active, their first route positions (returned, and in ws.act_off),
+// from E on carry nothing): each expert's first route position (returned)
+// and, with ``publish``, the active experts in ascending id
+// (experts.py:74-76) into ws.active, their first positions into ws.act_off,
 // the prefill tiles of mtile routes, and the totals in ws.hdr (written by the
 // workgroup's last lane).
 __device__ __forceinline__ int route_scan(int e, int E, int total, int mtile, MoeWs ws,
-                                          int (*s_wt)[kMaxExperts / 64]) {
+                                          int (*s_wt)[kMaxExperts / 64], bool publish = true) {
   const int lane = e & 63, wv = e >> 6;
   const int act = total > 0, nt = (total + mtile - 1) / mtile;
   // inclusive scans of (active, routes, tiles) in expert order: within each
@@ -237,6 +238,7 @@ __device__ __forceinline__ int route_scan(int e, int E, int total, int mtile, Mo
     it += s_wt[2][w];
   }
   const int slot = ia - act, base = ic - total, t0 = it - nt;
+  if (!publish) return base;
   if (e < E) {
     if (act) {
       ws.active[slot] = e;
@@ -386,6 +388,50 @@ __global__ void __launch_bounds__(kChunk)
   __syncthreads();
   route_place(s_ids, s_r, s_tp, bits, s_pos, nb, K, b0, ws);
   for (int i = tid; i < nb * K; i += kChunk) ws.tok_pos[e0 + i] = s_tp[i];
+}
+
+// Routing, passes 2 and 3 in one launch for at most kFoldChunks chunks (one
+// workgroup per chunk of max(kChunk, E rounded up to whole waves) lanes):
+// every workgroup scans the chunks' counts itself (lane e = expert e: its
+// expert's total and the routes of the earlier chunks, integer sums), chunk
+// 0's workgroup writes the tables, and each places its chunk's routes as pass
+// 3 does. The counts come from the count launch before it.
+constexpr int kFoldChunks = 32;
+
+__global__ void __launch_bounds__(kMaxExperts)
+    moe_route_scan_scatter_kernel(const int32_t* __restrict__ ids, int B, int K, int E, int nchunks, int mtile,
+                                  MoeWs ws, const int* __restrict__ chunk_cnt) {
+  extern __shared__ int sm[];
+  int* s_ids = sm;                                                     // [kChunk * K]
+  float* s_r = reinterpret_cast<float*>(sm + kChunk * K);              // [kChunk * K]
+  int* s_tp = sm + 2 * kChunk * K;                                     // [kChunk * K]
+  uint32_t* bits = reinterpret_cast<uint32_t*>(sm + 3 * kChunk * K);   // [E][kChunkWords]
+  int* s_pos = sm + 3 * kChunk * K + E * kChunkWords;                  // [E]
+  __shared__ int s_wt[3][kMaxExperts / 64];
+  const int tid = threadIdx.x, n = (int)blockDim.x, c = blockIdx.x, b0 = c * kChunk;
+  const int nb = B - b0 < kChunk ? B - b0 : kChunk;
+  const int64_t e0 = (int64_t)b0 * K;
+  for (int i = tid; i < E * kChunkWords; i += n) bits[i] = 0u;
+  // the expert's count in every chunk, loaded in one batch with the chunk's
+  // entries (lanes past E read expert E - 1's and use none of it)
+  int v[kFoldChunks];
+  const int ec = tid < E ? tid : E - 1;
+#pragma unroll
+  for (int q = 0; q < kFoldChunks; ++q) v[q] = q < nchunks ? chunk_cnt[(int64_t)q * E + ec] : 0;
+  if (tid < kChunk)
+    stage_chunk2(s_ids, ids + e0, [](int x) { return x; }, s_r, ws.ent_r + e0, [](float x) { return x; }, nb * K);
+  int total = 0, off = 0;
+#pragma unroll
+  for (int q = 0; q < kFoldChunks; ++q) {
+    total += v[q];
+    off += q < c ? v[q] : 0;
+  }
+  if (tid >= E) total = off = 0;
+  const int base = route_scan(tid, E, total, mtile, ws, s_wt, c == 0);
+  if (tid < E) s_pos[tid] = base + off;
+  __syncthreads();
+  route_place(s_ids, s_r, s_tp, bits, s_pos, nb, K, b0, ws);
+  for (int i = tid; i < nb * K; i += n) ws.tok_pos[e0 + i] = s_tp[i];
 }
 
 // Routing of at most kChunk tokens in one launch: the three passes above in
@@ -1525,6 +1571,8 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
                                 (int)scatter_lds(32, kMaxExperts));
       (void)hipFuncSetAttribute((const void*)moe_route_small_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)(scatter_lds(32, kMaxExperts) + kMaxExperts * 4));
+      (void)hipFuncSetAttribute((const void*)moe_route_scan_scatter_kernel,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)scatter_lds(32, kMaxExperts));
     });
     const int nchunks = (int)cdiv(B, kChunk);
     int* chunk_cnt = reinterpret_cast<int*>(w + L.chunk_cnt);
@@ -1536,10 +1584,17 @@ static int moe_forward_impl(const q6moe_moe_args* a, void* workspace, size_t wor
     } else {
       hipLaunchKernelGGL(moe_route_count_kernel, dim3(nchunks), dim3(kChunk), (size_t)kChunk * K * 8, s, a->ids,
                          a->weights, (int)B, (int)K, (int)E, ws, chunk_cnt);
-      hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3((unsigned)cdiv(E, 64) * 64), 0, s, (int)E, nchunks,
-                         (int)kPrefillTile, ws, chunk_cnt);
-      hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nchunks), dim3(kChunk), scatter_lds(K, E), s, a->ids,
-                         (int)B, (int)K, (int)E, nchunks, ws, chunk_cnt);
+      if (nchunks <= kFoldChunks) {
+        // the scan folded into the scatter workgroups (up to 8192 tokens)
+        const unsigned lanes = (unsigned)std::max<int64_t>(kChunk, cdiv(E, 64) * 64);
+        hipLaunchKernelGGL(moe_route_scan_scatter_kernel, dim3(nchunks), dim3(lanes), scatter_lds(K, E), s, a->ids,
+                           (int)B, (int)K, (int)E, nchunks, (int)kPrefillTile, ws, chunk_cnt);
+      } else {
+        hipLaunchKernelGGL(moe_route_scan_kernel, dim3(1), dim3((unsigned)cdiv(E, 64) * 64), 0, s, (int)E, nchunks,
+                           (int)kPrefillTile, ws, chunk_cnt);
+        hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nchunks), dim3(kChunk), scatter_lds(K, E), s, a->ids,
+                           (int)B, (int)K, (int)E, nchunks, ws, chunk_cnt);
+      }
     }
     if ((rc = check_launch("moe routing kernels"))) return rc;
   }

@@ -157,8 +157,9 @@ def test_duplicate_routes_sum_and_zero_rows_are_exact_zero(device):
     (100, 32, 256),  # one launch, 2 lanes per token, top-k above 16
     (256, 8, 64),    # one launch, one lane per token
     (180, 20, 48),   # one launch, one lane per token, top-k above 16
-    (513, 8, 16),    # three passes over three chunks
-    (600, 24, 96),   # three passes, top-k above 16
+    (513, 8, 16),    # count, then scan and placement in one launch, three chunks
+    (600, 24, 96),   # the same, top-k above 16
+    (8448, 2, 16),   # 33 chunks: count, scan and placement in three launches
 ])
 def test_grouped_routing_edge_entries(device, tokens, top_k, experts):
     # The grouped family's routing in each of its branches, fed a token whose
