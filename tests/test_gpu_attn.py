@@ -65,6 +65,7 @@ def _check(got, want):
     (3, 1, 3, 128, 3, [1, 129, 384]),    # one token; group of 3 heads; chunk edges
     (1, 4, 8, 256, 2, [257]),            # one token past the first chunk
     (2, 2, 4, 64, 40, [2560, 2049]),     # two 2048-token P.V chunks, the second partial
+    (2, 1, 8, 256, 16, [2048, 4096]),    # lengths on P.V chunk boundaries, one and two whole chunks
 ])
 def test_decode_attention_matches_oracle(device, batch, kvh, r, page_size, pps, lengths):
     pools, scales, table, q = _case(100 + batch * pps, batch, kvh, r, pages=batch * pps + 3,
