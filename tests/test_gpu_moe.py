@@ -160,6 +160,8 @@ def test_duplicate_routes_sum_and_zero_rows_are_exact_zero(device):
     (513, 8, 16),    # count, then scan and placement in one launch, three chunks
     (600, 24, 96),   # the same, top-k above 16
     (8448, 2, 16),   # 33 chunks: count, scan and placement in three launches
+    (257, 4, 1024),  # two chunks, the second of one token; workgroups of 1024 lanes
+    (300, 2, 2),     # two experts: every token routes to both
 ])
 def test_grouped_routing_edge_entries(device, tokens, top_k, experts):
     # The grouped family's routing in each of its branches, fed a token whose
